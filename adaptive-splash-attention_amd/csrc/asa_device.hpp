@@ -1,0 +1,138 @@
+// Device-side building blocks shared by the gfx950 kernels of libadasplash.
+//
+// MFMA conventions (v_mfma_f32_16x16x32_bf16 and v_mfma_f32_16x16x4_f32):
+//   A operand: lane L supplies row (L % 16) of A, B operand: column (L % 16)
+//   of B; lane group g = L / 16 supplies a fixed set of k slots, the same set
+//   for A and B.  A product is therefore correct for any assignment of
+//   reduction indices to (g, slot) as long as A and B use the same one; the
+//   kernels exploit this to feed an accumulator straight back in as the next
+//   product's operand.
+//   D (accumulator, 4 floats per lane): element r of lane L is
+//   D[4 * (L / 16) + r][L % 16].
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace asa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16;
+
+constexpr int kWave = 64;
+constexpr int kBlock = 64;          // query rows per block == key columns per block
+constexpr float kEps = 1e-8f;       // reference EPS (adasplashattention.cu:21)
+constexpr float kSentinel = -1e6f;  // empty top-k slot score (adasplashattention.cu:170)
+
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float bf16_to_f32(u16 h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+// Round-to-nearest-even float -> bf16 bits (NaN stays NaN).
+__device__ __forceinline__ u16 f32_to_bf16(float f) {
+  __bf16 b = static_cast<__bf16>(f);
+  return __builtin_bit_cast(u16, b);
+}
+
+// ---------------------------------------------------------------------------
+// Element access for the two storage types.
+// ---------------------------------------------------------------------------
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static __device__ __forceinline__ float load(const float* p) { return *p; }
+  static __device__ __forceinline__ void store(float* p, float v) { *p = v; }
+};
+template <> struct Elem<u16> {
+  static __device__ __forceinline__ float load(const u16* p) { return bf16_to_f32(*p); }
+  static __device__ __forceinline__ void store(u16* p, float v) { *p = f32_to_bf16(v); }
+};
+
+// ---------------------------------------------------------------------------
+// Powers.  x^e for x > 0 with the exponent known at compile time by class:
+//   kE2 (alpha 1.5 weights), kE1, kE0, kE3, kE4 (alpha 1.25 weights),
+//   kEM1 (alpha 2 f'' terms), kEGen (anything else, passed at run time).
+// pow_exact rounds once to float (double product chain / double pow), the
+// convention the CPU oracle uses too, so the tau recurrence agrees bit-for-bit
+// when both see the same top-k values.  pow_fast is used per score in the
+// attention passes: identical to pow_exact for kE0/kE1/kE2, within an ulp for
+// kE3/kE4, exp2(e log2 x) in hardware for kEGen.
+// ---------------------------------------------------------------------------
+enum PowClass : int { kE0 = 0, kE1 = 1, kE2 = 2, kE3 = 3, kE4 = 4, kEM1 = 5, kEGen = 6 };
+
+__host__ __device__ inline int pow_class_of(float e) {
+  if (e == 0.0f) return kE0;
+  if (e == 1.0f) return kE1;
+  if (e == 2.0f) return kE2;
+  if (e == 3.0f) return kE3;
+  if (e == 4.0f) return kE4;
+  if (e == -1.0f) return kEM1;
+  return kEGen;
+}
+
+__device__ __forceinline__ float pow_exact(float x, float e) {
+  const double xd = static_cast<double>(x);
+  if (e == 2.0f) return static_cast<float>(xd * xd);
+  if (e == 1.0f) return x;
+  if (e == 0.0f) return 1.0f;
+  if (e == 3.0f) return static_cast<float>(xd * xd * xd);
+  if (e == 4.0f) { const double x2 = xd * xd; return static_cast<float>(x2 * x2); }
+  if (e == -1.0f) return static_cast<float>(1.0 / xd);
+  return static_cast<float>(pow(xd, static_cast<double>(e)));
+}
+
+template <int PC>
+__device__ __forceinline__ float pow_fast(float x, float e) {
+  if constexpr (PC == kE2) return x * x;
+  else if constexpr (PC == kE1) return x;
+  else if constexpr (PC == kE0) return 1.0f;
+  else if constexpr (PC == kE3) return static_cast<float>(static_cast<double>(x) * x * x);
+  else if constexpr (PC == kE4) { const double x2 = static_cast<double>(x) * x; return static_cast<float>(x2 * x2); }
+  else if constexpr (PC == kEM1) return static_cast<float>(1.0 / static_cast<double>(x));
+  else return __builtin_amdgcn_exp2f(e * __builtin_amdgcn_logf(x));
+}
+
+__device__ __forceinline__ bool finite(float x) { return __builtin_isfinite(x); }
+
+// Score clamp of the reference (adasplashattention.cu:195-197): NaN -> -10.
+__device__ __forceinline__ float clamp_score(float s) {
+  return fminf(fmaxf(s, -10.0f), 10.0f);
+}
+
+// ---------------------------------------------------------------------------
+// 64-bit selection keys: larger key == better entry under the order
+// (score descending, key index ascending).  High word: order-preserving map
+// of the float score (-0 folded onto +0 so that it ties with +0 as a float
+// comparison does); low word: ~index.  The empty slot (score -1e6, index -1)
+// has low word 0.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t ord_of(float s) {
+  const uint32_t u = __float_as_uint(s + 0.0f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float score_of_ord(uint32_t o) {
+  const uint32_t u = (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o;
+  return __uint_as_float(u);
+}
+__device__ __forceinline__ uint64_t make_key(float s, int idx) {
+  return (static_cast<uint64_t>(ord_of(s)) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(idx));
+}
+__device__ __forceinline__ float key_score(uint64_t k) { return score_of_ord(static_cast<uint32_t>(k >> 32)); }
+__device__ __forceinline__ int key_index(uint64_t k) { return static_cast<int>(~static_cast<uint32_t>(k)); }
+
+// Reductions across the four lane groups that share a column of a 16x16
+// accumulator (lanes L, L^16, L^32, L^48).
+__device__ __forceinline__ float sum_groups(float v) {
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+}  // namespace asa

@@ -1,0 +1,88 @@
+// Host-side launch interface between the C ABI (capi.cpp) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace asa {
+
+// Problem constants shared by every kernel.
+struct Dims {
+  int BH, NQ, NK, D, k, nQB, nKB;
+  float alpha;  // already clamped to [1.05, 3]
+  float scale;
+};
+
+struct SelectParams {
+  Dims d;
+  const void* q;          // MFMA path
+  const void* k;
+  const float* scores;    // scores path: [BH, NQ, NK]
+  const int32_t* q_idx;
+  const int32_t* k_idx;
+  float* taus;
+  uint8_t* mask;
+  int32_t* topk_idx;      // optional
+  float* topk_val;        // optional
+};
+
+struct CompactParams {
+  int BH, nQB, nKB;
+  const uint8_t* mask;
+  int32_t* q_ptr;
+  int32_t* q_list;
+  int32_t* k_ptr;
+  int32_t* k_list;
+};
+
+struct ForwardParams {
+  Dims d;
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* q_idx;
+  const int32_t* k_idx;
+  const float* taus;
+  const int32_t* q_ptr;
+  const int32_t* q_list;
+  void* out;
+  float* norms;
+};
+
+struct BackwardParams {
+  Dims d;
+  int mode;  // 0 entmax Jacobian, 1 reference kernel's gradient
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out;
+  const void* dout;
+  const int32_t* q_idx;
+  const int32_t* k_idx;
+  const float* taus;
+  const float* norms;
+  const int32_t* q_ptr;
+  const int32_t* q_list;
+  const int32_t* k_ptr;
+  const int32_t* k_list;
+  float* delta;  // workspace [BH, NQ]
+  void* dq;
+  void* dk;
+  void* dv;
+};
+
+// Each launcher returns the launch status; `name` receives the kernel's
+// name for the profiler.
+hipError_t launch_select(const SelectParams& p, bool bf16, bool from_scores, hipStream_t s);
+size_t select_lds_bytes(const Dims& d);
+hipError_t launch_compact(const CompactParams& p, hipStream_t s);
+hipError_t launch_forward(const ForwardParams& p, bool bf16, hipStream_t s);
+hipError_t launch_bwd_delta(const BackwardParams& p, bool bf16, hipStream_t s);
+hipError_t launch_bwd_dq(const BackwardParams& p, bool bf16, hipStream_t s);
+hipError_t launch_bwd_dkdv(const BackwardParams& p, bool bf16, hipStream_t s);
+
+// Kernel-timing hooks implemented in capi.cpp (no-ops unless profiling).
+void profile_begin(const char* name, hipStream_t s);
+void profile_end(hipStream_t s);
+
+}  // namespace asa

@@ -1,0 +1,156 @@
+// LDS tiles and the two MFMA tile products used by the attention passes.
+//
+// A "tile" is 64 rows x D columns of a [rows, D] tensor.  bf16 tiles are
+// staged row-major (stride D+8) and, when a product needs the tile as a
+// transposed operand, also column-major (stride 64+8).  fp32 tiles are
+// staged row-major only: the fp32 MFMA takes one element per lane and k
+// slot, which a row-major tile serves without conflicts.
+//
+//   rows_x_frag:  acc[f] (16 tile rows 16f.. x 16 lanes' columns)
+//                 = sum_d Tile[16f + i][d] * Bfrag[d][col]
+//   tile_t_x_acc: o[db] (16 head dims 16db.. x 16 columns)
+//                 += sum_r Tile[r][16db + i] * X[r][col]
+//                 where X is given in the accumulator layout of rows_x_frag
+//                 (the row index r plays the MFMA k role; lane group g holds
+//                 rows 16f + 4g + 0..3 of each block f).
+#pragma once
+
+#include "asa_device.hpp"
+
+namespace asa {
+
+template <typename T, int D> struct Tile;
+template <int D> struct Tile<u16, D> {
+  static constexpr int kRs = D + 8;       // row-major stride
+  static constexpr int kTs = kBlock + 8;  // transposed stride
+};
+template <int D> struct Tile<float, D> {
+  static constexpr int kRs = D + 4;
+};
+
+// B-operand fragment of one row per lane (lane column c16 <- `row`),
+// covering the whole head dimension.
+template <typename T, int D> struct RowFrag;
+template <int D> struct RowFrag<u16, D> {
+  bf16x8 v[D / 32];
+  __device__ void load(const u16* row, bool ok, int lane) {
+    const int g = lane >> 4;
+    for (int s = 0; s < D / 32; ++s)
+      v[s] = ok ? *reinterpret_cast<const bf16x8*>(row + 32 * s + 8 * g) : bf16x8{};
+  }
+};
+template <int D> struct RowFrag<float, D> {
+  f32x4 v[D / 16];
+  __device__ void load(const float* row, bool ok, int lane) {
+    const int g = lane >> 4;
+    for (int j = 0; j < D / 16; ++j)
+      v[j] = ok ? *reinterpret_cast<const f32x4*>(row + 16 * j + 4 * g) : f32x4{};
+  }
+};
+
+// Stage rows [row0, row0 + 64) of a [*, D] tensor (rows >= nrows read as 0)
+// with `nthr` threads; either of `rm` / `tr` may be null (bf16).
+template <int D>
+__device__ __forceinline__ void stage_tile(u16* rm, u16* tr, const u16* src, int row0, int nrows,
+                                           int t, int nthr) {
+  constexpr int kChunks = kBlock * D / 8;
+  for (int c = t; c < kChunks; c += nthr) {
+    const int r = c / (D / 8), col = (c % (D / 8)) * 8;
+    uint4 v = {0, 0, 0, 0};
+    if (row0 + r < nrows) v = *reinterpret_cast<const uint4*>(src + size_t(row0 + r) * D + col);
+    if (rm) *reinterpret_cast<uint4*>(rm + r * Tile<u16, D>::kRs + col) = v;
+    if (tr) {
+      const u16* e = reinterpret_cast<const u16*>(&v);
+      for (int i = 0; i < 8; ++i) tr[(col + i) * Tile<u16, D>::kTs + r] = e[i];
+    }
+  }
+}
+template <int D>
+__device__ __forceinline__ void stage_tile(float* rm, float*, const float* src, int row0,
+                                           int nrows, int t, int nthr) {
+  constexpr int kChunks = kBlock * D / 4;
+  for (int c = t; c < kChunks; c += nthr) {
+    const int r = c / (D / 4), col = (c % (D / 4)) * 4;
+    f32x4 v = {0, 0, 0, 0};
+    if (row0 + r < nrows) v = *reinterpret_cast<const f32x4*>(src + size_t(row0 + r) * D + col);
+    *reinterpret_cast<f32x4*>(rm + r * Tile<float, D>::kRs + col) = v;
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const u16* rm,
+                                            const RowFrag<u16, D>& b, int lane) {
+  const int g = lane >> 4, c = lane & 15;
+  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < D / 32; ++s)
+    for (int f = 0; f < 4; ++f) {
+      const bf16x8 a =
+          *reinterpret_cast<const bf16x8*>(rm + (16 * f + c) * Tile<u16, D>::kRs + 32 * s + 8 * g);
+      acc[f] = mfma(a, b.v[s], acc[f]);
+    }
+}
+template <int D>
+__device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const float* rm,
+                                            const RowFrag<float, D>& b, int lane) {
+  const int g = lane >> 4, c = lane & 15;
+  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < D / 16; ++j)
+    for (int f = 0; f < 4; ++f) {
+      const f32x4 a =
+          *reinterpret_cast<const f32x4*>(rm + (16 * f + c) * Tile<float, D>::kRs + 16 * j + 4 * g);
+      for (int r = 0; r < 4; ++r) acc[f] = mfma(a[r], b.v[j][r], acc[f]);
+    }
+}
+
+// bf16: `tr` is the transposed tile.  x is rounded to bf16.
+template <int D>
+__device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const u16* tr,
+                                             const f32x4 (&x)[4], int lane) {
+  const int g = lane >> 4, c = lane & 15;
+  for (int cc = 0; cc < 2; ++cc) {
+    bf16x8 b;
+    for (int r = 0; r < 4; ++r) {
+      b[r] = static_cast<__bf16>(x[2 * cc][r]);
+      b[4 + r] = static_cast<__bf16>(x[2 * cc + 1][r]);
+    }
+    for (int db = 0; db < D / 16; ++db) {
+      const u16* p = tr + (16 * db + c) * Tile<u16, D>::kTs + 32 * cc + 4 * g;
+      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
+      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16);
+      const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o[db] = mfma(a, b, o[db]);
+    }
+  }
+}
+// fp32: `rm` is the row-major tile.
+template <int D>
+__device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const float* rm,
+                                             const f32x4 (&x)[4], int lane) {
+  const int g = lane >> 4, c = lane & 15;
+  for (int f = 0; f < 4; ++f)
+    for (int r = 0; r < 4; ++r) {
+      const float* p = rm + (16 * f + 4 * g + r) * Tile<float, D>::kRs + c;
+      for (int db = 0; db < D / 16; ++db) o[db] = mfma(p[16 * db], x[f][r], o[db]);
+    }
+}
+
+// Exponent classes of the two per-score powers, chosen from alpha:
+//   p = u^(1/(alpha-1)) and w = u^((2-alpha)/(alpha-1)) = p^(2-alpha).
+enum AlphaClass : int { kA15 = 0, kA20 = 1, kA125 = 2, kAGen = 3 };
+template <int AC> struct AlphaPow;
+template <> struct AlphaPow<kA15> { static constexpr int P = kE2, W = kE1; };
+template <> struct AlphaPow<kA20> { static constexpr int P = kE1, W = kE0; };
+template <> struct AlphaPow<kA125> { static constexpr int P = kE4, W = kE3; };
+template <> struct AlphaPow<kAGen> { static constexpr int P = kEGen, W = kEGen; };
+
+__host__ __device__ inline int alpha_class_of(float alpha) {
+  const float am1 = alpha - 1.0f;
+  const float a = 1.0f / am1;
+  const float ew = (2.0f - alpha) / am1;
+  if (a == 2.0f && ew == 1.0f) return kA15;
+  if (a == 1.0f && ew == 0.0f) return kA20;
+  if (a == 4.0f && ew == 3.0f) return kA125;
+  return kAGen;
+}
+
+}  // namespace asa

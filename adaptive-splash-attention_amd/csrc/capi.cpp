@@ -1,0 +1,347 @@
+// C ABI of libadasplash (declared in include/adasplash.h).
+//
+// Host side of the reference's forward_splash / backward_splash
+// (adasplashattention.cu:537-700): argument validation, the kernel sequence
+// on the caller's stream, and error reporting.  Unlike the reference it
+// allocates nothing, never synchronises, and reports errors through status
+// codes plus a thread-local message instead of exceptions.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/adasplash.h"
+#include "asa_launch.hpp"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int ok() {
+  g_error.clear();
+  return ASA_OK;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ASA_OK;
+  return fail(ASA_ERR_DEVICE, "%s failed: %s", what, hipGetErrorString(e));
+}
+
+struct Shape {
+  int BH, NQ, NK, D, k, nQB, nKB;
+  bool bf16;
+  float alpha, scale;
+};
+
+int validate(const asa_problem* p, Shape* sh) {
+  if (!p) return fail(ASA_ERR_INVALID_ARGUMENT, "problem descriptor is NULL");
+  if (p->batch < 1 || p->heads < 1)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "batch (%d) and heads (%d) must be >= 1", p->batch,
+                p->heads);
+  if (p->nq < 1 || p->nk < 1)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "nq (%d) and nk (%d) must be >= 1", p->nq, p->nk);
+  if (p->head_dim > 128)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "Head dimension too large (%d > 128)", p->head_dim);
+  if (p->head_dim != 64 && p->head_dim != 128)
+    return fail(ASA_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", p->head_dim);
+  if (p->k_keep < 1 || p->k_keep > 128)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "k_keep %d out of range [1, 128]", p->k_keep);
+  if (p->block_m != 64 || p->block_n != 64)
+    return fail(ASA_ERR_UNSUPPORTED, "block_m x block_n = %d x %d not supported (64 x 64)",
+                p->block_m, p->block_n);
+  if (p->dtype != ASA_DTYPE_F32 && p->dtype != ASA_DTYPE_BF16)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "unknown dtype %d", p->dtype);
+  if (!std::isfinite(p->alpha)) return fail(ASA_ERR_INVALID_ARGUMENT, "alpha is not finite");
+  if (!std::isfinite(p->sm_scale)) return fail(ASA_ERR_INVALID_ARGUMENT, "sm_scale is not finite");
+  const long long bh = (long long)p->batch * p->heads;
+  const long long nqb = (p->nq + 63) / 64, nkb = (p->nk + 63) / 64;
+  if (bh > (1LL << 31) - 1 || nqb * nkb > (1LL << 31) - 1 ||
+      bh * (long long)p->nq > (1LL << 40) || bh * (long long)p->nk > (1LL << 40))
+    return fail(ASA_ERR_INVALID_ARGUMENT, "problem too large");
+  sh->BH = int(bh);
+  sh->NQ = p->nq;
+  sh->NK = p->nk;
+  sh->D = p->head_dim;
+  sh->k = p->k_keep;
+  sh->nQB = int(nqb);
+  sh->nKB = int(nkb);
+  sh->bf16 = p->dtype == ASA_DTYPE_BF16;
+  // alpha is clamped to [1.05, 3] as the reference does (adasplashattention.cu:547).
+  sh->alpha = std::fmax(1.05f, std::fmin(p->alpha, 3.0f));
+  sh->scale = p->sm_scale;
+  return ASA_OK;
+}
+
+asa::Dims dims_of(const Shape& s) {
+  return asa::Dims{s.BH, s.NQ, s.NK, s.D, s.k, s.nQB, s.nKB, s.alpha, s.scale};
+}
+
+void sizes_of(const Shape& s, asa_sizes* z) {
+  const size_t rows = size_t(s.BH) * s.NQ;
+  const size_t blocks = size_t(s.BH) * s.nQB * s.nKB;
+  z->taus = rows * sizeof(float);
+  z->norms = rows * sizeof(float);
+  z->mask = blocks;
+  z->q_ptr = size_t(s.BH) * (s.nQB + 1) * sizeof(int32_t);
+  z->q_list = blocks * sizeof(int32_t);
+  z->k_ptr = size_t(s.BH) * (s.nKB + 1) * sizeof(int32_t);
+  z->k_list = blocks * sizeof(int32_t);
+  z->topk_idx = rows * s.k * sizeof(int32_t);
+  z->topk_val = rows * s.k * sizeof(float);
+  z->workspace = 2 * rows * sizeof(float);
+}
+
+int check_state(const asa_state* st, bool need_norms) {
+  if (!st) return fail(ASA_ERR_INVALID_ARGUMENT, "state is NULL");
+  if (!st->taus || !st->mask || !st->q_ptr || !st->q_list || !st->k_ptr || !st->k_list ||
+      (need_norms && !st->norms))
+    return fail(ASA_ERR_INVALID_ARGUMENT, "a required state buffer is NULL");
+  if ((st->topk_idx == nullptr) != (st->topk_val == nullptr))
+    return fail(ASA_ERR_INVALID_ARGUMENT, "topk_idx and topk_val must be both set or both NULL");
+  return ASA_OK;
+}
+
+int check_select_lds(const Shape& s) {
+  int dev = 0, max_lds = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (int rc = check_hip(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock,
+                                               dev),
+                         "hipDeviceGetAttribute"))
+    return rc;
+  const size_t need = asa::select_lds_bytes(dims_of(s));
+  if (need > size_t(max_lds))
+    return fail(ASA_ERR_UNSUPPORTED, "k_keep %d needs %zu bytes of LDS per block, device has %d",
+                s.k, need, max_lds);
+  return ASA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel timing (asa_profile_*).
+// ---------------------------------------------------------------------------
+struct Rec {
+  const char* name;
+  hipEvent_t start, stop;
+};
+thread_local bool g_prof = false;
+thread_local std::vector<Rec> g_recs;
+
+int run_select(const Shape& sh, const void* q, const void* k, const float* scores,
+               const int32_t* q_idx, const int32_t* k_idx, const asa_state* st, hipStream_t s) {
+  asa::SelectParams sp{};
+  sp.d = dims_of(sh);
+  sp.q = q;
+  sp.k = k;
+  sp.scores = scores;
+  sp.q_idx = q_idx;
+  sp.k_idx = k_idx;
+  sp.taus = st->taus;
+  sp.mask = st->mask;
+  sp.topk_idx = st->topk_idx;
+  sp.topk_val = st->topk_val;
+  asa::profile_begin(scores ? "select_scores" : "select", s);
+  hipError_t e = asa::launch_select(sp, sh.bf16, scores != nullptr, s);
+  asa::profile_end(s);
+  if (int rc = check_hip(e, "select kernel launch")) return rc;
+
+  asa::CompactParams cp{sh.BH, sh.nQB, sh.nKB, st->mask, st->q_ptr, st->q_list, st->k_ptr,
+                        st->k_list};
+  asa::profile_begin("compact", s);
+  e = asa::launch_compact(cp, s);
+  asa::profile_end(s);
+  return check_hip(e, "compact kernel launch");
+}
+
+}  // namespace
+
+namespace asa {
+
+void profile_begin(const char* name, hipStream_t s) {
+  if (!g_prof) return;
+  Rec r{name, nullptr, nullptr};
+  if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return;
+  hipEventRecord(r.start, s);
+  g_recs.push_back(r);
+}
+
+void profile_end(hipStream_t s) {
+  if (!g_prof || g_recs.empty()) return;
+  hipEventRecord(g_recs.back().stop, s);
+}
+
+}  // namespace asa
+
+extern "C" {
+
+int asa_abi_version(void) { return ASA_ABI_VERSION; }
+
+const char* asa_last_error(void) { return g_error.c_str(); }
+
+int asa_query_sizes(const asa_problem* p, asa_sizes* out) {
+  Shape sh;
+  if (int rc = validate(p, &sh)) return rc;
+  if (!out) return fail(ASA_ERR_INVALID_ARGUMENT, "output pointer is NULL");
+  sizes_of(sh, out);
+  return ok();
+}
+
+int asa_forward(const asa_problem* p, const void* q, const void* k, const void* v,
+                const int32_t* q_idx, const int32_t* k_idx, void* out, const asa_state* st,
+                void* workspace, void* stream) {
+  Shape sh;
+  if (int rc = validate(p, &sh)) return rc;
+  if (!q || !k || !v || !q_idx || !k_idx || !out)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
+  if (int rc = check_state(st, true)) return rc;
+  (void)workspace;
+  if (int rc = check_select_lds(sh)) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  if (int rc = run_select(sh, q, k, nullptr, q_idx, k_idx, st, s)) return rc;
+
+  asa::ForwardParams fp{};
+  fp.d = dims_of(sh);
+  fp.q = q;
+  fp.k = k;
+  fp.v = v;
+  fp.q_idx = q_idx;
+  fp.k_idx = k_idx;
+  fp.taus = st->taus;
+  fp.q_ptr = st->q_ptr;
+  fp.q_list = st->q_list;
+  fp.out = out;
+  fp.norms = st->norms;
+  asa::profile_begin("forward", s);
+  hipError_t e = asa::launch_forward(fp, sh.bf16, s);
+  asa::profile_end(s);
+  if (int rc = check_hip(e, "forward kernel launch")) return rc;
+  return ok();
+}
+
+int asa_backward(const asa_problem* p, int32_t grad_mode, const void* q, const void* k,
+                 const void* v, const int32_t* q_idx, const int32_t* k_idx, const void* out,
+                 const void* dout, const asa_state* st, void* dq, void* dk, void* dv,
+                 void* workspace, void* stream) {
+  Shape sh;
+  if (int rc = validate(p, &sh)) return rc;
+  if (grad_mode != ASA_GRAD_ENTMAX && grad_mode != ASA_GRAD_REFERENCE)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "unknown grad_mode %d", grad_mode);
+  if (!q || !k || !v || !q_idx || !k_idx || !dout || !dq || !dk || !dv)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
+  if (grad_mode == ASA_GRAD_REFERENCE && !out)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "reference-gradient mode needs the forward output");
+  if (!workspace) return fail(ASA_ERR_INVALID_ARGUMENT, "workspace is NULL");
+  if (int rc = check_state(st, true)) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  asa::BackwardParams bp{};
+  bp.d = dims_of(sh);
+  bp.mode = grad_mode;
+  bp.q = q;
+  bp.k = k;
+  bp.v = v;
+  bp.out = out;
+  bp.dout = dout;
+  bp.q_idx = q_idx;
+  bp.k_idx = k_idx;
+  bp.taus = st->taus;
+  bp.norms = st->norms;
+  bp.q_ptr = st->q_ptr;
+  bp.q_list = st->q_list;
+  bp.k_ptr = st->k_ptr;
+  bp.k_list = st->k_list;
+  bp.delta = static_cast<float*>(workspace);
+  bp.dq = dq;
+  bp.dk = dk;
+  bp.dv = dv;
+
+  hipError_t e;
+  if (grad_mode == ASA_GRAD_REFERENCE) {
+    asa::profile_begin("bwd_delta", s);
+    e = asa::launch_bwd_delta(bp, sh.bf16, s);
+    asa::profile_end(s);
+    if (int rc = check_hip(e, "backward delta kernel launch")) return rc;
+  }
+  asa::profile_begin("bwd_dq", s);
+  e = asa::launch_bwd_dq(bp, sh.bf16, s);
+  asa::profile_end(s);
+  if (int rc = check_hip(e, "backward dQ kernel launch")) return rc;
+  asa::profile_begin("bwd_dkdv", s);
+  e = asa::launch_bwd_dkdv(bp, sh.bf16, s);
+  asa::profile_end(s);
+  if (int rc = check_hip(e, "backward dK/dV kernel launch")) return rc;
+  return ok();
+}
+
+int asa_select_from_scores(const asa_problem* p, const float* scores, const int32_t* q_idx,
+                           const int32_t* k_idx, const asa_state* st, void* workspace,
+                           void* stream) {
+  Shape sh;
+  if (int rc = validate(p, &sh)) return rc;
+  if (!scores || !q_idx || !k_idx)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
+  if (int rc = check_state(st, false)) return rc;
+  (void)workspace;
+  if (int rc = check_select_lds(sh)) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int rc = run_select(sh, nullptr, nullptr, scores, q_idx, k_idx, st, s)) return rc;
+  return ok();
+}
+
+int asa_profile_enable(int on) {
+  g_prof = on != 0;
+  return ok();
+}
+
+int asa_profile_read(int max, char (*names)[64], int* counts, double* total_ms) {
+  struct Acc {
+    const char* name;
+    int n;
+    double ms;
+  };
+  std::vector<Acc> acc;
+  for (const Rec& r : g_recs) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(r.stop) == hipSuccess) hipEventElapsedTime(&ms, r.start, r.stop);
+    hipEventDestroy(r.start);
+    hipEventDestroy(r.stop);
+    bool found = false;
+    for (Acc& a : acc)
+      if (std::strcmp(a.name, r.name) == 0) {
+        a.n += 1;
+        a.ms += ms;
+        found = true;
+        break;
+      }
+    if (!found) acc.push_back(Acc{r.name, 1, double(ms)});
+  }
+  g_recs.clear();
+  int n = 0;
+  for (const Acc& a : acc) {
+    if (n >= max) break;
+    if (names) {
+      std::strncpy(names[n], a.name, 63);
+      names[n][63] = '\0';
+    }
+    if (counts) counts[n] = a.n;
+    if (total_ms) total_ms[n] = a.ms;
+    ++n;
+  }
+  ok();
+  return n;
+}
+
+}  // extern "C"

@@ -1,0 +1,55 @@
+"""splash_attention: block-sparse alpha-entmax attention on AMD MI355X (gfx950).
+
+Drop-in for mvideet/Adaptive-Splash-Attention:
+
+* ``AdaptiveSplashAttention`` -- the module its README documents
+  (README.md:102-124).
+* ``forward`` / ``backward`` -- the two native entry points its extension
+  binds (source/adasplashattention.cu:702-705), same argument order:
+  ``forward(Q, K, V, Q_idx, K_idx, sm_scale, alpha) -> Out`` and
+  ``backward(Q, K, V, Q_idx, K_idx, sm_scale, alpha, dOut) -> [dQ, dK, dV]``,
+  with ``k_keep`` as an extra keyword (the reference fixes it at 8 when it
+  is compiled, :17-19).  ``backward`` recomputes the selection like the
+  reference does (:669-676) and returns the reference kernel's gradient.
+* ``splash_attention`` -- functional form with autograd.
+
+All compute runs in hand-written HIP kernels in ``lib/libadasplash.so``;
+there is no CPU or PyTorch fallback.
+"""
+from __future__ import annotations
+
+from . import ops
+from ._lib import ASAError
+from .function import SplashAttentionFunction, splash_attention
+from .module import AdaptiveSplashAttention
+
+__all__ = [
+    "AdaptiveSplashAttention",
+    "ASAError",
+    "SplashAttentionFunction",
+    "backward",
+    "forward",
+    "ops",
+    "splash_attention",
+]
+
+__version__ = "0.1.0"
+
+
+def forward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, k_keep: int = 8):
+    """Reference-compatible native forward (adasplashattention.cu:537-609)."""
+    Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
+    out, _ = ops.splash_forward(Q, K, V, qi, ki, ops.clamp_alpha(alpha), k_keep, sm_scale)
+    return out
+
+
+def backward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, dOut, k_keep: int = 8,
+             grad_mode: str = "reference"):
+    """Reference-compatible native backward (adasplashattention.cu:611-700):
+    reruns the selection, then returns [dQ, dK, dV]."""
+    Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
+    a = ops.clamp_alpha(alpha)
+    out, st = ops.splash_forward(Q, K, V, qi, ki, a, k_keep, sm_scale)
+    dQ, dK, dV = ops.splash_backward(Q, K, V, qi, ki, out, dOut, st, a, k_keep, sm_scale,
+                                     grad_mode)
+    return [dQ, dK, dV]

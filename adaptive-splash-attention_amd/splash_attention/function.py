@@ -1,0 +1,53 @@
+"""Autograd wiring and the functional form of splash attention.
+
+The reference exposes only separate native forward/backward calls and no
+autograd wrapper (adasplashattention.cu:702-705); its README promises an
+``AdaptiveSplashAttention`` module (README.md:102-124).  Here the forward
+saves its selection state (tau, row sums, block mask, CSR lists) so that the
+backward does not recompute it (the reference backward rebuilds the mask,
+adasplashattention.cu:669-676).
+"""
+from __future__ import annotations
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from . import ops
+
+
+class SplashAttentionFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode):
+        out, st = ops.splash_forward(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale)
+        ctx.params = (alpha, k_keep, sm_scale, grad_mode)
+        ctx.save_for_backward(Q, K, V, Q_idx, K_idx, out, *st.tensors())
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dout):
+        Q, K, V, Q_idx, K_idx, out, *state = ctx.saved_tensors
+        alpha, k_keep, sm_scale, grad_mode = ctx.params
+        st = ops.SplashState(*state)
+        dQ, dK, dV = ops.splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st, alpha, k_keep,
+                                         sm_scale, grad_mode)
+        return dQ, dK, dV, None, None, None, None, None, None
+
+
+def splash_attention(Q, K, V, Q_idx=None, K_idx=None, alpha: float = 1.5, k_keep: int = 8,
+                     sm_scale: float | None = None, grad_mode: str = "entmax") -> torch.Tensor:
+    """Block-sparse alpha-entmax attention, differentiable in Q, K and V.
+
+    Q: [B, H, NQ, d]; K, V: [B, H, NK, d]; float32 or bfloat16 on one GPU.
+    Q_idx: [B*H, NQ] and K_idx: [B*H, NK] integer positions (None: arange);
+    key j is visible to query i iff K_idx[j] <= Q_idx[i].
+    grad_mode "entmax" (default) uses the alpha-entmax Jacobian; "reference"
+    reproduces the reference kernel's gradient.
+    """
+    if grad_mode not in ops.GRAD_MODES:
+        raise ValueError(f"grad_mode must be one of {sorted(ops.GRAD_MODES)}")
+    Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
+    if sm_scale is None:
+        sm_scale = Q.size(-1) ** -0.5
+    return SplashAttentionFunction.apply(Q, K, V, qi, ki, float(alpha), int(k_keep),
+                                         float(sm_scale), grad_mode)

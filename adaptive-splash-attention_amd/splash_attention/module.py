@@ -1,0 +1,56 @@
+"""``AdaptiveSplashAttention``: the module the reference README documents
+(README.md:102-124), with the same constructor and call convention."""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .function import splash_attention
+
+
+class AdaptiveSplashAttention(nn.Module):
+    """Block-sparse alpha-entmax attention.
+
+    Args follow README.md:105-111 of the reference:
+      head_dim: last dimension of Q, K, V (64 or 128).
+      alpha: entmax parameter, clamped to [1.05, 3] as the reference does.
+      k_keep: top-k kept per query row (1..128).
+      adaptive_threshold: accepted for compatibility.  The reference
+        recomputes tau on every call and has no parameters; so does this
+        module (it has no state_dict entries).
+      sm_scale: score scale (default 1/sqrt(head_dim)).
+      grad_mode: "entmax" (alpha-entmax Jacobian, default) or "reference"
+        (the reference kernel's gradient).
+
+    forward(Q, K, V, Q_idx=None, K_idx=None): Q [B, H, NQ, d], K and V
+    [B, H, NK, d]; Q_idx [B*H, NQ], K_idx [B*H, NK] positions (default
+    arange, i.e. causal).  Returns [B, H, NQ, d] in the input dtype.
+    """
+
+    def __init__(self, head_dim: int = 64, alpha: float = 1.5, k_keep: int = 8,
+                 adaptive_threshold: bool = True, sm_scale: float | None = None,
+                 grad_mode: str = "entmax"):
+        super().__init__()
+        if head_dim not in (64, 128):
+            raise ValueError(f"head_dim {head_dim} not supported (64 or 128)")
+        if not 1 <= int(k_keep) <= 128:
+            raise ValueError(f"k_keep {k_keep} out of range [1, 128]")
+        if grad_mode not in ("entmax", "reference"):
+            raise ValueError("grad_mode must be 'entmax' or 'reference'")
+        self.head_dim = int(head_dim)
+        self.alpha = float(alpha)
+        self.k_keep = int(k_keep)
+        self.adaptive_threshold = bool(adaptive_threshold)
+        self.sm_scale = float(sm_scale) if sm_scale is not None else self.head_dim ** -0.5
+        self.grad_mode = grad_mode
+
+    def extra_repr(self) -> str:
+        return (f"head_dim={self.head_dim}, alpha={self.alpha}, k_keep={self.k_keep}, "
+                f"sm_scale={self.sm_scale}, grad_mode={self.grad_mode!r}")
+
+    def forward(self, Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
+                Q_idx: torch.Tensor | None = None, K_idx: torch.Tensor | None = None) -> torch.Tensor:
+        if Q.size(-1) != self.head_dim:
+            raise ValueError(f"Q head dim {Q.size(-1)} != head_dim {self.head_dim}")
+        return splash_attention(Q, K, V, Q_idx, K_idx, self.alpha, self.k_keep, self.sm_scale,
+                                self.grad_mode)

@@ -1,0 +1,231 @@
+"""Tensor-level entry points over the C ABI.
+
+Every function here validates its torch tensors the way the reference
+extension does (source/adasplashattention.cu:542-558), allocates the
+outputs and per-call state with torch, and launches on the current HIP
+stream of the input's device.  Nothing synchronises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+BLOCK_M = 64
+BLOCK_N = 64
+MAX_HEAD_DIM = 128
+MAX_K_KEEP = 128
+
+_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
+
+GRAD_MODES = {"entmax": _lib.GRAD_ENTMAX, "reference": _lib.GRAD_REFERENCE}
+
+
+@dataclass
+class SplashState:
+    """Selection state of one forward call (see asa_state in adasplash.h)."""
+    taus: torch.Tensor       # [BH, NQ] float32
+    norms: torch.Tensor      # [BH, NQ] float32, sum of p per row
+    mask: torch.Tensor       # [BH, nQB, nKB] uint8
+    q_ptr: torch.Tensor      # [BH, nQB+1] int32 (reference Qi_ptr)
+    q_list: torch.Tensor     # [BH, nQB*nKB] int32 (reference Qi_idx)
+    k_ptr: torch.Tensor      # [BH, nKB+1] int32
+    k_list: torch.Tensor     # [BH, nKB*nQB] int32
+    topk_idx: torch.Tensor | None = None  # [BH, NQ, k] int32
+    topk_val: torch.Tensor | None = None  # [BH, NQ, k] float32
+
+    def c_struct(self) -> _lib.State:
+        def ptr(t):
+            return None if t is None else t.data_ptr()
+        return _lib.State(ptr(self.taus), ptr(self.norms), ptr(self.mask), ptr(self.q_ptr),
+                          ptr(self.q_list), ptr(self.k_ptr), ptr(self.k_list),
+                          ptr(self.topk_idx), ptr(self.topk_val))
+
+    def tensors(self) -> tuple:
+        return (self.taus, self.norms, self.mask, self.q_ptr, self.q_list, self.k_ptr,
+                self.k_list)
+
+
+def clamp_alpha(alpha: float) -> float:
+    """alpha as the kernels use it (adasplashattention.cu:547)."""
+    return max(1.05, min(float(alpha), 3.0))
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _index(idx, BH: int, N: int, B: int, H: int, device, name: str) -> torch.Tensor:
+    """Position indices as int32 [BH, N] on `device` (reference: Q_idx/K_idx [B*H, N])."""
+    if idx is None:
+        return torch.arange(N, device=device, dtype=torch.int32).unsqueeze(0).expand(BH, N).contiguous()
+    if not isinstance(idx, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if idx.dtype.is_floating_point or idx.dtype == torch.bool:
+        raise TypeError(f"{name} must be an integer tensor, got {idx.dtype}")
+    if idx.dim() == 1 and idx.shape[0] == N:
+        idx = idx.unsqueeze(0).expand(BH, N)
+    elif idx.dim() == 3 and tuple(idx.shape) == (B, H, N):
+        idx = idx.reshape(BH, N)
+    if tuple(idx.shape) != (BH, N):
+        raise ValueError(f"{name} must have shape [B*H, N] = [{BH}, {N}], got {tuple(idx.shape)}")
+    if idx.dtype != torch.int32:
+        if idx.numel() and (int(idx.min()) < -(2 ** 31) or int(idx.max()) >= 2 ** 31):
+            raise ValueError(f"{name} values do not fit int32")
+        idx = idx.to(torch.int32)
+    if idx.device != device:
+        raise RuntimeError("All tensors must be on same device")
+    return idx.contiguous()
+
+
+def check_inputs(Q, K, V, Q_idx=None, K_idx=None):
+    """Validate and normalise (Q, K, V, Q_idx, K_idx); returns contiguous tensors."""
+    for name, t in (("Q", Q), ("K", K), ("V", V)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a tensor")
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be 4-D [B, H, N, d], got shape {tuple(t.shape)}")
+    if Q.size(3) > MAX_HEAD_DIM:
+        raise ValueError("Head dimension too large; increase D_MAX")
+    if not Q.is_cuda:
+        raise RuntimeError("Tensors must be on CUDA device")
+    if K.device != Q.device or V.device != Q.device:
+        raise RuntimeError("All tensors must be on same device")
+    if Q.dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {Q.dtype}; use torch.float32 or torch.bfloat16")
+    if K.dtype != Q.dtype or V.dtype != Q.dtype:
+        raise TypeError("Q, K and V must have the same dtype")
+    B, H, NQ, d = Q.shape
+    if K.shape[0] != B or K.shape[1] != H or K.shape[3] != d:
+        raise ValueError(f"K shape {tuple(K.shape)} does not match Q shape {tuple(Q.shape)}")
+    if V.shape != K.shape:
+        raise ValueError(f"V shape {tuple(V.shape)} must equal K shape {tuple(K.shape)}")
+    if d not in (64, 128):
+        raise ValueError(f"head dimension {d} not supported (64 or 128)")
+    NK = K.shape[2]
+    if NQ < 1 or NK < 1 or B < 1 or H < 1:
+        raise ValueError("empty attention problem")
+    BH = B * H
+    qi = _index(Q_idx, BH, NQ, B, H, Q.device, "Q_idx")
+    ki = _index(K_idx, BH, NK, B, H, Q.device, "K_idx")
+    return _aligned(Q), _aligned(K), _aligned(V), qi, ki
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous with a 16-byte aligned base (the kernels load 16-byte vectors)."""
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def make_problem(B, H, NQ, NK, d, dtype, alpha, k_keep, sm_scale) -> _lib.Problem:
+    if not (1 <= int(k_keep) <= MAX_K_KEEP):
+        raise ValueError(f"k_keep {k_keep} out of range [1, {MAX_K_KEEP}]")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    return _lib.Problem(B, H, NQ, NK, d, int(k_keep), BLOCK_M, BLOCK_N, float(alpha),
+                        float(sm_scale), _DTYPES[dtype] if isinstance(dtype, torch.dtype) else dtype)
+
+
+def alloc_state(p: _lib.Problem, device, with_topk: bool = False) -> SplashState:
+    BH = p.batch * p.heads
+    nQB = -(-p.nq // BLOCK_M)
+    nKB = -(-p.nk // BLOCK_N)
+    i32 = dict(device=device, dtype=torch.int32)
+    f32 = dict(device=device, dtype=torch.float32)
+    st = SplashState(
+        taus=torch.empty((BH, p.nq), **f32),
+        norms=torch.empty((BH, p.nq), **f32),
+        mask=torch.empty((BH, nQB, nKB), device=device, dtype=torch.uint8),
+        q_ptr=torch.empty((BH, nQB + 1), **i32),
+        q_list=torch.empty((BH, nQB * nKB), **i32),
+        k_ptr=torch.empty((BH, nKB + 1), **i32),
+        k_list=torch.empty((BH, nKB * nQB), **i32),
+    )
+    if with_topk:
+        st.topk_idx = torch.empty((BH, p.nq, p.k_keep), **i32)
+        st.topk_val = torch.empty((BH, p.nq, p.k_keep), **f32)
+    return st
+
+
+def splash_forward(Q, K, V, Q_idx, K_idx, alpha: float, k_keep: int, sm_scale=None,
+                   with_topk: bool = False):
+    """Forward pass; returns (out, SplashState).  Inputs as check_inputs() returns them."""
+    lib = _lib.load()
+    B, H, NQ, d = Q.shape
+    p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale)
+    st = alloc_state(p, Q.device, with_topk)
+    out = torch.empty_like(Q)
+    cst = st.c_struct()
+    with torch.cuda.device(Q.device):
+        rc = lib.asa_forward(ctypes.byref(p), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
+                             Q_idx.data_ptr(), K_idx.data_ptr(), out.data_ptr(),
+                             ctypes.byref(cst), None, _stream(Q.device))
+    _lib.check(rc)
+    return out, st
+
+
+def splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st: SplashState, alpha: float,
+                    k_keep: int, sm_scale=None, grad_mode: str = "entmax"):
+    """Gradients (dQ, dK, dV) from a forward's state."""
+    lib = _lib.load()
+    if grad_mode not in GRAD_MODES:
+        raise ValueError(f"grad_mode must be one of {sorted(GRAD_MODES)}")
+    B, H, NQ, d = Q.shape
+    p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale)
+    if dout.shape != Q.shape:
+        raise ValueError(f"dOut shape {tuple(dout.shape)} must equal Q shape {tuple(Q.shape)}")
+    dout = _aligned(dout.to(Q.dtype))
+    z = _lib.query_sizes(p)
+    ws = torch.empty(z.workspace // 4, device=Q.device, dtype=torch.float32)
+    dQ = torch.empty_like(Q)
+    dK = torch.empty_like(K)
+    dV = torch.empty_like(V)
+    cst = st.c_struct()
+    with torch.cuda.device(Q.device):
+        rc = lib.asa_backward(ctypes.byref(p), GRAD_MODES[grad_mode], Q.data_ptr(), K.data_ptr(),
+                              V.data_ptr(), Q_idx.data_ptr(), K_idx.data_ptr(),
+                              None if out is None else out.data_ptr(), dout.data_ptr(),
+                              ctypes.byref(cst), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(),
+                              ws.data_ptr(), _stream(Q.device))
+    _lib.check(rc)
+    return dQ, dK, dV
+
+
+def select_from_scores(scores, Q_idx, K_idx, alpha: float, k_keep: int, batch: int = 1,
+                       heads: int | None = None) -> SplashState:
+    """Top-k, tau, block mask and CSR lists from given fp32 scores [BH, NQ, NK]
+    (no reference counterpart: exposes the reference's selection stage,
+    adasplashattention.cu:199-216, for checks on identical scores)."""
+    lib = _lib.load()
+    if scores.dim() == 4:
+        batch, heads = scores.shape[0], scores.shape[1]
+        scores = scores.reshape(-1, scores.shape[2], scores.shape[3])
+    if scores.dim() != 3:
+        raise ValueError("scores must be [BH, NQ, NK] or [B, H, NQ, NK]")
+    if scores.dtype != torch.float32:
+        raise TypeError("scores must be float32")
+    if not scores.is_cuda:
+        raise RuntimeError("Tensors must be on CUDA device")
+    BH, NQ, NK = scores.shape
+    if heads is None:
+        heads = BH // batch
+    if batch * heads != BH:
+        raise ValueError("batch * heads must equal scores.shape[0]")
+    qi = _index(Q_idx, BH, NQ, batch, heads, scores.device, "Q_idx")
+    ki = _index(K_idx, BH, NK, batch, heads, scores.device, "K_idx")
+    p = make_problem(batch, heads, NQ, NK, 64, torch.float32, alpha, k_keep, 1.0)
+    st = alloc_state(p, scores.device, with_topk=True)
+    scores = scores.contiguous()
+    cst = st.c_struct()
+    with torch.cuda.device(scores.device):
+        rc = lib.asa_select_from_scores(ctypes.byref(p), scores.data_ptr(), qi.data_ptr(),
+                                        ki.data_ptr(), ctypes.byref(cst), None,
+                                        _stream(scores.device))
+    _lib.check(rc)
+    return st

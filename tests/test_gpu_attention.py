@@ -1,0 +1,72 @@
+"""Forward and backward on the GPU vs the CPU oracle on identical seeded inputs.
+
+Tolerances (max |gpu - oracle| / max |oracle| per tensor): 1e-5 for fp32,
+2e-2 for bf16.  Selection state (mask, CSR) must match exactly; tau must
+match to 1e-5 relative (scores differ in the last bits between the MFMA
+dot products and the oracle's double-precision ones).
+Reference: adasplashattention.cu:150-700.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests._util import assert_close, causal_idx, make_inputs, np32
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+
+
+def _gpu(dev, Q, K, V, dO, qidx, kidx, alpha, k, scale, mode):
+    import splash_attention as sa
+
+    q, kk, v = (t.to(dev) for t in (Q, K, V))
+    qi, ki = qidx.to(dev), kidx.to(dev)
+    q, kk, v, qi, ki = sa.ops.check_inputs(q, kk, v, qi, ki)
+    out, st = sa.ops.splash_forward(q, kk, v, qi, ki, alpha, k, scale, with_topk=True)
+    grads = sa.ops.splash_backward(q, kk, v, qi, ki, out, dO.to(dev), st, alpha, k, scale, mode)
+    torch.cuda.synchronize()
+    return out, st, grads
+
+
+def _check(name, dtype, out, st, grads, fw, ograds, check_state=True):
+    tol = TOL[dtype]
+    if check_state:
+        np.testing.assert_array_equal(st.mask.cpu().numpy(), fw.mask, err_msg=f"{name}: mask")
+        np.testing.assert_array_equal(st.q_list.cpu().numpy(), fw.csr.q_list)
+        np.testing.assert_array_equal(st.k_list.cpu().numpy(), fw.csr.k_list)
+        assert_close(f"{name}: taus", st.taus.cpu().numpy(), fw.taus, 1e-5)
+    e_out = assert_close(f"{name}: out", np32(out), fw.out, tol)
+    errs = {"out": e_out}
+    for gname, g, w in zip(("dQ", "dK", "dV"), grads, ograds):
+        errs[gname] = assert_close(f"{name}: {gname}", np32(g), w, tol)
+    print(f"  {name}: " + ", ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
+
+
+CASES = [
+    # name, B, H, NQ, NK, d, alpha, k, scale, dtype
+    ("c1_fp32", 1, 2, 256, 256, 64, 1.5, 8, 0.125, torch.float32),
+    ("c1_fp32_k32", 1, 2, 256, 256, 64, 1.5, 32, 0.125, torch.float32),
+    ("fp32_d128_sparsemax", 1, 2, 192, 192, 128, 2.0, 16, 128 ** -0.5, torch.float32),
+    ("bf16_small", 1, 2, 256, 256, 64, 1.5, 32, 0.125, torch.bfloat16),
+    ("bf16_d128_a125", 1, 2, 256, 256, 128, 1.25, 64, 128 ** -0.5, torch.bfloat16),
+    ("fp32_ragged", 2, 1, 100, 150, 64, 1.5, 8, 0.125, torch.float32),
+    ("fp32_alpha_general", 1, 1, 128, 128, 64, 1.7, 8, 0.125, torch.float32),
+]
+
+
+@pytest.mark.parametrize("mode", ["entmax", "reference"])
+@pytest.mark.parametrize("name,B,H,NQ,NK,d,alpha,k,scale,dtype", CASES, ids=[c[0] for c in CASES])
+def test_attention_parity(dev, name, B, H, NQ, NK, d, alpha, k, scale, dtype, mode):
+    print(f"[attn] {name} mode={mode} B={B} H={H} NQ={NQ} NK={NK} d={d} a={alpha} k={k} {dtype}",
+          flush=True)
+    Q, K, V, dO = make_inputs(B, H, NQ, NK, d, seed=0, dtype=dtype)
+    BH = B * H
+    qidx = causal_idx(BH, NQ) + (NK - NQ if NK > NQ else 0)
+    kidx = causal_idx(BH, NK)
+    out, st, grads = _gpu(dev, Q, K, V, dO, qidx, kidx, alpha, k, scale, mode)
+    m = orc.GRAD_ENTMAX if mode == "entmax" else orc.GRAD_REFERENCE
+    fw, og = orc.attention(np32(Q), np32(K), np32(V), qidx.numpy(), kidx.numpy(), np32(dO), alpha,
+                           scale, k, mode=m)
+    _check(f"{name}/{mode}", dtype, out, st, grads, fw, og)
