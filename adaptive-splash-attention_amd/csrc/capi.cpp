@@ -7,10 +7,12 @@
 // codes plus a thread-local message instead of exceptions.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -130,14 +132,19 @@ int check_select_lds(const Shape& s) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel timing (asa_profile_*).
+// Kernel timing (asa_profile_*).  Process-wide: a backward pass may run on
+// another thread than the one that enabled profiling (e.g. an autograd
+// worker).
 // ---------------------------------------------------------------------------
 struct Rec {
   const char* name;
   hipEvent_t start, stop;
+  hipStream_t stream;
 };
-thread_local bool g_prof = false;
-thread_local std::vector<Rec> g_recs;
+std::atomic<bool> g_prof{false};
+std::mutex g_prof_mu;
+std::vector<Rec> g_recs;
+thread_local int g_open = -1;  // index of this thread's launch being timed
 
 int run_select(const Shape& sh, const void* q, const void* k, const float* scores,
                const int32_t* q_idx, const int32_t* k_idx, const asa_state* st, hipStream_t s) {
@@ -170,16 +177,33 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
 namespace asa {
 
 void profile_begin(const char* name, hipStream_t s) {
-  if (!g_prof) return;
-  Rec r{name, nullptr, nullptr};
-  if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return;
+  g_open = -1;
+  if (!g_prof.load(std::memory_order_relaxed)) return;
+  Rec r{name, nullptr, nullptr, s};
+  if (hipEventCreate(&r.start) != hipSuccess) return;
+  if (hipEventCreate(&r.stop) != hipSuccess) {
+    hipEventDestroy(r.start);
+    return;
+  }
   hipEventRecord(r.start, s);
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_open = int(g_recs.size());
   g_recs.push_back(r);
 }
 
 void profile_end(hipStream_t s) {
-  if (!g_prof || g_recs.empty()) return;
-  hipEventRecord(g_recs.back().stop, s);
+  if (g_open < 0) return;
+  hipEvent_t stop;
+  {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    if (g_open >= int(g_recs.size())) {
+      g_open = -1;
+      return;
+    }
+    stop = g_recs[g_open].stop;
+  }
+  hipEventRecord(stop, s);
+  g_open = -1;
 }
 
 }  // namespace asa
@@ -313,7 +337,12 @@ int asa_profile_read(int max, char (*names)[64], int* counts, double* total_ms) 
     double ms;
   };
   std::vector<Acc> acc;
-  for (const Rec& r : g_recs) {
+  std::vector<Rec> recs;
+  {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    recs.swap(g_recs);
+  }
+  for (const Rec& r : recs) {
     float ms = 0.0f;
     if (hipEventSynchronize(r.stop) == hipSuccess) hipEventElapsedTime(&ms, r.start, r.stop);
     hipEventDestroy(r.start);
@@ -328,7 +357,6 @@ int asa_profile_read(int max, char (*names)[64], int* counts, double* total_ms) 
       }
     if (!found) acc.push_back(Acc{r.name, 1, double(ms)});
   }
-  g_recs.clear();
   int n = 0;
   for (const Acc& a : acc) {
     if (n >= max) break;

@@ -1,0 +1,254 @@
+#!/usr/bin/env python3
+"""Headline benchmark: block-sparse alpha-entmax attention fwd+bwd on one MI355X.
+
+Workload: B=4, H=16, N=4096, d=64, bf16,
+alpha=1.5, k_keep=32, sm_scale=0.125, causal (Q_idx = K_idx = arange),
+64x64 blocks, Q/K/V and the upstream gradient ~ N(0,1) (synthetic, seeded).
+
+One step = forward (score pass, CSR compaction, block-sparse forward) plus
+backward (dQ, dK/dV, entmax-Jacobian gradient) through the autograd API,
+inputs resident in HBM.  value = effective TFLOP/s with the FlashAttention
+convention for dense causal fwd+bwd, 3.5 * 4 * BH * d * N^2 / 2 = 481.0 GFLOP
+per step.
+
+Per-kernel durations come from HIP events the library records around each
+launch on the launch stream (asa_profile_*) during the timed steps; the
+roofline of each kernel uses its algorithmic FLOPs / bytes per launch.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "adaptive-splash-attention_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "fwd+bwd ms & eff. TFLOP/s at B4 H16 N4096 d64 bf16; % MFMA/HBM roofline"
+WORK = dict(B=4, H=16, N=4096, d=64, alpha=1.5, k_keep=32, sm_scale=0.125)
+PEAK_MFMA_BF16 = 2.5e15  # dense bf16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12        # HBM3E, bytes/s
+ELEM = 2                 # bf16 bytes
+
+
+def effective_flops(B, H, N, d):
+    return 3.5 * 4 * B * H * d * N * N / 2
+
+
+def kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep):
+    """Algorithmic FLOPs and HBM bytes per launch of every kernel."""
+    BH = B * H
+    rows = BH * N
+    vis = BH * N * (N + 1) // 2          # visible (query, key) pairs, causal
+    tile = 64 * d * ELEM                 # one 64-row tile of Q, K, V or dO
+    csr = 4 * BH * (2 * nQB * nKB + nQB + nKB + 2)
+    vis_blocks = BH * nQB * (nQB + 1) // 2
+    return {
+        "select": dict(bound="mfma", flops=2.0 * d * vis,
+                       bytes=rows * d * ELEM + vis_blocks * tile + rows * 4 + BH * nQB * nKB),
+        "compact": dict(bound="hbm", flops=0.0, bytes=2 * BH * nQB * nKB + csr),
+        "forward": dict(bound="hbm", flops=4.0 * 64 * 64 * d * nnzb,
+                        bytes=nnzb * 2 * tile + 2 * rows * d * ELEM + 2 * rows * 4
+                        + 4 * BH * (nQB + 1 + nnzb // BH)),
+        "bwd_dq": dict(bound="hbm", flops=8.0 * 64 * 64 * d * nnzb,
+                       bytes=nnzb * 2 * tile + 3 * rows * d * ELEM + 4 * rows * 4),
+        "bwd_dkdv": dict(bound="hbm", flops=8.0 * 64 * 64 * d * nnzb,
+                         bytes=nnzb * 2 * tile + 4 * rows * d * ELEM + nnzb * 64 * 4 * 5),
+    }
+
+
+def roofline_of(model, ms):
+    t = ms / 1e3
+    mf = model["flops"] / t / PEAK_MFMA_BF16 if model["flops"] else 0.0
+    hb = model["bytes"] / t / PEAK_HBM
+    if model["bound"] == "mfma":
+        ach, peak, unit = model["flops"] / t / 1e12, PEAK_MFMA_BF16 / 1e12, "TFLOP/s"
+    else:
+        ach, peak, unit = model["bytes"] / t / 1e9, PEAK_HBM / 1e9, "GB/s"
+    return {"bound": model["bound"], "achieved": round(ach, 3), "peak": peak, "unit": unit,
+            "frac": round(ach / peak, 4), "traffic": None, "avg_ms": round(ms, 5),
+            "mfma_frac": round(mf, 4), "hbm_frac_algorithmic": round(hb, 4),
+            "alg_flops": model["flops"], "alg_bytes": model["bytes"]}
+
+
+def dense_gpu_baseline(Q, K, V, dO, alpha, scale, iters=40):
+    """Dense exact alpha-entmax attention fwd+bwd in PyTorch on the GPU (fp32
+    math, materialised [BH, N, N] scores, tau by bisection, exact entmax
+    Jacobian); returns ms per fwd+bwd."""
+    import torch
+
+    def run():
+        q, k, v, go = (t.float() for t in (Q, K, V, dO))
+        kt = k.transpose(-1, -2).contiguous()
+        S = torch.matmul(q, kt).mul_(scale).clamp_(-10.0, 10.0)
+        N = S.shape[-1]
+        causal = torch.ones(N, N, device=S.device, dtype=torch.bool).tril_()
+        z = S.mul_(alpha - 1.0).masked_fill_(~causal, -float("inf"))
+        a = 1.0 / (alpha - 1.0)
+        hi = z.amax(-1, keepdim=True)
+        lo = hi - 1.0
+        for _ in range(iters):
+            mid = 0.5 * (lo + hi)
+            f = (z - mid).clamp_(min=0).pow_(a).sum(-1, keepdim=True) - 1.0
+            pos = f > 0
+            lo = torch.where(pos, mid, lo)
+            hi = torch.where(pos, hi, mid)
+        P = (z - 0.5 * (lo + hi)).clamp_(min=0).pow_(a)
+        P = P / P.sum(-1, keepdim=True)
+        O = torch.matmul(P, v)
+        dP = torch.matmul(go, v.transpose(-1, -2).contiguous())
+        g = torch.where(P > 0, P.pow(2.0 - alpha), torch.zeros_like(P))
+        shift = (g * dP).sum(-1, keepdim=True) / g.sum(-1, keepdim=True)
+        dS = g * (dP - shift)
+        dQ = torch.matmul(dS, k) * scale
+        dK = torch.matmul(dS.transpose(-1, -2).contiguous(), q) * scale
+        dV = torch.matmul(P.transpose(-1, -2).contiguous(), go)
+        return O, dQ, dK, dV
+
+    run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3
+
+
+def cpu_baseline(heads=16, trials=3):
+    """The CPU oracle (C restatement of the reference algorithm, OpenMP over
+    rows / heads) on a sample of the headline workload: `heads` of its 64
+    (batch, head) slices, full N=4096, bf16-rounded inputs in fp32."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as orc
+
+    N, d = WORK["N"], WORK["d"]
+    g = torch.Generator().manual_seed(0)
+    Q, K, V, dO = (torch.randn(heads, N, d, generator=g).to(torch.bfloat16).float().numpy()
+                   for _ in range(4))
+    idx = np.broadcast_to(np.arange(N, dtype=np.int32), (heads, N)).copy()
+    times = []
+    for _ in range(trials):
+        t0 = time.perf_counter()
+        orc.attention(Q, K, V, idx, idx, dO, WORK["alpha"], WORK["sm_scale"], WORK["k_keep"])
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    flops = effective_flops(1, heads, N, d)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(flops / t / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle fwd+bwd (entmax grad) on {heads} of 64 (batch,head) slices, "
+                      f"N={N} d={d} k={WORK['k_keep']}, median of {trials}: {t:.2f} s",
+            "ms_per_step_scaled": round(t * 1e3 * 64 / heads, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--grad-mode", default="entmax", choices=["entmax", "reference"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-dense-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (no collectives or sharding); "
+              "use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import splash_attention as sa
+    from splash_attention import _lib
+
+    dev = torch.device("cuda:0")
+    B, H, N, d = WORK["B"], WORK["H"], WORK["N"], WORK["d"]
+    alpha, k_keep, scale = WORK["alpha"], WORK["k_keep"], WORK["sm_scale"]
+    g = torch.Generator().manual_seed(0)
+    Q, K, V = (torch.randn(B, H, N, d, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+    dO = torch.randn(B, H, N, d, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+    idx = torch.arange(N, dtype=torch.int32, device=dev).unsqueeze(0).expand(B * H, N).contiguous()
+    q, k, v = (t.clone().requires_grad_(True) for t in (Q, K, V))
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        out = sa.splash_attention(q, k, v, idx, idx, alpha, k_keep, scale, args.grad_mode)
+        out.backward(dO)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_read()  # drop anything recorded so far
+    _lib.profile_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.profile_enable(False)
+    kern = _lib.profile_read()
+    ms = (t1 - t0) * 1e3 / args.steps
+
+    # Block-mask density of this workload (same for every step: same inputs).
+    _, st = sa.ops.splash_forward(*sa.ops.check_inputs(Q, K, V, idx, idx), alpha, k_keep, scale)
+    nnzb = int(st.mask.sum().item())
+    nQB = nKB = N // 64
+    models = kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep)
+    kernels = {}
+    for name, (cnt, tot) in kern.items():
+        if name in models:
+            kernels[name] = roofline_of(models[name], tot / cnt)
+            kernels[name]["launches"] = cnt
+    dominant = max(kernels, key=lambda n: kernels[n]["avg_ms"])
+    roof = {kk: kernels[dominant][kk] for kk in ("bound", "achieved", "peak", "unit", "frac",
+                                                 "traffic")}
+    roof["kernel"] = dominant
+
+    eff = effective_flops(B, H, N, d)
+    line = {
+        "metric": METRIC,
+        "value": round(eff / (ms / 1e3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) inputs, seeded",
+        "config": {"workload": "adaptive splash attention fwd+bwd (BASELINE configs[2])",
+                   "B": B, "H": H, "N": N, "d": d, "alpha": alpha, "k_keep": k_keep,
+                   "sm_scale": scale, "mask": "causal", "block": "64x64",
+                   "grad_mode": args.grad_mode, "parallelism": "single GPU",
+                   "active_block_pairs": nnzb,
+                   "active_block_density_of_causal": round(nnzb / (B * H * nQB * (nQB + 1) / 2), 4)},
+        "roofline": roof,
+        "kernels": kernels,
+    }
+    if not args.no_dense_baseline:
+        try:
+            dms = dense_gpu_baseline(Q, K, V, dO, alpha, scale)
+            line["dense_gpu_baseline"] = {"ms_per_step": round(dms, 3),
+                                          "speedup": round(dms / ms, 2),
+                                          "what": "PyTorch dense exact alpha-entmax fwd+bwd, fp32 "
+                                                  "math, [64,4096,4096] scores, 40 bisection steps"}
+        except Exception as e:  # report, do not fail the bench line
+            line["dense_gpu_baseline"] = {"error": repr(e)[:200]}
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -157,11 +157,12 @@ int asa_select_from_scores(const asa_problem *p, const float *scores, const int3
                            const int32_t *k_idx, const asa_state *st, void *workspace,
                            void *stream);
 
-/* Kernel timing for benchmarks (no reference counterpart).  While enabled,
- * every kernel launch on this thread is bracketed by HIP events;
- * asa_profile_read() synchronises on them and reports, per kernel name,
- * the number of launches and the summed duration in milliseconds, then
- * clears the record.  Returns the number of distinct kernels (<= max).    */
+/* Kernel timing for benchmarks (no reference counterpart).  While enabled
+ * (process-wide), every kernel launch of the library is bracketed by HIP
+ * events recorded on its launch stream; asa_profile_read() synchronises on
+ * them and reports, per kernel name, the number of launches and the summed
+ * duration in milliseconds, then clears the record.  Call it when no other
+ * thread is launching.  Returns the number of distinct kernels (<= max).  */
 int asa_profile_enable(int on);
 int asa_profile_read(int max, char (*names)[64], int *counts, double *total_ms);
 
