@@ -127,6 +127,18 @@ __device__ __forceinline__ uint64_t make_key(float s, int idx) {
 __device__ __forceinline__ float key_score(uint64_t k) { return score_of_ord(static_cast<uint32_t>(k >> 32)); }
 __device__ __forceinline__ int key_index(uint64_t k) { return static_cast<int>(~static_cast<uint32_t>(k)); }
 
+// XCD-aware block order.  MI355X places block i of a launch on XCD i % 8,
+// and each XCD has its own L2.  A 1-D launch of `total` blocks is mapped so
+// that the blocks of each XCD cover one contiguous range of tasks (a task
+// index is (batch*head) * blocks_per_head + block), which keeps the K/V (or
+// Q/dO) tiles of a head in the L2 of the XCD that reads them.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_task(int i, int total) {
+  const int x = i % kXcds, j = i / kXcds;
+  const int base = total / kXcds, rem = total % kXcds;
+  return x * base + (x < rem ? x : rem) + j;
+}
+
 // Reductions across the four lane groups that share a column of a 16x16
 // accumulator (lanes L, L^16, L^32, L^48).
 __device__ __forceinline__ float sum_groups(float v) {

@@ -24,6 +24,8 @@ struct SelectParams {
   uint8_t* mask;
   int32_t* topk_idx;      // optional
   float* topk_val;        // optional
+  uint64_t* cand;         // workspace: [BH, NQ, cap] candidate keys
+  int cap;                // select_capacity(k)
 };
 
 struct CompactParams {
@@ -75,6 +77,7 @@ struct BackwardParams {
 // name for the profiler.
 hipError_t launch_select(const SelectParams& p, bool bf16, bool from_scores, hipStream_t s);
 size_t select_lds_bytes(const Dims& d);
+int select_capacity(int k);
 hipError_t launch_compact(const CompactParams& p, hipStream_t s);
 hipError_t launch_forward(const ForwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_delta(const BackwardParams& p, bool bf16, hipStream_t s);

@@ -83,7 +83,8 @@ __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
-  const int qb = blockIdx.x, bh = blockIdx.y;
+  const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
+  const int qb = task % nQB, bh = task / nQB;
   const int q = qb * kBlock + 16 * w + c16;
   const bool qok = q < NQ;
   const size_t rows = size_t(p.d.BH) * NQ;
@@ -215,7 +216,8 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
-  const int kb = blockIdx.x, bh = blockIdx.y;
+  const int task = xcd_task(blockIdx.x, nKB * p.d.BH);
+  const int kb = task % nKB, bh = task / nKB;
   const int j = kb * kBlock + 16 * w + c16;  // this lane's key row
   const bool jok = j < NK;
   const size_t krow = size_t(bh) * NK + (jok ? j : 0);
@@ -304,7 +306,7 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
 
 template <typename T, int D>
 hipError_t launch_dq_td(const BackwardParams& p, hipStream_t s) {
-  dim3 grid(p.d.nQB, p.d.BH);
+  dim3 grid(p.d.nQB * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
     case kA15: hipLaunchKernelGGL((dq_kernel<T, D, kA15>), grid, dim3(kThreads), 0, s, p); break;
     case kA20: hipLaunchKernelGGL((dq_kernel<T, D, kA20>), grid, dim3(kThreads), 0, s, p); break;
@@ -316,7 +318,7 @@ hipError_t launch_dq_td(const BackwardParams& p, hipStream_t s) {
 
 template <typename T, int D>
 hipError_t launch_dkdv_td(const BackwardParams& p, hipStream_t s) {
-  dim3 grid(p.d.nKB, p.d.BH);
+  dim3 grid(p.d.nKB * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
     case kA15: hipLaunchKernelGGL((dkdv_kernel<T, D, kA15>), grid, dim3(kThreads), 0, s, p); break;
     case kA20: hipLaunchKernelGGL((dkdv_kernel<T, D, kA20>), grid, dim3(kThreads), 0, s, p); break;

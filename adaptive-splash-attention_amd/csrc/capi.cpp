@@ -104,7 +104,10 @@ void sizes_of(const Shape& s, asa_sizes* z) {
   z->k_list = blocks * sizeof(int32_t);
   z->topk_idx = rows * s.k * sizeof(int32_t);
   z->topk_val = rows * s.k * sizeof(float);
-  z->workspace = 2 * rows * sizeof(float);
+  // forward: candidate keys of the score pass; backward: two floats per row
+  const size_t fwd_ws = rows * size_t(asa::select_capacity(s.k)) * sizeof(uint64_t);
+  const size_t bwd_ws = 2 * rows * sizeof(float);
+  z->workspace = fwd_ws > bwd_ws ? fwd_ws : bwd_ws;
 }
 
 int check_state(const asa_state* st, bool need_norms) {
@@ -147,8 +150,11 @@ std::vector<Rec> g_recs;
 thread_local int g_open = -1;  // index of this thread's launch being timed
 
 int run_select(const Shape& sh, const void* q, const void* k, const float* scores,
-               const int32_t* q_idx, const int32_t* k_idx, const asa_state* st, hipStream_t s) {
+               const int32_t* q_idx, const int32_t* k_idx, const asa_state* st, void* workspace,
+               hipStream_t s) {
   asa::SelectParams sp{};
+  sp.cand = static_cast<uint64_t*>(workspace);
+  sp.cap = asa::select_capacity(sh.k);
   sp.d = dims_of(sh);
   sp.q = q;
   sp.k = k;
@@ -230,11 +236,11 @@ int asa_forward(const asa_problem* p, const void* q, const void* k, const void* 
   if (!q || !k || !v || !q_idx || !k_idx || !out)
     return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
   if (int rc = check_state(st, true)) return rc;
-  (void)workspace;
+  if (!workspace) return fail(ASA_ERR_INVALID_ARGUMENT, "workspace is NULL");
   if (int rc = check_select_lds(sh)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
-  if (int rc = run_select(sh, q, k, nullptr, q_idx, k_idx, st, s)) return rc;
+  if (int rc = run_select(sh, q, k, nullptr, q_idx, k_idx, st, workspace, s)) return rc;
 
   asa::ForwardParams fp{};
   fp.d = dims_of(sh);
@@ -318,10 +324,10 @@ int asa_select_from_scores(const asa_problem* p, const float* scores, const int3
   if (!scores || !q_idx || !k_idx)
     return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
   if (int rc = check_state(st, false)) return rc;
-  (void)workspace;
+  if (!workspace) return fail(ASA_ERR_INVALID_ARGUMENT, "workspace is NULL");
   if (int rc = check_select_lds(sh)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (int rc = run_select(sh, nullptr, nullptr, scores, q_idx, k_idx, st, s)) return rc;
+  if (int rc = run_select(sh, nullptr, nullptr, scores, q_idx, k_idx, st, workspace, s)) return rc;
   return ok();
 }
 

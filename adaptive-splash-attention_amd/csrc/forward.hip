@@ -48,7 +48,8 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
-  const int qb = blockIdx.x, bh = blockIdx.y;
+  const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
+  const int qb = task % nQB, bh = task / nQB;
   const int q = qb * kBlock + 16 * w + c16;  // this lane's query row
   const bool qok = q < NQ;
   const size_t row = size_t(bh) * NQ + (qok ? q : 0);
@@ -115,7 +116,7 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
 
 template <typename T, int D>
 hipError_t launch_td(const ForwardParams& p, hipStream_t s) {
-  dim3 grid(p.d.nQB, p.d.BH);
+  dim3 grid(p.d.nQB * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
     case kA15: hipLaunchKernelGGL((forward_kernel<T, D, kE2>), grid, dim3(kThreads), 0, s, p); break;
     case kA20: hipLaunchKernelGGL((forward_kernel<T, D, kE1>), grid, dim3(kThreads), 0, s, p); break;

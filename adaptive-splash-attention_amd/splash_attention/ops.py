@@ -153,6 +153,12 @@ def alloc_state(p: _lib.Problem, device, with_topk: bool = False) -> SplashState
     return st
 
 
+def workspace(p: _lib.Problem, device) -> torch.Tensor:
+    """Scratch memory the entry points need for problem `p` (asa_sizes.workspace)."""
+    z = _lib.query_sizes(p)
+    return torch.empty(max(z.workspace, 16), device=device, dtype=torch.uint8)
+
+
 def splash_forward(Q, K, V, Q_idx, K_idx, alpha: float, k_keep: int, sm_scale=None,
                    with_topk: bool = False):
     """Forward pass; returns (out, SplashState).  Inputs as check_inputs() returns them."""
@@ -161,11 +167,12 @@ def splash_forward(Q, K, V, Q_idx, K_idx, alpha: float, k_keep: int, sm_scale=No
     p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale)
     st = alloc_state(p, Q.device, with_topk)
     out = torch.empty_like(Q)
+    ws = workspace(p, Q.device)
     cst = st.c_struct()
     with torch.cuda.device(Q.device):
         rc = lib.asa_forward(ctypes.byref(p), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
                              Q_idx.data_ptr(), K_idx.data_ptr(), out.data_ptr(),
-                             ctypes.byref(cst), None, _stream(Q.device))
+                             ctypes.byref(cst), ws.data_ptr(), _stream(Q.device))
     _lib.check(rc)
     return out, st
 
@@ -181,8 +188,7 @@ def splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st: SplashState, alpha: fl
     if dout.shape != Q.shape:
         raise ValueError(f"dOut shape {tuple(dout.shape)} must equal Q shape {tuple(Q.shape)}")
     dout = _aligned(dout.to(Q.dtype))
-    z = _lib.query_sizes(p)
-    ws = torch.empty(z.workspace // 4, device=Q.device, dtype=torch.float32)
+    ws = workspace(p, Q.device)
     dQ = torch.empty_like(Q)
     dK = torch.empty_like(K)
     dV = torch.empty_like(V)
@@ -222,10 +228,11 @@ def select_from_scores(scores, Q_idx, K_idx, alpha: float, k_keep: int, batch: i
     p = make_problem(batch, heads, NQ, NK, 64, torch.float32, alpha, k_keep, 1.0)
     st = alloc_state(p, scores.device, with_topk=True)
     scores = scores.contiguous()
+    ws = workspace(p, scores.device)
     cst = st.c_struct()
     with torch.cuda.device(scores.device):
         rc = lib.asa_select_from_scores(ctypes.byref(p), scores.data_ptr(), qi.data_ptr(),
-                                        ki.data_ptr(), ctypes.byref(cst), None,
+                                        ki.data_ptr(), ctypes.byref(cst), ws.data_ptr(),
                                         _stream(scores.device))
     _lib.check(rc)
     return st
