@@ -102,28 +102,41 @@ __device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const float* rm,
     }
 }
 
-// bf16: `tr` is the transposed tile.  x is rounded to bf16.
-template <int D>
+// bf16: `tr` is the transposed tile.  x is rounded to bf16; with Split,
+// x is carried as the sum of two bf16 terms (hi = bf16(x), lo = bf16(x - hi),
+// 16 significant bits), so that sums with heavy cancellation -- gradient
+// rows whose weights sum to zero against keys that share a common
+// component -- keep fp32-level accuracy at the cost of a second MFMA.
+template <int D, bool Split = false>
 __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const u16* tr,
                                              const f32x4 (&x)[4], int lane) {
   const int g = lane >> 4, c = lane & 15;
   for (int cc = 0; cc < 2; ++cc) {
-    bf16x8 b;
+    bf16x8 b, bl;
     for (int r = 0; r < 4; ++r) {
       b[r] = static_cast<__bf16>(x[2 * cc][r]);
       b[4 + r] = static_cast<__bf16>(x[2 * cc + 1][r]);
+      if (Split) {
+        bl[r] = static_cast<__bf16>(x[2 * cc][r] - static_cast<float>(b[r]));
+        bl[4 + r] = static_cast<__bf16>(x[2 * cc + 1][r] - static_cast<float>(b[4 + r]));
+      }
     }
+    bf16x8 a[D / 16];
     for (int db = 0; db < D / 16; ++db) {
       const u16* p = tr + (16 * db + c) * Tile<u16, D>::kTs + 32 * cc + 4 * g;
       const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
       const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16);
-      const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      o[db] = mfma(a, b, o[db]);
+      a[db] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o[db] = mfma(a[db], b, o[db]);
     }
+    // the lo terms after all hi terms: D/16 independent chains between
+    // two products into the same accumulator
+    if (Split)
+      for (int db = 0; db < D / 16; ++db) o[db] = mfma(a[db], bl, o[db]);
   }
 }
-// fp32: `rm` is the row-major tile.
-template <int D>
+// fp32: `rm` is the row-major tile (exact operands; Split has no effect).
+template <int D, bool Split = false>
 __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const float* rm,
                                              const f32x4 (&x)[4], int lane) {
   const int g = lane >> 4, c = lane & 15;

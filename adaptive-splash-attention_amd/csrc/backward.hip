@@ -22,6 +22,12 @@
 //                  on MFMA, P = p / (sum p + EPS), ds = c w (dp - shift),
 //                  dV^T += dO^T P and dK^T += Q^T ds on MFMA.
 //
+// bf16 inputs: the per-score operands of the dQ and dK products (w dp, w,
+// ds) enter the MFMA as hi + lo bf16 pairs.  A row's ds sums to zero, so
+// with keys (or queries) that share a common component the products cancel
+// heavily; a single bf16 rounding of ds would leave an error relative to
+// sum |ds| |k| rather than to the (much smaller) result.
+//
 // In both modes ds = c * w * (dp - shift); the modes differ in (c, shift):
 //   entmax (ASA_GRAD_ENTMAX):     c = (sum p + EPS)^(alpha-2),
 //                                 shift = sum(w dp) / sum(w)
@@ -156,8 +162,8 @@ __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
           dacc[f][r] = wv;
         }
       }
-    tile_t_x_acc<D>(a1, sm.k_operand(), sacc, lane);
-    if (!ref) tile_t_x_acc<D>(a2, sm.k_operand(), dacc, lane);
+    tile_t_x_acc<D, true>(a1, sm.k_operand(), sacc, lane);
+    if (!ref) tile_t_x_acc<D, true>(a2, sm.k_operand(), dacc, lane);
   }
 
   if (!ref) {
@@ -287,7 +293,7 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
         dacc[f][r] = pn;
       }
     tile_t_x_acc<D>(av, sm.do_operand(), dacc, lane);
-    tile_t_x_acc<D>(ak, sm.q_operand(), sacc, lane);
+    tile_t_x_acc<D, true>(ak, sm.q_operand(), sacc, lane);
   }
 
   if (jok) {

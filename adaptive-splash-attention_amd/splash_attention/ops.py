@@ -91,10 +91,6 @@ def check_inputs(Q, K, V, Q_idx=None, K_idx=None):
             raise ValueError(f"{name} must be 4-D [B, H, N, d], got shape {tuple(t.shape)}")
     if Q.size(3) > MAX_HEAD_DIM:
         raise ValueError("Head dimension too large; increase D_MAX")
-    if not Q.is_cuda:
-        raise RuntimeError("Tensors must be on CUDA device")
-    if K.device != Q.device or V.device != Q.device:
-        raise RuntimeError("All tensors must be on same device")
     if Q.dtype not in _DTYPES:
         raise TypeError(f"unsupported dtype {Q.dtype}; use torch.float32 or torch.bfloat16")
     if K.dtype != Q.dtype or V.dtype != Q.dtype:
@@ -109,6 +105,10 @@ def check_inputs(Q, K, V, Q_idx=None, K_idx=None):
     NK = K.shape[2]
     if NQ < 1 or NK < 1 or B < 1 or H < 1:
         raise ValueError("empty attention problem")
+    if not Q.is_cuda:
+        raise RuntimeError("Tensors must be on CUDA device")
+    if K.device != Q.device or V.device != Q.device:
+        raise RuntimeError("All tensors must be on same device")
     BH = B * H
     qi = _index(Q_idx, BH, NQ, B, H, Q.device, "Q_idx")
     ki = _index(K_idx, BH, NK, B, H, Q.device, "K_idx")

@@ -1,0 +1,114 @@
+"""The C ABI library (no GPU needed): it loads, exports every function that
+include/adasplash.h declares, and validates arguments on the host."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "adasplash.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*\*?\s*(asa_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from splash_attention import _lib
+
+    return _lib.load()
+
+
+def test_header_declares_what_the_binding_binds():
+    from splash_attention import _lib
+
+    assert _declared() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    from splash_attention import _lib
+
+    assert lib.asa_abi_version() == _lib.ABI_VERSION
+    hdr = open(os.path.join(ROOT, "include", "adasplash.h")).read()
+    assert f"#define ASA_ABI_VERSION {_lib.ABI_VERSION}" in hdr
+
+
+def _problem(**kw):
+    from splash_attention import _lib
+
+    base = dict(batch=4, heads=16, nq=4096, nk=4096, head_dim=64, k_keep=32, block_m=64,
+                block_n=64, alpha=1.5, sm_scale=0.125, dtype=_lib.DTYPE_BF16)
+    base.update(kw)
+    return _lib.Problem(**base)
+
+
+def test_query_sizes_headline():
+    from splash_attention import _lib
+
+    z = _lib.query_sizes(_problem())
+    rows = 64 * 4096
+    assert z.taus == rows * 4 and z.norms == rows * 4
+    assert z.mask == 64 * 64 * 64
+    assert z.q_ptr == 64 * 65 * 4 and z.k_ptr == 64 * 65 * 4
+    assert z.q_list == 64 * 64 * 64 * 4 and z.k_list == z.q_list
+    assert z.topk_idx == rows * 32 * 4
+    assert z.workspace >= 2 * rows * 4
+
+
+@pytest.mark.parametrize("bad,code,msg", [
+    (dict(head_dim=256), 1, "Head dimension too large"),
+    (dict(head_dim=96), 2, "head_dim 96 not supported"),
+    (dict(k_keep=0), 1, "k_keep"),
+    (dict(k_keep=129), 1, "k_keep"),
+    (dict(block_m=32), 2, "block_m"),
+    (dict(nq=0), 1, "nq"),
+    (dict(batch=0), 1, "batch"),
+    (dict(dtype=7), 1, "dtype"),
+    (dict(alpha=float("nan")), 1, "alpha"),
+    (dict(sm_scale=float("inf")), 1, "sm_scale"),
+])
+def test_invalid_problems_are_rejected_on_the_host(lib, bad, code, msg):
+    from splash_attention import _lib
+
+    p = _problem(**bad)
+    z = _lib.Sizes()
+    assert lib.asa_query_sizes(ctypes.byref(p), ctypes.byref(z)) == code
+    assert msg in lib.asa_last_error().decode()
+    # the entry points validate before touching the device
+    st = _lib.State()
+    rc = lib.asa_forward(ctypes.byref(p), None, None, None, None, None, None, ctypes.byref(st),
+                         None, None)
+    assert rc == code
+
+
+def test_null_pointers_are_rejected(lib):
+    from splash_attention import _lib
+
+    p = _problem()
+    st = _lib.State()
+    assert lib.asa_forward(ctypes.byref(p), None, None, None, None, None, None,
+                           ctypes.byref(st), None, None) == _lib.ASA_ERR_INVALID_ARGUMENT
+    assert "NULL" in lib.asa_last_error().decode()
+    assert lib.asa_backward(ctypes.byref(p), 5, None, None, None, None, None, None, None,
+                            ctypes.byref(st), None, None, None, None, None) == \
+        _lib.ASA_ERR_INVALID_ARGUMENT
+    assert "grad_mode" in lib.asa_last_error().decode()
+
+
+def test_error_string_is_cleared_on_success(lib):
+    from splash_attention import _lib
+
+    z = _lib.Sizes()
+    bad = _problem(k_keep=0)
+    lib.asa_query_sizes(ctypes.byref(bad), ctypes.byref(z))
+    assert lib.asa_last_error().decode() != ""
+    good = _problem()
+    assert lib.asa_query_sizes(ctypes.byref(good), ctypes.byref(z)) == 0
+    assert lib.asa_last_error().decode() == ""

@@ -1,0 +1,89 @@
+"""Host-side behaviour of the Python API (no GPU needed)."""
+import pytest
+import torch
+
+import splash_attention as sa
+from splash_attention import ops
+
+
+def _t(*shape, dtype=torch.float32):
+    return torch.zeros(*shape, dtype=dtype)
+
+
+def test_module_mirrors_readme_signature():
+    m = sa.AdaptiveSplashAttention(head_dim=64, alpha=1.5, k_keep=8, adaptive_threshold=True,
+                                   sm_scale=0.125)
+    assert (m.head_dim, m.alpha, m.k_keep, m.sm_scale) == (64, 1.5, 8, 0.125)
+    assert len(m.state_dict()) == 0 and len(list(m.parameters())) == 0
+    assert "k_keep=8" in repr(m)
+    assert sa.AdaptiveSplashAttention(head_dim=128).sm_scale == pytest.approx(128 ** -0.5)
+
+
+@pytest.mark.parametrize("kw", [dict(head_dim=96), dict(k_keep=0), dict(k_keep=200),
+                                dict(grad_mode="exact")])
+def test_module_rejects_bad_config(kw):
+    with pytest.raises(ValueError):
+        sa.AdaptiveSplashAttention(**kw)
+
+
+def test_head_dim_limit_message_matches_reference():
+    # adasplashattention.cu:542
+    with pytest.raises(ValueError, match="Head dimension too large; increase D_MAX"):
+        ops.check_inputs(_t(1, 1, 8, 256), _t(1, 1, 8, 256), _t(1, 1, 8, 256))
+
+
+def test_cpu_tensors_are_rejected_like_the_reference():
+    # adasplashattention.cu:543
+    with pytest.raises(RuntimeError, match="Tensors must be on CUDA device"):
+        ops.check_inputs(_t(1, 2, 8, 64), _t(1, 2, 8, 64), _t(1, 2, 8, 64))
+
+
+@pytest.mark.parametrize("Q,K,V,err", [
+    (_t(1, 2, 8), _t(1, 2, 8, 64), _t(1, 2, 8, 64), ValueError),
+    (_t(1, 2, 8, 64), _t(1, 3, 8, 64), _t(1, 3, 8, 64), ValueError),
+    (_t(1, 2, 8, 64), _t(1, 2, 8, 64), _t(1, 2, 9, 64), ValueError),
+    (_t(1, 2, 8, 32), _t(1, 2, 8, 32), _t(1, 2, 8, 32), ValueError),
+    (_t(1, 2, 8, 64, dtype=torch.float16), _t(1, 2, 8, 64, dtype=torch.float16),
+     _t(1, 2, 8, 64, dtype=torch.float16), TypeError),
+    (_t(1, 2, 8, 64), _t(1, 2, 8, 64, dtype=torch.bfloat16), _t(1, 2, 8, 64), TypeError),
+])
+def test_shape_and_dtype_validation(Q, K, V, err):
+    with pytest.raises(err):
+        ops.check_inputs(Q, K, V)
+
+
+def test_index_normalisation():
+    dev = torch.device("cpu")
+    a = ops._index(None, 6, 5, 2, 3, dev, "Q_idx")
+    assert a.dtype == torch.int32 and a.shape == (6, 5) and a[3].tolist() == [0, 1, 2, 3, 4]
+    b = ops._index(torch.arange(5, dtype=torch.int64), 6, 5, 2, 3, dev, "Q_idx")
+    assert torch.equal(a, b)
+    c = ops._index(torch.arange(5).expand(2, 3, 5), 6, 5, 2, 3, dev, "K_idx")
+    assert torch.equal(a, c) and c.is_contiguous()
+    with pytest.raises(ValueError, match="int32"):
+        ops._index(torch.full((6, 5), 2 ** 40), 6, 5, 2, 3, dev, "Q_idx")
+    with pytest.raises(TypeError):
+        ops._index(torch.zeros(6, 5), 6, 5, 2, 3, dev, "Q_idx")
+    with pytest.raises(ValueError, match=r"\[B\*H, N\]"):
+        ops._index(torch.zeros(6, 4, dtype=torch.int32), 6, 5, 2, 3, dev, "Q_idx")
+
+
+def test_alpha_clamp_matches_reference():
+    # adasplashattention.cu:547
+    assert ops.clamp_alpha(0.5) == 1.05 and ops.clamp_alpha(7.0) == 3.0
+    assert ops.clamp_alpha(1.5) == 1.5
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from splash_attention import _build, _lib
+
+    monkeypatch.setattr(_build, "LIB", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(_lib, "_handle", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load()
+
+
+def test_grad_mode_validation():
+    with pytest.raises(ValueError):
+        sa.splash_attention(_t(1, 1, 8, 64), _t(1, 1, 8, 64), _t(1, 1, 8, 64),
+                            grad_mode="bogus")

@@ -1,0 +1,140 @@
+"""GPU tests of the user-facing API against the CPU oracle.
+
+Tolerances: max |gpu - oracle| / max |oracle| <= 1e-5 (fp32), 2e-2 (bf16).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import splash_attention as sa
+from oracle import oracle as orc
+from tests._util import assert_close, causal_idx, make_inputs, np32
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def test_module_autograd_matches_oracle(dev):
+    print("[api] module autograd fp32 1x2x256x64", flush=True)
+    B, H, N, d = 1, 2, 256, 64
+    Q, K, V, dO = make_inputs(B, H, N, N, d, seed=3)
+    attn = sa.AdaptiveSplashAttention(head_dim=64, alpha=1.5, k_keep=8, sm_scale=0.125)
+    q, k, v = (t.to(dev).requires_grad_(True) for t in (Q, K, V))
+    idx = causal_idx(B * H, N).to(dev)
+    out = attn(q, k, v, idx, idx)
+    out.backward(dO.to(dev))
+    fw, (gq, gk, gv) = orc.attention(np32(Q), np32(K), np32(V), idx.cpu().numpy(),
+                                     idx.cpu().numpy(), np32(dO), 1.5, 0.125, 8)
+    assert_close("out", np32(out), fw.out, 1e-5)
+    assert_close("dQ", np32(q.grad), gq, 1e-5)
+    assert_close("dK", np32(k.grad), gk, 1e-5)
+    assert_close("dV", np32(v.grad), gv, 1e-5)
+
+
+def test_reference_style_entry_points(dev):
+    """sa.forward / sa.backward take the reference's argument order
+    (adasplashattention.cu:537-541, :611-616) and return its gradient."""
+    print("[api] reference-style forward/backward", flush=True)
+    B, H, N, d = 1, 2, 192, 64
+    Q, K, V, dO = make_inputs(B, H, N, N, d, seed=4)
+    idx = causal_idx(B * H, N)
+    out = sa.forward(Q.to(dev), K.to(dev), V.to(dev), idx.to(dev), idx.to(dev), 0.125, 1.5)
+    dQ, dK, dV = sa.backward(Q.to(dev), K.to(dev), V.to(dev), idx.to(dev), idx.to(dev), 0.125,
+                             1.5, dO.to(dev))
+    fw, (gq, gk, gv) = orc.attention(np32(Q), np32(K), np32(V), idx.numpy(), idx.numpy(),
+                                     np32(dO), 1.5, 0.125, 8, mode=orc.GRAD_REFERENCE)
+    assert_close("out", np32(out), fw.out, 1e-5)
+    assert_close("dQ", np32(dQ), gq, 1e-5)
+    assert_close("dK", np32(dK), gk, 1e-5)
+    assert_close("dV", np32(dV), gv, 1e-5)
+
+
+def test_default_int64_arange_indices_are_accepted(dev):
+    """README.md:120-121 passes int64 arange indices (the reference would
+    reject them, adasplashattention.cu:571); they are converted."""
+    B, H, N, d = 1, 1, 128, 64
+    Q, K, V, _ = make_inputs(B, H, N, N, d, seed=5)
+    i64 = torch.arange(N, device=dev).expand(B * H, N).contiguous()
+    a = sa.forward(Q.to(dev), K.to(dev), V.to(dev), i64, i64, 0.125, 1.5)
+    b = sa.forward(Q.to(dev), K.to(dev), V.to(dev), i64.int(), i64.int(), 0.125, 1.5)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_deterministic(dev, dtype):
+    print(f"[api] determinism {dtype}", flush=True)
+    B, H, N, d = 2, 2, 320, 64
+    Q, K, V, dO = make_inputs(B, H, N, N, d, seed=6, dtype=dtype)
+    res = []
+    for _ in range(2):
+        q, k, v = (t.to(dev).requires_grad_(True) for t in (Q, K, V))
+        out = sa.splash_attention(q, k, v, None, None, 1.5, 16, 0.125)
+        out.backward(dO.to(dev))
+        res.append([x.detach().cpu() for x in (out, q.grad, k.grad, v.grad)])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
+def test_golden_fixture_on_gpu(dev):
+    g = dict(np.load(os.path.join(GOLDEN, "c1_head0.npz")))
+    print("[api] golden c1_head0 fp32", flush=True)
+    t = lambda a: torch.from_numpy(a).unsqueeze(0).to(dev)  # [1, 1, N, d]
+    q, k, v = t(g["Q"]), t(g["K"]), t(g["V"])
+    qi = torch.from_numpy(g["idx"]).to(dev)
+    q, k, v, qi, ki = sa.ops.check_inputs(q, k, v, qi, qi)
+    out, st = sa.ops.splash_forward(q, k, v, qi, ki, float(g["alpha"]), int(g["k"]),
+                                    float(g["scale"]), with_topk=True)
+    np.testing.assert_array_equal(st.mask.cpu().numpy(), g["mask"])
+    np.testing.assert_array_equal(st.q_list.cpu().numpy(), g["q_list"])
+    assert_close("taus", st.taus.cpu().numpy(), g["taus"], 1e-5)
+    assert_close("out", np32(out), g["out"], 1e-5)
+    for mode in ("entmax", "reference"):
+        grads = sa.ops.splash_backward(q, k, v, qi, ki, out, t(g["dO"]), st, float(g["alpha"]),
+                                       int(g["k"]), float(g["scale"]), mode)
+        for name, x in zip(("dQ", "dK", "dV"), grads):
+            assert_close(f"{name}/{mode}", np32(x), g[f"{name}_{mode}"], 1e-5)
+
+
+def test_nan_scores_follow_reference_clamp(dev):
+    """A NaN score clamps to -10 (fmaxf/fminf, adasplashattention.cu:196-197);
+    the output stays finite and matches the oracle's identical rule."""
+    B, H, N, d = 1, 1, 128, 64
+    Q, K, V, dO = make_inputs(B, H, N, N, d, seed=8)
+    Q[0, 0, 5, :] = float("nan")
+    K[0, 0, 17, 3] = float("nan")
+    idx = causal_idx(1, N)
+    out = sa.forward(Q.to(dev), K.to(dev), V.to(dev), idx.to(dev), idx.to(dev), 0.125, 1.5)
+    assert torch.isfinite(out).all()
+    fw = orc.forward(np32(Q), np32(K), np32(V), idx.numpy(), idx.numpy(), 1.5, 0.125, 8)
+    assert_close("out", np32(out), fw.out, 1e-5)
+
+
+def test_noncausal_positions_and_nq_ne_nk(dev):
+    """Non-causal attention expressed by positions (Q_idx = NK-1), NQ != NK."""
+    B, H, NQ, NK, d = 1, 2, 96, 200, 64
+    Q, K, V, dO = make_inputs(B, H, NQ, NK, d, seed=9)
+    qi = torch.full((B * H, NQ), NK - 1, dtype=torch.int32)
+    ki = causal_idx(B * H, NK)
+    q, k, v = (t.to(dev).requires_grad_(True) for t in (Q, K, V))
+    out = sa.splash_attention(q, k, v, qi.to(dev), ki.to(dev), 2.0, 16, 0.125)
+    out.backward(dO.to(dev))
+    fw, (gq, gk, gv) = orc.attention(np32(Q), np32(K), np32(V), qi.numpy(), ki.numpy(),
+                                     np32(dO), 2.0, 0.125, 16)
+    assert_close("out", np32(out), fw.out, 1e-5)
+    assert_close("dQ", np32(q.grad), gq, 1e-5)
+    assert_close("dK", np32(k.grad), gk, 1e-5)
+    assert_close("dV", np32(v.grad), gv, 1e-5)
+
+
+def test_non_contiguous_inputs(dev):
+    B, H, N, d = 1, 2, 128, 64
+    Q, K, V, _ = make_inputs(B, H, N, N, d, seed=10)
+    # [B, N, H, d] storage viewed as [B, H, N, d]
+    qt, kt, vt = (t.transpose(1, 2).contiguous().transpose(1, 2).to(dev) for t in (Q, K, V))
+    assert not qt.is_contiguous()
+    idx = causal_idx(B * H, N).to(dev)
+    a = sa.forward(qt, kt, vt, idx, idx, 0.125, 1.5)
+    b = sa.forward(Q.to(dev), K.to(dev), V.to(dev), idx, idx, 0.125, 1.5)
+    assert torch.equal(a, b)

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from tests._util import assert_close, causal_idx, make_inputs, np32
+from tests._util import assert_close, assert_tau_close, causal_idx, make_inputs, np32, oracle_at_gpu_tau
 
 pytestmark = pytest.mark.gpu
 
@@ -67,6 +67,8 @@ def test_attention_parity(dev, name, B, H, NQ, NK, d, alpha, k, scale, dtype, mo
     kidx = causal_idx(BH, NK)
     out, st, grads = _gpu(dev, Q, K, V, dO, qidx, kidx, alpha, k, scale, mode)
     m = orc.GRAD_ENTMAX if mode == "entmax" else orc.GRAD_REFERENCE
-    fw, og = orc.attention(np32(Q), np32(K), np32(V), qidx.numpy(), kidx.numpy(), np32(dO), alpha,
-                           scale, k, mode=m)
-    _check(f"{name}/{mode}", dtype, out, st, grads, fw, og)
+    own, fw, og = oracle_at_gpu_tau(np32(Q), np32(K), np32(V), np32(dO), qidx.numpy(),
+                                    kidx.numpy(), alpha, scale, k, st.taus.cpu().numpy(), m)
+    assert_tau_close(st.taus.cpu().numpy(), own.taus, alpha)
+    np.testing.assert_array_equal(st.mask.cpu().numpy(), own.mask, err_msg=f"{name}: mask")
+    _check(f"{name}/{mode}", dtype, out, st, grads, fw, og, check_state=False)

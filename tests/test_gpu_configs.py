@@ -1,0 +1,160 @@
+"""The BASELINE.json configurations at their real shapes on the GPU.
+
+Where the oracle can afford the whole problem it checks everything; at the
+large shapes it checks sampled (batch, head) slices or 64-row query blocks
+(rows of different query blocks are independent given all keys), and the
+full gradients through size-independent identities of the entmax-Jacobian
+gradient:
+  sum_j dK_j = 0        (entmax weights are invariant to adding a constant to
+                         all scores of a row, so each row's ds sums to zero)
+  sum_j dV_j = sum_i N_i / (N_i + EPS) dO_i   (each row's weights sum to
+                         N_i / (N_i + EPS))
+Tolerances: 1e-5 relative (fp32), 2e-2 relative (bf16), max-norm.
+"""
+import numpy as np
+import pytest
+import torch
+
+import splash_attention as sa
+from oracle import oracle as orc
+from tests._util import assert_close, assert_tau_close, causal_idx, np32, oracle_at_gpu_tau
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(dev, Q, K, V, dO, qi, ki, alpha, k, scale, mode="entmax"):
+    q, kk, v, qi_, ki_ = sa.ops.check_inputs(Q.to(dev), K.to(dev), V.to(dev), qi.to(dev), ki.to(dev))
+    out, st = sa.ops.splash_forward(q, kk, v, qi_, ki_, alpha, k, scale)
+    grads = sa.ops.splash_backward(q, kk, v, qi_, ki_, out, dO.to(dev), st, alpha, k, scale, mode)
+    torch.cuda.synchronize()
+    return out, st, grads
+
+
+def _gauss(shape, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dtype)
+
+
+def _identities(name, out_norms, grads, dO, tol):
+    """Size-independent checks of a full (entmax-mode) backward."""
+    dQ, dK, dV = (g.float() for g in grads)
+    BH = dK.shape[0] * dK.shape[1]
+    dKs = dK.reshape(BH, -1, dK.shape[-1]).double().sum(1)
+    e = float(dKs.abs().max() / dK.double().abs().amax(dim=(0, 1, 2)).max().clamp_min(1e-30))
+    assert e < 50 * tol, f"{name}: sum_j dK_j not ~0 (rel {e:.2e})"
+    n = out_norms.double()
+    wsum = (n / (n + 1e-8)).unsqueeze(-1)
+    want = (wsum * dO.reshape(BH, -1, dO.shape[-1]).to(dV.device).double()).sum(1)
+    got = dV.reshape(BH, -1, dV.shape[-1]).double().sum(1)
+    e2 = float((got - want).abs().max() / want.abs().max())
+    assert e2 < tol, f"{name}: sum_j dV_j mismatch (rel {e2:.2e})"
+    for g in (dQ, dK, dV):
+        assert torch.isfinite(g).all()
+
+
+def test_c2_fp32_full(dev):
+    """B=2, H=8, N=1024, d=64 fp32, alpha 1.5, k 8, causal."""
+    print("[cfg] c2 fp32 2x8x1024x64", flush=True)
+    B, H, N, d = 2, 8, 1024, 64
+    Q, K, V = (_gauss((B, H, N, d), s, torch.float32) for s in (0, 1, 2))
+    dO = _gauss((B, H, N, d), 3, torch.float32)
+    idx = causal_idx(B * H, N)
+    for mode, m in (("entmax", orc.GRAD_ENTMAX), ("reference", orc.GRAD_REFERENCE)):
+        out, st, grads = _run(dev, Q, K, V, dO, idx, idx, 1.5, 8, 0.125, mode)
+        own, fw, og = oracle_at_gpu_tau(np32(Q), np32(K), np32(V), np32(dO), idx.numpy(),
+                                        idx.numpy(), 1.5, 0.125, 8, st.taus.cpu().numpy(), m)
+        np.testing.assert_array_equal(st.mask.cpu().numpy(), own.mask)
+        assert_tau_close(st.taus.cpu().numpy(), own.taus, 1.5)
+        assert_close("out", np32(out), fw.out, 1e-5)
+        for nm, g, w in zip(("dQ", "dK", "dV"), grads, og):
+            assert_close(f"{nm}/{mode}", np32(g), w, 1e-5)
+        if mode == "entmax":
+            _identities("c2", st.norms, grads, dO, 1e-5)
+
+
+def test_headline_bf16_sampled_heads(dev):
+    """B=4, H=16, N=4096, d=64 bf16, alpha 1.5, k 32, causal."""
+    print("[cfg] headline bf16 4x16x4096x64", flush=True)
+    B, H, N, d = 4, 16, 4096, 64
+    Q, K, V = (_gauss((B, H, N, d), s, torch.bfloat16) for s in (0, 1, 2))
+    dO = _gauss((B, H, N, d), 3, torch.bfloat16)
+    idx = causal_idx(B * H, N)
+    out, st, grads = _run(dev, Q, K, V, dO, idx, idx, 1.5, 32, 0.125)
+    assert torch.isfinite(out).all()
+    _identities("headline", st.norms, grads, dO, 2e-2)
+    for bh in (0, 37):
+        b, h = divmod(bh, H)
+        sl = lambda t: np32(t[b:b + 1, h:h + 1])
+        own, fw, og = oracle_at_gpu_tau(sl(Q), sl(K), sl(V), sl(dO), idx[:1].numpy(),
+                                        idx[:1].numpy(), 1.5, 0.125, 32,
+                                        st.taus[bh:bh + 1].cpu().numpy())
+        np.testing.assert_array_equal(st.mask[bh:bh + 1].cpu().numpy(), own.mask)
+        assert_tau_close(st.taus[bh:bh + 1].cpu().numpy(), own.taus, 1.5)
+        assert_close(f"out[{bh}]", sl(out), fw.out, 2e-2)
+        for nm, g, w in zip(("dQ", "dK", "dV"), grads, og):
+            assert_close(f"{nm}[{bh}]", sl(g), w, 2e-2)
+
+
+def _clustered(B, H, N, d, seed):
+    """configs[3] inputs: 64 Gaussian centres per head (sigma 1); keys are
+    centres + N(0, 0.1); queries are noisy copies (sigma 0.1) of random
+    centres; V ~ N(0, 1)."""
+    g = torch.Generator().manual_seed(seed)
+    C = torch.randn(B, H, 64, d, generator=g)
+    kid = torch.randint(0, 64, (B, H, N), generator=g)
+    qid = torch.randint(0, 64, (B, H, N), generator=g)
+    K = torch.gather(C, 2, kid.unsqueeze(-1).expand(B, H, N, d)) + 0.1 * torch.randn(B, H, N, d, generator=g)
+    Q = torch.gather(C, 2, qid.unsqueeze(-1).expand(B, H, N, d)) + 0.1 * torch.randn(B, H, N, d, generator=g)
+    V = torch.randn(B, H, N, d, generator=g)
+    dO = torch.randn(B, H, N, d, generator=g)
+    return tuple(t.to(torch.bfloat16) for t in (Q, K, V, dO))
+
+
+def _row_sample_check(name, out, taus, grads, Q, K, V, dO, qi, ki, alpha, k, scale, bh_list, q0s,
+                      H):
+    """Oracle on 64-row query blocks [q0, q0+64) of chosen heads: out and dQ."""
+    for bh in bh_list:
+        b, h = divmod(bh, H)
+        for q0 in q0s:
+            qs = slice(q0, q0 + 64)
+            own, fw, og = oracle_at_gpu_tau(np32(Q[b:b + 1, h:h + 1, qs]),
+                                            np32(K[b:b + 1, h:h + 1]), np32(V[b:b + 1, h:h + 1]),
+                                            np32(dO[b:b + 1, h:h + 1, qs]),
+                                            qi[bh:bh + 1, qs].numpy(), ki[bh:bh + 1].numpy(),
+                                            alpha, scale, k, taus[bh:bh + 1, qs].cpu().numpy())
+            assert_tau_close(taus[bh:bh + 1, qs].cpu().numpy(), own.taus, alpha)
+            assert_close(f"{name} out[{bh},{q0}]", np32(out[b:b + 1, h:h + 1, qs]), fw.out, 2e-2)
+            assert_close(f"{name} dQ[{bh},{q0}]", np32(grads[0][b:b + 1, h:h + 1, qs]), og[0], 2e-2)
+
+
+def test_c4_clustered_sparsemax_noncausal(dev):
+    """B=1, H=32, N=16384, d=128 bf16, alpha 2, k 64, non-causal."""
+    print("[cfg] c4 bf16 1x32x16384x128 clustered", flush=True)
+    B, H, N, d = 1, 32, 16384, 128
+    Q, K, V, dO = _clustered(B, H, N, d, seed=0)
+    qi = torch.full((B * H, N), N - 1, dtype=torch.int32)
+    ki = causal_idx(B * H, N)
+    scale = 128 ** -0.5
+    out, st, grads = _run(dev, Q, K, V, dO, qi, ki, 2.0, 64, scale)
+    assert torch.isfinite(out).all()
+    _identities("c4", st.norms, grads, dO, 2e-2)
+    _row_sample_check("c4", out, st.taus, grads, Q, K, V, dO, qi, ki, 2.0, 64, scale, (0, 21),
+                      (0, 8192), H)
+
+
+def test_c5_long_sinks(dev):
+    """B=1, H=8, N=32768, d=128 bf16, alpha 1.25, k 128, causal,
+    keys at positions 0..15 scaled x4 (attention sinks)."""
+    print("[cfg] c5 bf16 1x8x32768x128 sinks", flush=True)
+    B, H, N, d = 1, 8, 32768, 128
+    Q, K, V = (_gauss((B, H, N, d), s, torch.float32) for s in (0, 1, 2))
+    K[:, :, :16] *= 4
+    Q, K, V = (t.to(torch.bfloat16) for t in (Q, K, V))
+    dO = _gauss((B, H, N, d), 3, torch.bfloat16)
+    idx = causal_idx(B * H, N)
+    scale = 128 ** -0.5
+    out, st, grads = _run(dev, Q, K, V, dO, idx, idx, 1.25, 128, scale)
+    assert torch.isfinite(out).all()
+    _identities("c5", st.norms, grads, dO, 2e-2)
+    _row_sample_check("c5", out, st.taus, grads, Q, K, V, dO, idx, idx, 1.25, 128, scale, (3,),
+                      (0, 16384, 32704), H)
