@@ -88,6 +88,20 @@ __device__ __forceinline__ float pow_exact(float x, float e) {
   return static_cast<float>(pow(xd, static_cast<double>(e)));
 }
 
+// pow_exact with the exponent class fixed at compile time.  For kE2 the
+// float product is correctly rounded, hence equal to the double product
+// rounded once.
+template <int PC>
+__device__ __forceinline__ float pow_exact_c(float x, float e) {
+  if constexpr (PC == kE2) return x * x;
+  else if constexpr (PC == kE1) return x;
+  else if constexpr (PC == kE0) return 1.0f;
+  else if constexpr (PC == kE3) { const double xd = x; return static_cast<float>(xd * xd * xd); }
+  else if constexpr (PC == kE4) { const double x2 = static_cast<double>(x) * x; return static_cast<float>(x2 * x2); }
+  else if constexpr (PC == kEM1) return static_cast<float>(1.0 / static_cast<double>(x));
+  else return static_cast<float>(pow(static_cast<double>(x), static_cast<double>(e)));
+}
+
 template <int PC>
 __device__ __forceinline__ float pow_fast(float x, float e) {
   if constexpr (PC == kE2) return x * x;
@@ -137,6 +151,47 @@ __device__ __forceinline__ int xcd_task(int i, int total) {
   const int x = i % kXcds, j = i / kXcds;
   const int base = total / kXcds, rem = total % kXcds;
   return x * base + (x < rem ? x : rem) + j;
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane moves on the VALU (DPP), no trip through the LDS crossbar.
+//   quad_perm 0xB1 / 0x4E / 0x1B: lane i <- lane i^1 / i^2 / i^3 (in quads)
+//   row_half_mirror 0x141: lane i <- lane i^7 (in 8-lane half rows)
+//   row_mirror 0x140: lane i <- lane i^15 (in 16-lane rows)
+//   row_shr:n 0x110+n, row_bcast:15 0x142, row_bcast:31 0x143
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xf, 0xf, false));
+}
+// lane i <- lane i ^ M
+template <int M>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+  if constexpr (M == 1) return dpp_mov<0xB1>(v);
+  else if constexpr (M == 2) return dpp_mov<0x4E>(v);
+  else if constexpr (M == 4) return dpp_mov<0x1B>(dpp_mov<0x141>(v));  // (i^7)^3
+  else if constexpr (M == 8) return dpp_mov<0x141>(dpp_mov<0x140>(v)); // (i^15)^7
+  else return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), M, 64));
+}
+template <int M>
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t v) {
+  const uint32_t lo = lane_xor<M>(static_cast<uint32_t>(v));
+  const uint32_t hi = lane_xor<M>(static_cast<uint32_t>(v >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+// Whole-wave min / max, result in every lane: DPP partial reductions inside
+// 16-lane rows, row broadcasts into lane 63, then readlane.
+template <bool kMax>
+__device__ __forceinline__ int wave_reduce_minmax(int v) {
+  const int id = kMax ? INT32_MIN : INT32_MAX;
+  auto op = [](int a, int b) { return kMax ? (a > b ? a : b) : (a < b ? a : b); };
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x111, 0xf, 0xf, false));
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x112, 0xf, 0xf, false));
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x114, 0xf, 0xf, false));
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x118, 0xf, 0xf, false));
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x142, 0xa, 0xf, false));
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x143, 0xc, 0xf, false));
+  return __builtin_amdgcn_readlane(v, 63);
 }
 
 // Reductions across the four lane groups that share a column of a 16x16

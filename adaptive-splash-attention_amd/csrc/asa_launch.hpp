@@ -24,8 +24,8 @@ struct SelectParams {
   uint8_t* mask;
   int32_t* topk_idx;      // optional
   float* topk_val;        // optional
-  uint64_t* cand;         // workspace: [BH, NQ, cap] candidate keys
-  int cap;                // select_capacity(k)
+  float* tkv;             // workspace: sorted top-k values, [k][BH * NQ]
+  int cap;                // candidate keys per row in LDS (select_capacity)
 };
 
 struct CompactParams {
@@ -76,8 +76,12 @@ struct BackwardParams {
 // Each launcher returns the launch status; `name` receives the kernel's
 // name for the profiler.
 hipError_t launch_select(const SelectParams& p, bool bf16, bool from_scores, hipStream_t s);
-size_t select_lds_bytes(const Dims& d);
-int select_capacity(int k);
+// LDS bytes of one select block holding `cap` candidate keys per row.
+size_t select_lds_bytes(const Dims& d, bool bf16, bool from_scores, int cap);
+// Candidate keys per row that fit `max_lds` bytes (k + 32 at most; -1 if
+// not even k + 8 fit).
+int select_capacity(const Dims& d, bool bf16, bool from_scores, size_t max_lds);
+hipError_t launch_tau(const SelectParams& p, hipStream_t s);
 hipError_t launch_compact(const CompactParams& p, hipStream_t s);
 hipError_t launch_forward(const ForwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_delta(const BackwardParams& p, bool bf16, hipStream_t s);

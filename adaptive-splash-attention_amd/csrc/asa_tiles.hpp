@@ -147,14 +147,15 @@ __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const float* rm
     }
 }
 
-// Exponent classes of the two per-score powers, chosen from alpha:
-//   p = u^(1/(alpha-1)) and w = u^((2-alpha)/(alpha-1)) = p^(2-alpha).
+// Exponent classes of the per-score powers, chosen from alpha:
+//   p = u^(1/(alpha-1)), w = u^((2-alpha)/(alpha-1)) = p^(2-alpha), and the
+//   tau recurrence's f'' terms u^((3-2 alpha)/(alpha-1)) (class V).
 enum AlphaClass : int { kA15 = 0, kA20 = 1, kA125 = 2, kAGen = 3 };
 template <int AC> struct AlphaPow;
-template <> struct AlphaPow<kA15> { static constexpr int P = kE2, W = kE1; };
-template <> struct AlphaPow<kA20> { static constexpr int P = kE1, W = kE0; };
-template <> struct AlphaPow<kA125> { static constexpr int P = kE4, W = kE3; };
-template <> struct AlphaPow<kAGen> { static constexpr int P = kEGen, W = kEGen; };
+template <> struct AlphaPow<kA15> { static constexpr int P = kE2, W = kE1, V = kE0; };
+template <> struct AlphaPow<kA20> { static constexpr int P = kE1, W = kE0, V = kEM1; };
+template <> struct AlphaPow<kA125> { static constexpr int P = kE4, W = kE3, V = kE2; };
+template <> struct AlphaPow<kAGen> { static constexpr int P = kEGen, W = kEGen, V = kEGen; };
 
 __host__ __device__ inline int alpha_class_of(float alpha) {
   const float am1 = alpha - 1.0f;

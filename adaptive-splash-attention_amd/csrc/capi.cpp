@@ -104,8 +104,8 @@ void sizes_of(const Shape& s, asa_sizes* z) {
   z->k_list = blocks * sizeof(int32_t);
   z->topk_idx = rows * s.k * sizeof(int32_t);
   z->topk_val = rows * s.k * sizeof(float);
-  // forward: candidate keys of the score pass; backward: two floats per row
-  const size_t fwd_ws = rows * size_t(asa::select_capacity(s.k)) * sizeof(uint64_t);
+  // forward: the rows' sorted top-k values; backward: two floats per row
+  const size_t fwd_ws = rows * size_t(s.k) * sizeof(float);
   const size_t bwd_ws = 2 * rows * sizeof(float);
   z->workspace = fwd_ws > bwd_ws ? fwd_ws : bwd_ws;
 }
@@ -120,17 +120,20 @@ int check_state(const asa_state* st, bool need_norms) {
   return ASA_OK;
 }
 
-int check_select_lds(const Shape& s) {
+// Candidate capacity per row of the select kernel on the current device
+// (*cap), or an error when even the smallest capacity does not fit its LDS.
+int select_cap(const Shape& s, bool from_scores, int* cap) {
   int dev = 0, max_lds = 0;
   if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
   if (int rc = check_hip(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock,
                                                dev),
                          "hipDeviceGetAttribute"))
     return rc;
-  const size_t need = asa::select_lds_bytes(dims_of(s));
-  if (need > size_t(max_lds))
+  const asa::Dims d = dims_of(s);
+  *cap = asa::select_capacity(d, s.bf16, from_scores, size_t(max_lds));
+  if (*cap < 0)
     return fail(ASA_ERR_UNSUPPORTED, "k_keep %d needs %zu bytes of LDS per block, device has %d",
-                s.k, need, max_lds);
+                s.k, asa::select_lds_bytes(d, s.bf16, from_scores, s.k + 8), max_lds);
   return ASA_OK;
 }
 
@@ -153,8 +156,8 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
                const int32_t* q_idx, const int32_t* k_idx, const asa_state* st, void* workspace,
                hipStream_t s) {
   asa::SelectParams sp{};
-  sp.cand = static_cast<uint64_t*>(workspace);
-  sp.cap = asa::select_capacity(sh.k);
+  sp.tkv = static_cast<float*>(workspace);
+  if (int rc = select_cap(sh, scores != nullptr, &sp.cap)) return rc;
   sp.d = dims_of(sh);
   sp.q = q;
   sp.k = k;
@@ -169,6 +172,10 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
   hipError_t e = asa::launch_select(sp, sh.bf16, scores != nullptr, s);
   asa::profile_end(s);
   if (int rc = check_hip(e, "select kernel launch")) return rc;
+  asa::profile_begin("tau", s);
+  e = asa::launch_tau(sp, s);
+  asa::profile_end(s);
+  if (int rc = check_hip(e, "tau kernel launch")) return rc;
 
   asa::CompactParams cp{sh.BH, sh.nQB, sh.nKB, st->mask, st->q_ptr, st->q_list, st->k_ptr,
                         st->k_list};
@@ -237,7 +244,6 @@ int asa_forward(const asa_problem* p, const void* q, const void* k, const void* 
     return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
   if (int rc = check_state(st, true)) return rc;
   if (!workspace) return fail(ASA_ERR_INVALID_ARGUMENT, "workspace is NULL");
-  if (int rc = check_select_lds(sh)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (int rc = run_select(sh, q, k, nullptr, q_idx, k_idx, st, workspace, s)) return rc;
@@ -325,7 +331,6 @@ int asa_select_from_scores(const asa_problem* p, const float* scores, const int3
     return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
   if (int rc = check_state(st, false)) return rc;
   if (!workspace) return fail(ASA_ERR_INVALID_ARGUMENT, "workspace is NULL");
-  if (int rc = check_select_lds(sh)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (int rc = run_select(sh, nullptr, nullptr, scores, q_idx, k_idx, st, workspace, s)) return rc;
   return ok();

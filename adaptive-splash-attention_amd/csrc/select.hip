@@ -2,10 +2,12 @@
 //
 // Reference: build_mask_kernel + insert_topk + entmax_threshold
 // (adasplashattention.cu:35-217), one thread per query that scans every key
-// and keeps a sorted top-k by insertion.  Here one block owns one 64-row
-// query block of one (batch, head); each wave owns 16*QF of its rows and
-// forms S^T = K Q^T tiles on MFMA (K fragments straight from global memory,
-// Q^T fragments in registers).  The top-k is found in two sweeps over the
+// and keeps a sorted top-k by insertion.  Here one 256-thread block owns one
+// 64-row query block of one (batch, head); wave w owns rows 16w..16w+15 and
+// forms S^T = K Q^T tiles on MFMA.  The K tiles of the visible key blocks
+// stream through a double-buffered LDS stage shared by the four waves (each
+// thread prefetches its share of the next tile into registers while the
+// current one is multiplied).  The top-k is found in two sweeps over the
 // visible key blocks instead of by insertion:
 //
 //   sweep 1  every score updates one of 64*R running "class maxima" of its
@@ -14,17 +16,17 @@
 //            >= x, and every top-k key scores >= x.  A short bisection per
 //            row finds such an x close to the k-th largest class maximum.
 //   sweep 2  the scores are recomputed and every key scoring >= x is
-//            appended, as a 64-bit (score, ~index) key, to the row's slice of
-//            a candidate buffer in the workspace (about 1.2-1.4 k keys per row
-//            on random data).  If a row overflows its slice, the k-th best
-//            stored key becomes an exact key threshold and the sweep repeats
-//            for that row; the threshold rises strictly, so this ends.
+//            appended, as a 64-bit (score, ~index) key, to the row's list in
+//            LDS (about 1.05-1.15 k keys per row on random data).  If a row
+//            overflows its list, the k-th best stored key becomes an exact
+//            key threshold and the block sweeps again for those rows; the
+//            threshold rises strictly, so this ends.
 //   select   each row's candidates are sorted (segmented bitonic sort across
 //            lanes, descending key order = score desc, index asc); the first
 //            k are the reference's top-k, padded with the empty slot
 //            (score -1e6, index -1).
-//   finish   the tau recurrence runs per row on the sorted values, the row's
-//            top-k key blocks are OR-ed into the block's mask bitmap.
+//   finish   the rows' top-k key blocks are OR-ed into the block's mask
+//            bitmap; one wave runs the tau recurrence, one lane per row.
 //
 // Sweep filters compare raw dot products (scale > 0) against a threshold
 // widened by a relative margin, so that no key whose clamped, scaled score
@@ -36,20 +38,15 @@
 
 #include "asa_device.hpp"
 #include "asa_launch.hpp"
+#include "asa_tiles.hpp"
 
 namespace asa {
 namespace {
 
-constexpr int kStride = 68;  // floats per staged row (16-byte aligned)
+constexpr int kThreads = 256;  // four waves of 16 query rows
 
-__device__ __forceinline__ int wave_min(int v) {
-  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, kWave));
-  return v;
-}
-__device__ __forceinline__ int wave_max(int v) {
-  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
-  return v;
-}
+__device__ __forceinline__ int wave_min(int v) { return wave_reduce_minmax<false>(v); }
+__device__ __forceinline__ int wave_max(int v) { return wave_reduce_minmax<true>(v); }
 // Reductions over the 4 lanes (L, L^16, L^32, L^48) that share a row.
 __device__ __forceinline__ int group_sum(int v) {
   v += __shfl_xor(v, 16, kWave);
@@ -87,25 +84,32 @@ __device__ __forceinline__ uint32_t count_ge(uint32_t c, float x, float t) {
       : "vcc");
   return c;
 }
-__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
-  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m, kWave);
-  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m, kWave);
-  return (static_cast<uint64_t>(hi) << 32) | lo;
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
 }
+
+constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x / 2); }
 
 // Descending bitonic sort of independent segments of 8*LS keys: lanes
 // [s*LS, (s+1)*LS) hold segment s, element e = (lane % LS) * 8 + p in v[p].
-// Keys are distinct except for the padding value 0.
+// Keys are distinct except for the padding value 0.  Exchanges between
+// lanes use DPP moves for lane distances below 16.
 template <int LS>
 __device__ __forceinline__ void segment_sort_desc(uint64_t (&v)[8], int lane) {
   const int i = lane & (LS - 1);
-  for (int size = 2; size <= 8 * LS; size <<= 1) {
-    for (int j = size >> 1; j > 0; j >>= 1) {
-      if (j >= 8) {
+  static_for<1, ilog2(8 * LS) + 1>([&](auto sc) {
+    constexpr int size = 1 << decltype(sc)::value;
+    static_for<0, decltype(sc)::value>([&](auto jc) {
+      constexpr int j = (size >> 1) >> decltype(jc)::value;
+      if constexpr (j >= 8) {
         const bool lower = (i & (j >> 3)) == 0;  // e & j depends on the lane only
         for (int p = 0; p < 8; ++p) {
           const int e = i * 8 + p;
-          const uint64_t o = shfl_xor64(v[p], j >> 3);
+          const uint64_t o = lane_xor64<(j >> 3)>(v[p]);
           const bool keep_max = ((e & size) == 0) == lower;
           const bool gt = v[p] > o;
           v[p] = (keep_max == gt) ? v[p] : o;
@@ -122,11 +126,11 @@ __device__ __forceinline__ void segment_sort_desc(uint64_t (&v)[8], int lane) {
           }
         }
       }
-    }
-  }
+    });
+  });
 }
 
-// tau from the sorted top-k values of one row, tk[j * 64 + lq] (best first),
+// tau from the sorted top-k values of one row, tk[j * stride + lq] (best first),
 // following the reference recurrence step by step
 // (adasplashattention.cu:51-125): bracket from the extreme kept values,
 // midpoint start, up to five rounds of {f, f', f'' over the leading positive
@@ -136,8 +140,10 @@ __device__ __forceinline__ void segment_sort_desc(uint64_t (&v)[8], int lane) {
 // powers via pow_exact: bit-identical to the CPU oracle on equal inputs.
 // The sorted values are read four at a time so that one LDS round trip
 // serves four terms.
-__device__ float entmax_tau(const float* tk, int lq, int k, float alpha_in) {
+template <int AC>
+__device__ float entmax_tau(const float* tk, size_t stride, size_t lq, int k, float alpha_in) {
 #pragma clang fp contract(off)
+  constexpr int PA = AlphaPow<AC>::P, P1 = AlphaPow<AC>::W, P2 = AlphaPow<AC>::V;
   const float alpha = fmaxf(1.05f, fminf(alpha_in, 3.0f));
   const float am1 = alpha - 1.0f;
   const float a = 1.0f / am1;
@@ -145,7 +151,7 @@ __device__ float entmax_tau(const float* tk, int lq, int k, float alpha_in) {
   const float e2 = (3.0f - 2.0f * alpha) * a;
   const float c2 = a * ((a + 1.0f) - alpha);
   const float top = tk[lq];
-  const float bottom = tk[(k - 1) * kWave + lq];
+  const float bottom = tk[size_t(k - 1) * stride + lq];
   float lo = am1 * bottom - 2.0f;
   float hi = am1 * top + 2.0f;
   float tau = 0.5f * (lo + hi);
@@ -154,19 +160,19 @@ __device__ float entmax_tau(const float* tk, int lq, int k, float alpha_in) {
     float buf[4];
     for (int j = 0; j < k; ++j) {
       if ((j & 3) == 0)
-        for (int i = 0; i < 4; ++i) buf[i] = tk[min(j + i, k - 1) * kWave + lq];
+        for (int i = 0; i < 4; ++i) buf[i] = tk[size_t(min(j + i, k - 1)) * stride + lq];
       float sj = buf[0];
       for (int i = 1; i < 4; ++i)
         if (i == (j & 3)) sj = buf[i];
       const float u = am1 * sj - tau;
       if (u <= 0.0f) break;
       const float ue = fmaxf(u, kEps);
-      float t = pow_exact(ue, a);
+      float t = pow_exact_c<PA>(ue, a);
       if (!finite(t)) t = 0.0f;
       f = f + t;
-      const float t1 = -a * pow_exact(ue, e1);
+      const float t1 = -a * pow_exact_c<P1>(ue, e1);
       if (finite(t1)) df = df + t1;
-      const float t2 = c2 * pow_exact(ue, e2);
+      const float t2 = c2 * pow_exact_c<P2>(ue, e2);
       if (finite(t2)) d2f = d2f + t2;
     }
     if (fabsf(f) < 1e-4f) break;
@@ -179,13 +185,13 @@ __device__ float entmax_tau(const float* tk, int lq, int k, float alpha_in) {
     float gsum = -1.0f;
     for (int j = 0; j < k; ++j) {
       if ((j & 3) == 0)
-        for (int i = 0; i < 4; ++i) buf[i] = tk[min(j + i, k - 1) * kWave + lq];
+        for (int i = 0; i < 4; ++i) buf[i] = tk[size_t(min(j + i, k - 1)) * stride + lq];
       float sj = buf[0];
       for (int i = 1; i < 4; ++i)
         if (i == (j & 3)) sj = buf[i];
       const float u = am1 * sj - next;
       if (u <= 0.0f) break;
-      const float t = pow_exact(fmaxf(u, kEps), a);
+      const float t = pow_exact_c<PA>(fmaxf(u, kEps), a);
       if (finite(t)) gsum = gsum + t;
     }
     if (gsum > 0.0f) lo = next;
@@ -211,86 +217,92 @@ __device__ __forceinline__ float sweep_floor(float th, bool exact, float scale) 
   return f;
 }
 
-// Q^T operand fragments of QF 16-row groups.
-template <typename T, int D, int QF> struct QFrags;
-template <int D, int QF> struct QFrags<u16, D, QF> {
-  bf16x8 v[QF][D / 32];
-  __device__ void load(const u16* Q, int row0, int NQ, int lane) {
-    const int g = lane >> 4, c = lane & 15;
-    for (int m = 0; m < QF; ++m) {
-      const int row = row0 + 16 * m + c;
-      for (int s = 0; s < D / 32; ++s)
-        v[m][s] = row < NQ ? *reinterpret_cast<const bf16x8*>(Q + size_t(row) * D + 32 * s + 8 * g)
-                           : bf16x8{};
+
+// K tile of 64 keys in LDS: row-major with a padded row stride, filled by
+// all 256 threads in 16-byte chunks (consecutive threads, consecutive
+// chunks of a row: coalesced global reads).
+template <typename T, int D> struct KStage {
+  static constexpr int kRs = sizeof(T) == 2 ? D + 8 : D + 4;   // elements per LDS row
+  static constexpr int kRowChunks = D * int(sizeof(T)) / 16;    // 16-byte chunks per row
+  static constexpr int kPerThread = kBlock * kRowChunks / kThreads;
+  static_assert(kBlock * kRowChunks % kThreads == 0, "tile chunks must divide the block");
+  uint4 r[kPerThread];
+  // rows >= NK read as zero (such keys are never visible)
+  __device__ __forceinline__ void load(const T* Kb, int kbase, int NK, int t) {
+    for (int j = 0; j < kPerThread; ++j) {
+      const int ch = t + j * kThreads, row = ch / kRowChunks;
+      const int col = (ch % kRowChunks) * (16 / int(sizeof(T)));
+      r[j] = kbase + row < NK
+                 ? *reinterpret_cast<const uint4*>(Kb + size_t(kbase + row) * D + col)
+                 : uint4{0u, 0u, 0u, 0u};
     }
   }
-};
-template <int D, int QF> struct QFrags<float, D, QF> {
-  f32x4 v[QF][D / 16];
-  __device__ void load(const float* Q, int row0, int NQ, int lane) {
-    const int g = lane >> 4, c = lane & 15;
-    for (int m = 0; m < QF; ++m) {
-      const int row = row0 + 16 * m + c;
-      for (int j = 0; j < D / 16; ++j)
-        v[m][j] = row < NQ ? *reinterpret_cast<const f32x4*>(Q + size_t(row) * D + 16 * j + 4 * g)
-                           : f32x4{};
+  __device__ __forceinline__ void store(T* buf, int t) const {
+    for (int j = 0; j < kPerThread; ++j) {
+      const int ch = t + j * kThreads, row = ch / kRowChunks;
+      const int col = (ch % kRowChunks) * (16 / int(sizeof(T)));
+      *reinterpret_cast<uint4*>(buf + row * kRs + col) = r[j];
     }
   }
 };
 
-// K^T operand fragments of one 64-key block (4 groups of 16 keys).
-template <typename T, int D> struct KFrags;
-template <int D> struct KFrags<u16, D> {
-  bf16x8 v[4][D / 32];
-  __device__ void load(const u16* K, int kbase, int NK, int lane) {
-    const int g = lane >> 4, c = lane & 15;
-    for (int f = 0; f < 4; ++f) {
-      const int row = min(kbase + 16 * f + c, NK - 1);
-      for (int s = 0; s < D / 32; ++s)
-        v[f][s] = *reinterpret_cast<const bf16x8*>(K + size_t(row) * D + 32 * s + 8 * g);
-    }
+// Q^T operand fragment of the lane's query row (column c of the products).
+template <typename T, int D> struct QFrag;
+template <int D> struct QFrag<u16, D> {
+  bf16x8 v[D / 32];
+  __device__ void load(const u16* row, bool ok, int g) {
+    for (int s = 0; s < D / 32; ++s)
+      v[s] = ok ? *reinterpret_cast<const bf16x8*>(row + 32 * s + 8 * g) : bf16x8{};
   }
 };
-template <int D> struct KFrags<float, D> {
-  f32x4 v[4][D / 16];
-  __device__ void load(const float* K, int kbase, int NK, int lane) {
-    const int g = lane >> 4, c = lane & 15;
-    for (int f = 0; f < 4; ++f) {
-      const int row = min(kbase + 16 * f + c, NK - 1);
-      for (int j = 0; j < D / 16; ++j)
-        v[f][j] = *reinterpret_cast<const f32x4*>(K + size_t(row) * D + 16 * j + 4 * g);
-    }
+template <int D> struct QFrag<float, D> {
+  f32x4 v[D / 16];
+  __device__ void load(const float* row, bool ok, int g) {
+    for (int j = 0; j < D / 16; ++j)
+      v[j] = ok ? *reinterpret_cast<const f32x4*>(row + 16 * j + 4 * g) : f32x4{};
   }
 };
 
-template <int D, int QF>
-__device__ __forceinline__ void mma(f32x4 (&acc)[4][QF], const KFrags<u16, D>& kf,
-                                    const QFrags<u16, D, QF>& qf) {
-  for (int f = 0; f < 4; ++f)
-    for (int m = 0; m < QF; ++m) acc[f][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+// acc[f] = S^T block of keys 16f.. x the wave's 16 rows, from the LDS tile.
+// Same operands and accumulation order as the attention passes' score
+// products, so every pass sees bit-identical scores.
+template <int D>
+__device__ __forceinline__ void tile_scores(f32x4 (&acc)[4], const u16* buf, const QFrag<u16, D>& q,
+                                            int g, int c) {
+  constexpr int rs = KStage<u16, D>::kRs;
+  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < D / 32; ++s)
-    for (int f = 0; f < 4; ++f)
-      for (int m = 0; m < QF; ++m) acc[f][m] = mfma(kf.v[f][s], qf.v[m][s], acc[f][m]);
+    for (int f = 0; f < 4; ++f) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(buf + (16 * f + c) * rs + 32 * s + 8 * g);
+      acc[f] = mfma(a, q.v[s], acc[f]);
+    }
 }
-template <int D, int QF>
-__device__ __forceinline__ void mma(f32x4 (&acc)[4][QF], const KFrags<float, D>& kf,
-                                    const QFrags<float, D, QF>& qf) {
-  for (int f = 0; f < 4; ++f)
-    for (int m = 0; m < QF; ++m) acc[f][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+template <int D>
+__device__ __forceinline__ void tile_scores(f32x4 (&acc)[4], const float* buf,
+                                            const QFrag<float, D>& q, int g, int c) {
+  constexpr int rs = KStage<float, D>::kRs;
+  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < D / 16; ++j)
-    for (int r = 0; r < 4; ++r)
-      for (int f = 0; f < 4; ++f)
-        for (int m = 0; m < QF; ++m) acc[f][m] = mfma(kf.v[f][j][r], qf.v[m][j][r], acc[f][m]);
+    for (int f = 0; f < 4; ++f) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(buf + (16 * f + c) * rs + 16 * j + 4 * g);
+      for (int r = 0; r < 4; ++r) acc[f] = mfma(a[r], q.v[j][r], acc[f]);
+    }
 }
 
-struct Lds {
-  float* stage;    // [64][kStride]   staged sweep values, row = local query
-  float* tk;       // [k][64]         sorted top-k scores, slot-major
-  uint64_t* tkey;  // [64]            exact key threshold of an overflow round
-  uint32_t* cnt;   // [64]            candidates appended per row
-  uint32_t* bits;  // [ceil(nKB/32)]  block mask of the query block
-  uint8_t* kvis;   // [nKB]           visibility class of every key block
-};
+// acc[b >> 2][b & 3] for a per-lane index b in [0, 16): a select tree on
+// the index bits instead of a dynamically indexed register array.
+__device__ __forceinline__ float pick16(const f32x4 (&acc)[4], int b) {
+  const bool b2 = (b & 4) != 0, b3 = (b & 8) != 0;
+  f32x4 x;
+  for (int r = 0; r < 4; ++r) {
+    const float lo = b2 ? acc[1][r] : acc[0][r];
+    const float hi = b2 ? acc[3][r] : acc[2][r];
+    x[r] = b3 ? hi : lo;
+  }
+  const float y0 = (b & 1) ? x[1] : x[0];
+  const float y1 = (b & 1) ? x[3] : x[2];
+  return (b & 2) ? y1 : y0;
+}
 
 enum SweepMode : int {
   kRawDots = 0,     // MFMA dot products, scale > 0: filters on raw dots
@@ -298,61 +310,76 @@ enum SweepMode : int {
   kGivenScores = 2  // caller-given scores
 };
 
-template <typename T, int D, int QF, int MODE>
-__global__ __launch_bounds__(kWave * (4 / QF)) void select_kernel(SelectParams p) {
-  constexpr int NW = 4 / QF;   // waves per block
-  constexpr int R = NW;        // class sets per (lane, row, slot): 64 R classes per row
-  constexpr int QW = 16 * QF;  // rows per wave
-  constexpr int NB = 16 * QF;  // sweep values per lane per key block
+// LDS layout, shared by the kernel and the host-side size query.
+struct SelLayout {
+  int tiles, tk, cand, tkey, cnt, ctl, bits, vlist, kvis, total;
+};
+__host__ __device__ inline int align_up(int x, int a) { return (x + a - 1) / a * a; }
+__host__ __device__ inline SelLayout sel_layout(int k, int cap, int nKB, int D, int tbytes,
+                                                bool given_scores) {
+  SelLayout l;
+  const int rs = tbytes == 2 ? D + 8 : D + 4;
+  const int tiles = given_scores ? 0 : 2 * kBlock * rs * tbytes;
+  const int tk = k * kWave * 4;
+  // the sorted top-k values reuse the tile buffers once the sweeps are over
+  const int a = align_up(tiles > tk ? tiles : tk, 16);
+  l.tiles = 0;
+  l.tk = 0;
+  l.cand = a;
+  l.tkey = l.cand + kBlock * cap * 8;
+  l.cnt = l.tkey + kBlock * 8;
+  l.ctl = l.cnt + kBlock * 4;
+  l.bits = l.ctl + 16;
+  l.vlist = l.bits + align_up((nKB + 31) / 32 * 4, 16);
+  l.kvis = l.vlist + align_up(nKB * 4, 16);
+  l.total = align_up(l.kvis + nKB, 16);
+  return l;
+}
+
+template <typename T, int D, int MODE, int R>
+__global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
   constexpr bool kExact = MODE != kRawDots;
-  static_assert(NB <= 32, "candidate masks are 32-bit");
+  constexpr bool kTiles = MODE != kGivenScores;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int k = p.d.k, NQ = p.d.NQ, NK = p.d.NK, nKB = p.d.nKB, nQB = p.d.nQB;
   const int cap = p.cap;
   const int nbw = (nKB + 31) >> 5;
-  Lds s;
-  s.stage = reinterpret_cast<float*>(smem);
-  s.tk = s.stage + kBlock * kStride;
-  s.tkey = reinterpret_cast<uint64_t*>(s.tk + size_t(k) * kWave);
-  s.cnt = reinterpret_cast<uint32_t*>(s.tkey + kBlock);
-  s.bits = s.cnt + kBlock;
-  s.kvis = reinterpret_cast<uint8_t*>(s.bits + nbw);
+  const SelLayout lay = sel_layout(k, cap, nKB, D, int(sizeof(T)), !kTiles);
+  T* s_tiles = reinterpret_cast<T*>(smem + lay.tiles);
+  float* s_tk = reinterpret_cast<float*>(smem + lay.tk);
+  uint64_t* s_cand = reinterpret_cast<uint64_t*>(smem + lay.cand);
+  uint64_t* s_tkey = reinterpret_cast<uint64_t*>(smem + lay.tkey);
+  uint32_t* s_cnt = reinterpret_cast<uint32_t*>(smem + lay.cnt);
+  uint32_t* s_ctl = reinterpret_cast<uint32_t*>(smem + lay.ctl);
+  uint32_t* s_bits = reinterpret_cast<uint32_t*>(smem + lay.bits);
+  int32_t* s_vlist = reinterpret_cast<int32_t*>(smem + lay.vlist);
+  uint8_t* s_kvis = smem + lay.kvis;
+  constexpr int kTileElems = kBlock * KStage<T, D>::kRs;
 
-  const int t = threadIdx.x, w = t >> 6, L = t & 63, g = L >> 4, c16 = L & 15;
+  const int t = threadIdx.x, w = t >> 6, L = t & 63, g = L >> 4, c = L & 15;
   const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
   const int qb = task % nQB, bh = task / nQB, q0 = qb * kBlock;
-  const int qw0 = w * QW;  // first local row of this wave
+  const int lq = 16 * w + c;  // this lane's row within the block
+  const bool rowok = q0 + lq < NQ;
+  const size_t grow = size_t(bh) * NQ + q0 + lq;  // global row (valid if rowok)
+  const int qpos = rowok ? p.q_idx[grow] : 0;
   const float scale = p.d.scale;
 
-  // Rows of this lane in the accumulator layout: local row qw0 + 16m + c16.
-  int qid[QF];
-  uint32_t rowbits = 0;  // bits of the sweep values that belong to valid rows
-  for (int m = 0; m < QF; ++m) {
-    const int qq = q0 + qw0 + 16 * m + c16;
-    const bool ok = qq < NQ;
-    qid[m] = ok ? p.q_idx[size_t(bh) * NQ + qq] : 0;
-    if (ok) rowbits |= 0xffffu << (16 * m);
-  }
-  // Position range of the valid rows of the whole query block.
+  // Position range of the valid rows of the whole block (lane L <-> row L).
   const bool lv = q0 + L < NQ;
   const int lpos = lv ? p.q_idx[size_t(bh) * NQ + q0 + L] : 0;
   const int qmax_blk = wave_max(lv ? lpos : INT_MIN);
   const int qmin_blk = wave_min(lv ? lpos : INT_MAX);
 
-  if (t < kBlock) s.cnt[t] = 0u;
-  for (int i = t; i < nbw; i += kWave * NW) s.bits[i] = 0u;
+  if (t < kBlock) s_cnt[t] = 0u;
+  if (t < 4) s_ctl[t] = 0u;
+  for (int i = t; i < nbw; i += kThreads) s_bits[i] = 0u;
 
-  QFrags<T, D, QF> qf;
-  const T* Kb = nullptr;
-  if constexpr (MODE != kGivenScores) {
-    qf.load(static_cast<const T*>(p.q) + size_t(bh) * NQ * D, q0 + qw0, NQ, L);
-    Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
-  }
   const int32_t* kidx = p.k_idx + size_t(bh) * NK;
   // Visibility class of every key block: 0 no key visible to any row of the
-  // query block, 1 partially visible, 2 every key visible to every row.
-  // Four blocks per wave per step keep four loads in flight.
-  for (int kt0 = 4 * w; kt0 < nKB; kt0 += 4 * NW) {
+  // block, 1 partially visible, 2 every key visible to every row.  Four
+  // blocks per wave step keep four loads in flight.
+  for (int kt0 = 4 * w; kt0 < nKB; kt0 += 16) {
     int kid[4];
     bool kin[4];
     for (int j = 0; j < 4; ++j) {
@@ -365,82 +392,123 @@ __global__ __launch_bounds__(kWave * (4 / QF)) void select_kernel(SelectParams p
       const int kmin = wave_min(kin[j] ? kid[j] : INT_MAX);
       const int kmax = wave_max(kin[j] ? kid[j] : INT_MIN);
       if (kt < nKB && L == 0)
-        s.kvis[kt] = kmin > qmax_blk ? 0 : ((kmax > qmin_blk || (kt + 1) * kBlock > NK) ? 1 : 2);
+        s_kvis[kt] = kmin > qmax_blk ? 0 : ((kmax > qmin_blk || (kt + 1) * kBlock > NK) ? 1 : 2);
     }
   }
   __syncthreads();
+  // Visible key blocks in ascending order: entry = block | class << 24.
+  if (w == 0) {
+    int n = 0;
+    for (int base = 0; base < nKB; base += kWave) {
+      const int kt = base + L;
+      const int v = kt < nKB ? s_kvis[kt] : 0;
+      const uint64_t m = __ballot(v != 0);
+      const int before = __builtin_popcountll(m & ((uint64_t(1) << L) - 1));
+      if (v != 0) s_vlist[n + before] = kt | (v << 24);
+      n += __builtin_popcountll(m);
+    }
+    if (L == 0) s_ctl[1] = uint32_t(n);
+  }
+  __syncthreads();
+  const int nvis = int(s_ctl[1]);
 
-  // Sweep values of key block kt in the accumulator layout (bit 16m+4f+r of
-  // the returned mask set where the value is visible to its valid row;
-  // invisible values are set to -inf).
-  KFrags<T, D> kf;
-  auto sweep_values = [&](int kt, int vis, f32x4 (&acc)[4][QF]) -> uint32_t {
+  QFrag<T, D> qf;
+  const T* Kb = nullptr;
+  if constexpr (kTiles) {
+    qf.load(static_cast<const T*>(p.q) + grow * D, rowok, g);
+    Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
+  }
+  KStage<T, D> ks;
+
+  // Sweep values of one key block for the lane's row: acc[f][r] is the value
+  // of key 16f + 4g + r.  Bit 4f + r of the returned mask is set where that
+  // key is visible to a valid row; invisible values are set to -inf.
+  auto sweep_values = [&](const T* buf, int kt, int vis, f32x4 (&acc)[4]) -> uint32_t {
     const int kbase = kt * kBlock;
     if constexpr (MODE == kGivenScores) {
       for (int f = 0; f < 4; ++f)
-        for (int m = 0; m < QF; ++m)
-          for (int r = 0; r < 4; ++r) {
-            const int key = kbase + 16 * f + 4 * g + r;
-            const size_t row = size_t(bh) * NQ + q0 + qw0 + 16 * m + c16;
-            acc[f][m][r] = ((rowbits >> (16 * m)) & 1u) && key < NK
-                               ? clamp_score(p.scores[row * NK + key]) : 0.0f;
-          }
+        for (int r = 0; r < 4; ++r) {
+          const int key = kbase + 16 * f + 4 * g + r;
+          acc[f][r] = rowok && key < NK ? clamp_score(p.scores[grow * NK + key]) : 0.0f;
+        }
     } else {
-      mma<D, QF>(acc, kf, qf);
+      tile_scores<D>(acc, buf, qf, g, c);
       if constexpr (MODE == kExactScores)
         for (int f = 0; f < 4; ++f)
-          for (int m = 0; m < QF; ++m)
-            for (int r = 0; r < 4; ++r) acc[f][m][r] = clamp_score(acc[f][m][r] * scale);
+          for (int r = 0; r < 4; ++r) acc[f][r] = clamp_score(acc[f][r] * scale);
     }
-    uint32_t vb = rowbits;
+    uint32_t vb = rowok ? 0xffffu : 0u;
     if (vis == 1) {
       for (int f = 0; f < 4; ++f)
         for (int r = 0; r < 4; ++r) {
           const int key = kbase + 16 * f + 4 * g + r;
           const int kp = key < NK ? kidx[key] : INT_MAX;
-          for (int m = 0; m < QF; ++m)
-            if (!(key < NK && kp <= qid[m])) {
-              vb &= ~(1u << (16 * m + 4 * f + r));
-              acc[f][m][r] = -__builtin_inff();
-            }
+          if (!(key < NK && kp <= qpos)) {
+            vb &= ~(1u << (4 * f + r));
+            acc[f][r] = -__builtin_inff();
+          }
         }
     }
     return vb;
   };
 
-  // ---------------- sweep 1: class maxima ----------------
-  float cm[QF][16][R];
-  for (int m = 0; m < QF; ++m)
-    for (int i = 0; i < 16; ++i)
-      for (int c = 0; c < R; ++c) cm[m][i][c] = -__builtin_inff();
-  if constexpr (MODE != kGivenScores) kf.load(Kb, 0, NK, L);
-  for (int kt0 = 0; kt0 < nKB; kt0 += R) {
-    for (int c = 0; c < R; ++c) {
-      const int kt = kt0 + c;
-      if (kt >= nKB) break;
-      const int vis = s.kvis[kt];
-      if (vis == 0) {
-        if constexpr (MODE != kGivenScores) kf.load(Kb, (kt + 1) * kBlock, NK, L);
-        continue;
+  // One pass over the visible key blocks: body(u, kt, vb, acc) for each, with
+  // u = (ordinal of the block) % U known at compile time.  The next tile is
+  // stored to the other LDS buffer and the one after it fetched into
+  // registers while the current tile is in use.
+  auto sweep = [&](auto u_tag, auto&& body) {
+    constexpr int U = decltype(u_tag)::value;
+    if constexpr (kTiles) {
+      if (nvis > 0) {
+        ks.load(Kb, (s_vlist[0] & 0xffffff) * kBlock, NK, t);
+        ks.store(s_tiles, t);
       }
-      f32x4 acc[4][QF];
-      sweep_values(kt, vis, acc);
-      if constexpr (MODE != kGivenScores) kf.load(Kb, (kt + 1) * kBlock, NK, L);
-      for (int m = 0; m < QF; ++m)
-        for (int f = 0; f < 4; ++f)
-          for (int r = 0; r < 4; ++r) cm[m][4 * f + r][c] = vmax(cm[m][4 * f + r][c], acc[f][m][r]);
+      if (nvis > 1) ks.load(Kb, (s_vlist[1] & 0xffffff) * kBlock, NK, t);
+      __syncthreads();
     }
-  }
+    for (int i0 = 0; i0 < nvis; i0 += U) {
+      static_for<0, U>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        const int i = i0 + u;
+        if (i < nvis) {
+          const int e = s_vlist[i];
+          const int kt = e & 0xffffff, vis = e >> 24;
+          const T* buf = s_tiles + (i & 1) * kTileElems;
+          f32x4 acc[4];
+          const uint32_t vb = sweep_values(buf, kt, vis, acc);
+          body(uc, kt, vb, acc);
+          if constexpr (kTiles) {
+            if (i + 1 < nvis) {
+              ks.store(s_tiles + ((i + 1) & 1) * kTileElems, t);
+              if (i + 2 < nvis) ks.load(Kb, (s_vlist[i + 2] & 0xffffff) * kBlock, NK, t);
+            }
+            __syncthreads();
+          }
+        }
+      });
+    }
+    __syncthreads();
+  };
+
+  // ---------------- sweep 1: class maxima ----------------
+  float cm[16][R];
+  for (int i = 0; i < 16; ++i)
+    for (int j = 0; j < R; ++j) cm[i][j] = -__builtin_inff();
+  sweep(std::integral_constant<int, R>{}, [&](auto uc, int, uint32_t, f32x4 (&acc)[4]) {
+    constexpr int u = decltype(uc)::value;
+    for (int f = 0; f < 4; ++f)
+      for (int r = 0; r < 4; ++r) cm[4 * f + r][u] = vmax(cm[4 * f + r][u], acc[f][r]);
+  });
 
   // Per row: a value x with at least k class maxima >= x (bisection between
   // the smallest and largest class maximum), then the sweep-2 floor.
-  float floor_m[QF];
-  for (int m = 0; m < QF; ++m) {
+  float floor_v;
+  {
     float lo = __builtin_inff(), hi = -__builtin_inff();
     uint32_t nfin = 0;
     for (int i = 0; i < 16; ++i)
-      for (int c = 0; c < R; ++c) {
-        const float v = cm[m][i][c];
+      for (int j = 0; j < R; ++j) {
+        const float v = cm[i][j];
         nfin = count_ge(nfin, v, -3.0e38f);
         if (v >= -3.0e38f) {
           lo = fminf(lo, v);
@@ -456,162 +524,121 @@ __global__ __launch_bounds__(kWave * (4 / QF)) void select_kernel(SelectParams p
         const float mid = 0.5f * (lo + hi);
         uint32_t cnt = 0;
         for (int i = 0; i < 16; ++i)
-          for (int c = 0; c < R; ++c) cnt = count_ge(cnt, cm[m][i][c], mid);
+          for (int j = 0; j < R; ++j) cnt = count_ge(cnt, cm[i][j], mid);
         if (group_sum(int(cnt)) >= k) lo = mid;
         else hi = mid;
       }
       x = lo;
     }
     const float th = kExact ? x : (x == -__builtin_inff() ? x : clamp_score(x * scale));
-    floor_m[m] = sweep_floor(th, kExact, scale);
+    floor_v = sweep_floor(th, kExact, scale);
   }
 
   // ---------------- sweep 2 (and overflow rounds): candidates ----------------
-  float* wstage = s.stage + qw0 * kStride;
-  const size_t cand_row0 = (size_t(bh) * NQ + q0) * cap;
-  // Round 0 takes every key at or above the row's floor.  A row whose count
-  // exceeds `cap` gets the k-th best of its stored keys as an exact key
-  // threshold and is swept again; the other rows are final.
+  uint64_t* my_cand = s_cand + size_t(lq) * cap;
+  bool take = rowok;  // this lane's row collects in the current round
+  uint64_t tkey = 0;  // exact key threshold of the row (rounds > 0)
   for (int round = 0;; ++round) {
-    uint32_t take = rowbits;
-    uint64_t tkey[QF];
-    for (int m = 0; m < QF; ++m) tkey[m] = 0;
-    if (round > 0) {
-      take = 0;
-      for (int m = 0; m < QF; ++m)
-        if (s.cnt[qw0 + 16 * m + c16] > uint32_t(cap)) take |= rowbits & (0xffffu << (16 * m));
-      if (!__any(take != 0)) break;
-      for (int lq = qw0; lq < qw0 + QW; ++lq) {
-        if (!(s.cnt[lq] > uint32_t(cap)) || q0 + lq >= NQ) continue;  // uniform
-        uint64_t v[8];
-        for (int pp = 0; pp < 8; ++pp) {
-          const int e = (L & 31) * 8 + pp;
-          v[pp] = e < cap ? p.cand[cand_row0 + size_t(lq) * cap + e] : 0ull;
-        }
-        segment_sort_desc<32>(v, L);
-        // element k-1 lives in lane (k-1)/8, slot (k-1)%8 (both halves agree)
-        const int src = (k - 1) >> 3, sp = (k - 1) & 7;
-        uint64_t mine = v[0];
-        for (int pp = 1; pp < 8; ++pp)
-          if (pp == sp) mine = v[pp];
-        const uint64_t th =
-            (static_cast<uint64_t>(__shfl(static_cast<uint32_t>(mine >> 32), src, kWave)) << 32) |
-            __shfl(static_cast<uint32_t>(mine), src, kWave);
-        if (L == 0) s.tkey[lq] = th;
-      }
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      for (int m = 0; m < QF; ++m)
-        if ((take >> (16 * m)) & 1u) {
-          tkey[m] = s.tkey[qw0 + 16 * m + c16];
-          floor_m[m] = sweep_floor(key_score(tkey[m]), kExact, scale);
-        }
-      __builtin_amdgcn_wave_barrier();
-      for (int m = 0; m < QF; ++m)
-        if (((take >> (16 * m)) & 1u) && g == 0) s.cnt[qw0 + 16 * m + c16] = 0u;
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-    }
-
-    if constexpr (MODE != kGivenScores) kf.load(Kb, 0, NK, L);
-    for (int kt = 0; kt < nKB; ++kt) {
-      const int vis = s.kvis[kt];
-      if (vis == 0) {
-        if constexpr (MODE != kGivenScores) kf.load(Kb, (kt + 1) * kBlock, NK, L);
-        continue;
-      }
-      f32x4 acc[4][QF];
-      const uint32_t vb = sweep_values(kt, vis, acc);
-      if constexpr (MODE != kGivenScores) kf.load(Kb, (kt + 1) * kBlock, NK, L);
-      // bit 16m + 4f + r <- value >= floor (or NaN), highest bit first
+    sweep(std::integral_constant<int, 1>{}, [&](auto, int kt, uint32_t vb, f32x4 (&acc)[4]) {
+      // bit 4f + r <- value >= floor (or NaN), highest bit first
       uint32_t cand = 0;
-      for (int m = QF - 1; m >= 0; --m)
-        for (int f = 3; f >= 0; --f)
-          for (int r = 3; r >= 0; --r) cand = shift_in_nlt(cand, acc[f][m][r], floor_m[m]);
-      cand &= vb & take;
-      if (!__any(cand != 0)) continue;
-      for (int f = 0; f < 4; ++f)
-        for (int m = 0; m < QF; ++m)
-          *reinterpret_cast<f32x4*>(wstage + (16 * m + c16) * kStride + 16 * f + 4 * g) = acc[f][m];
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      const int kbase = kt * kBlock;
+      for (int f = 3; f >= 0; --f)
+        for (int r = 3; r >= 0; --r) cand = shift_in_nlt(cand, acc[f][r], floor_v);
+      cand &= take ? vb : 0u;
+      if (!__any(cand != 0)) return;
+      const int kbase = kt * kBlock + 4 * g;
+      // key of value b = 4f + r: score, index kbase + 16f + r
+      auto key_of = [&](int b) {
+        const float v = pick16(acc, b);
+        const float sc = kExact ? v : clamp_score(v * scale);
+        return make_key(sc, kbase + 16 * (b >> 2) + (b & 3));
+      };
       if (round > 0) {
-        // Exact key thresholds: drop the candidates below them first.
+        // exact key threshold: drop the candidates below it first
         uint32_t c2 = cand;
         while (c2) {
           const int b = __builtin_ctz(c2);
           c2 &= c2 - 1;
-          const int m = b >> 4, f = (b >> 2) & 3, r = b & 3;
-          const float v = wstage[(16 * m + c16) * kStride + 16 * f + 4 * g + r];
-          const float sc = kExact ? v : clamp_score(v * scale);
-          uint64_t th = tkey[0];
-          for (int mm = 1; mm < QF; ++mm)
-            if (mm == m) th = tkey[mm];
-          if (make_key(sc, kbase + 16 * f + 4 * g + r) < th) cand &= ~(1u << b);
+          if (key_of(b) < tkey) cand &= ~(1u << b);
         }
       }
-      // One slot reservation per (lane, row), then the stores.
-      uint32_t pos[QF];
-      for (int m = 0; m < QF; ++m) {
-        const uint32_t mb = (cand >> (16 * m)) & 0xffffu;
-        pos[m] = mb ? atomicAdd(&s.cnt[qw0 + 16 * m + c16], uint32_t(__builtin_popcount(mb))) : 0u;
-      }
+      uint32_t pos = cand ? atomicAdd(&s_cnt[lq], uint32_t(__builtin_popcount(cand))) : 0u;
       while (cand) {
         const int b = __builtin_ctz(cand);
         cand &= cand - 1;
-        const int m = b >> 4, f = (b >> 2) & 3, r = b & 3;
-        const int lq = qw0 + 16 * m + c16;
-        const float v = wstage[(16 * m + c16) * kStride + 16 * f + 4 * g + r];
-        const float sc = kExact ? v : clamp_score(v * scale);
-        uint32_t at = pos[0];
-        for (int mm = 1; mm < QF; ++mm)
-          if (mm == m) at = pos[mm];
-        if (at < uint32_t(cap))
-          p.cand[cand_row0 + size_t(lq) * cap + at] = make_key(sc, kbase + 16 * f + 4 * g + r);
-        for (int mm = 0; mm < QF; ++mm)
-          if (mm == m) ++pos[mm];
+        const uint64_t key = key_of(b);
+        if (pos < uint32_t(cap)) my_cand[pos] = key;
+        ++pos;
       }
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
+    });
+    // (the sweep ends with a block barrier: every count is final)
+    const bool over = rowok && s_cnt[lq] > uint32_t(cap);
+    if (__any(over) && L == 0) s_ctl[0] = uint32_t(round + 1);
+    __syncthreads();
+    if (s_ctl[0] != uint32_t(round + 1) || round >= 64) break;  // block-uniform
+    // Rows that overflowed: the k-th best stored key becomes the row's exact
+    // threshold (every top-k key is >= it), the row's list restarts.
+    for (int j = 0; j < 16; ++j) {
+      const int r = 16 * w + j;
+      if (!(q0 + r < NQ && s_cnt[r] > uint32_t(cap))) continue;  // wave-uniform
+      uint64_t v[8];
+      for (int pp = 0; pp < 8; ++pp) {
+        const int e = (L & 31) * 8 + pp;
+        v[pp] = e < cap ? s_cand[size_t(r) * cap + e] : 0ull;
+      }
+      segment_sort_desc<32>(v, L);
+      // element k-1 lives in lane (k-1)/8, slot (k-1)%8 (both halves agree)
+      const int src = (k - 1) >> 3, sp = (k - 1) & 7;
+      uint64_t mine = v[0];
+      for (int pp = 1; pp < 8; ++pp)
+        if (pp == sp) mine = v[pp];
+      const uint64_t th =
+          (static_cast<uint64_t>(__shfl(static_cast<uint32_t>(mine >> 32), src, kWave)) << 32) |
+          __shfl(static_cast<uint32_t>(mine), src, kWave);
+      if (c == j) {
+        tkey = th;
+        floor_v = sweep_floor(key_score(th), kExact, scale);
+      }
     }
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    if (round > 64) break;  // the threshold rises every round; never reached
+    __syncthreads();  // all overflow reads of the lists and counts are done
+    take = rowok && s_cnt[lq] > uint32_t(cap);
+    __syncthreads();
+    if (take && g == 0) s_cnt[lq] = 0u;
+    // (the next sweep's prologue barrier orders this reset before any append)
   }
 
   // ---------------- select: sort each row's candidates ----------------
-  auto emit = [&](int lq, int e, uint64_t key) {
-    if (e >= k || q0 + lq >= NQ) return;
+  auto emit = [&](int r, int e, uint64_t key) {
+    if (e >= k || q0 + r >= NQ) return;
     const bool real = key != 0ull;
     const float sv = real ? key_score(key) : kSentinel;
     const int idx = real ? key_index(key) : -1;
-    s.tk[e * kWave + lq] = sv;
-    const size_t r = size_t(bh) * NQ + q0 + lq;
+    s_tk[e * kWave + r] = sv;
+    const size_t gr = size_t(bh) * NQ + q0 + r;
     if (p.topk_idx) {
-      p.topk_idx[r * k + e] = idx;
-      p.topk_val[r * k + e] = sv;
+      p.topk_idx[gr * k + e] = idx;
+      p.topk_val[gr * k + e] = sv;
     }
     if (idx >= 0) {
       const int kb = idx / kBlock;
-      atomicOr(&s.bits[kb >> 5], 1u << (kb & 31));
+      atomicOr(&s_bits[kb >> 5], 1u << (kb & 31));
     }
   };
-  auto ncand = [&](int lq) -> int { return (q0 + lq < NQ) ? min(int(s.cnt[lq]), cap) : 0; };
+  auto ncand = [&](int r) -> int { return (q0 + r < NQ) ? min(int(s_cnt[r]), cap) : 0; };
   // Segments of LS lanes x 8 keys sort one row each; a group of 8 rows runs as
   // one LS=8 pass (<= 64 keys per row), two LS=16 or four LS=32 passes.
   auto sort_rows = [&](auto ls_tag, int row0) {
     constexpr int LS = decltype(ls_tag)::value;
-    const int lq = row0 + L / LS, i = L & (LS - 1), n = ncand(lq);
+    const int r = row0 + L / LS, i = L & (LS - 1), n = ncand(r);
     uint64_t v[8];
     for (int pp = 0; pp < 8; ++pp) {
       const int e = i * 8 + pp;
-      v[pp] = e < n ? p.cand[cand_row0 + size_t(lq) * cap + e] : 0ull;
+      v[pp] = e < n ? s_cand[size_t(r) * cap + e] : 0ull;
     }
     segment_sort_desc<LS>(v, L);
-    for (int pp = 0; pp < 8; ++pp) emit(lq, i * 8 + pp, v[pp]);
+    for (int pp = 0; pp < 8; ++pp) emit(r, i * 8 + pp, v[pp]);
   };
-  for (int base = qw0; base < qw0 + QW; base += 8) {
+  for (int base = 16 * w; base < 16 * w + 16; base += 8) {
     int need = k;
     for (int j = 0; j < 8; ++j) need = max(need, ncand(base + j));
     if (need <= 64) {
@@ -623,64 +650,88 @@ __global__ __launch_bounds__(kWave * (4 / QF)) void select_kernel(SelectParams p
       for (int h = 0; h < 4; ++h) sort_rows(std::integral_constant<int, 32>{}, base + 2 * h);
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-
-  // ---------------- tau per row ----------------
-  if (L < QW) {
-    const int lq = qw0 + L;
-    if (q0 + lq < NQ) p.taus[size_t(bh) * NQ + q0 + lq] = entmax_tau(s.tk, lq, k, p.d.alpha);
-  }
   __syncthreads();
+
+  // ---------------- mask row; sorted values for the tau kernel ----------------
   uint8_t* mrow = p.mask + (size_t(bh) * nQB + qb) * nKB;
-  for (int kb = t; kb < nKB; kb += kWave * NW) mrow[kb] = uint8_t((s.bits[kb >> 5] >> (kb & 31)) & 1u);
+  for (int kb = t; kb < nKB; kb += kThreads) mrow[kb] = uint8_t((s_bits[kb >> 5] >> (kb & 31)) & 1u);
+  const size_t rows = size_t(p.d.BH) * NQ;
+  for (int i = t; i < k * kBlock; i += kThreads) {
+    const int e = i >> 6, r = i & 63;
+    if (q0 + r < NQ) p.tkv[size_t(e) * rows + size_t(bh) * NQ + q0 + r] = s_tk[e * kWave + r];
+  }
 }
 
-template <typename T, int D, int QF, int MODE>
+// tau of every row from its sorted top-k values (one thread per row):
+// tkv[e * rows + row], e < k.
+template <int AC>
+__global__ __launch_bounds__(kThreads) void tau_kernel(SelectParams p) {
+  const size_t rows = size_t(p.d.BH) * p.d.NQ;
+  const size_t r = size_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (r >= rows) return;
+  p.taus[r] = entmax_tau<AC>(p.tkv, rows, r, p.d.k, p.d.alpha);
+}
+
+template <typename T, int D, int MODE, int R>
 hipError_t launch_one(const SelectParams& p, hipStream_t s) {
-  const size_t lds = select_lds_bytes(p.d);
-  auto kern = select_kernel<T, D, QF, MODE>;
-  if (lds > 65536) {
+  const SelLayout l = sel_layout(p.d.k, p.cap, p.d.nKB, D, int(sizeof(T)), MODE == kGivenScores);
+  auto kern = select_kernel<T, D, MODE, R>;
+  if (l.total > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, l.total);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3(p.d.nQB * p.d.BH), dim3(kWave * (4 / QF)), lds, s, p);
+  hipLaunchKernelGGL(kern, dim3(p.d.nQB * p.d.BH), dim3(kThreads), l.total, s, p);
   return hipGetLastError();
 }
 
+// Class sets per (row, position): more sets tighten the sweep-2 floor; the
+// larger k, the more candidates a loose floor admits.
 template <typename T, int D, int MODE>
-hipError_t launch_qf(const SelectParams& p, hipStream_t s) {
-  if (p.d.k <= 64) return launch_one<T, D, 2, MODE>(p, s);
-  return launch_one<T, D, 1, MODE>(p, s);
+hipError_t launch_r(const SelectParams& p, hipStream_t s) {
+  if (p.d.k <= 64) return launch_one<T, D, MODE, 4>(p, s);
+  return launch_one<T, D, MODE, 8>(p, s);
 }
 
 template <typename T, int D>
 hipError_t launch_mode(const SelectParams& p, hipStream_t s) {
-  if (p.d.scale > 0.0f) return launch_qf<T, D, kRawDots>(p, s);
-  return launch_qf<T, D, kExactScores>(p, s);
+  if (p.d.scale > 0.0f) return launch_r<T, D, kRawDots>(p, s);
+  return launch_r<T, D, kExactScores>(p, s);
 }
+
+int tbytes_of(bool bf16) { return bf16 ? 2 : 4; }
+int dim_of(const Dims& d, bool from_scores) { return from_scores ? 64 : d.D; }
 
 }  // namespace
 
-int select_capacity(int k) {
-  const int c = k + (k > 64 ? k : 64);
-  return c > 256 ? 256 : c;
+hipError_t launch_tau(const SelectParams& p, hipStream_t s) {
+  const size_t rows = size_t(p.d.BH) * p.d.NQ;
+  const dim3 grid(unsigned((rows + kThreads - 1) / kThreads));
+  switch (alpha_class_of(p.d.alpha)) {
+    case kA15: hipLaunchKernelGGL(tau_kernel<kA15>, grid, dim3(kThreads), 0, s, p); break;
+    case kA20: hipLaunchKernelGGL(tau_kernel<kA20>, grid, dim3(kThreads), 0, s, p); break;
+    case kA125: hipLaunchKernelGGL(tau_kernel<kA125>, grid, dim3(kThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL(tau_kernel<kAGen>, grid, dim3(kThreads), 0, s, p); break;
+  }
+  return hipGetLastError();
 }
 
-size_t select_lds_bytes(const Dims& d) {
-  const size_t nbw = size_t(d.nKB + 31) / 32;
-  size_t b = size_t(kBlock) * kStride * sizeof(float)      // stage
-             + size_t(d.k) * kWave * sizeof(float)         // sorted top-k scores
-             + size_t(kBlock) * sizeof(uint64_t)           // key thresholds
-             + size_t(kBlock) * sizeof(uint32_t)           // counters
-             + nbw * sizeof(uint32_t)                      // mask bits
-             + size_t(d.nKB);                              // key-block visibility
-  return (b + 15) & ~size_t(15);
+size_t select_lds_bytes(const Dims& d, bool bf16, bool from_scores, int cap) {
+  return size_t(sel_layout(d.k, cap, d.nKB, dim_of(d, from_scores),
+                           from_scores ? 4 : tbytes_of(bf16), from_scores).total);
+}
+
+int select_capacity(const Dims& d, bool bf16, bool from_scores, size_t max_lds) {
+  // k + 32 keys per row holds the candidates of random rows with room to
+  // spare; less still works (overflow rounds), as long as it exceeds k.
+  int cap = d.k + 32;
+  if (cap > 256) cap = 256;
+  while (cap > d.k && select_lds_bytes(d, bf16, from_scores, cap) > max_lds) cap -= 8;
+  return cap > d.k ? cap : -1;
 }
 
 hipError_t launch_select(const SelectParams& p, bool bf16, bool from_scores, hipStream_t s) {
-  if (from_scores) return launch_qf<float, 64, kGivenScores>(p, s);
+  if (from_scores) return launch_r<float, 64, kGivenScores>(p, s);
   if (bf16) {
     if (p.d.D == 64) return launch_mode<u16, 64>(p, s);
     if (p.d.D == 128) return launch_mode<u16, 128>(p, s);

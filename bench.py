@@ -39,6 +39,9 @@ PEAK_HBM = 8.0e12        # HBM3E, bytes/s
 ELEM = 2                 # bf16 bytes
 
 
+COPY_BYTES = 256 << 20   # --copy-calibration copy size
+
+
 def effective_flops(B, H, N, d):
     return 3.5 * 4 * B * H * d * N * N / 2
 
@@ -53,7 +56,9 @@ def kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep):
     vis_blocks = BH * nQB * (nQB + 1) // 2
     return {
         "select": dict(bound="mfma", flops=2.0 * d * vis,
-                       bytes=rows * d * ELEM + vis_blocks * tile + rows * 4 + BH * nQB * nKB),
+                       bytes=rows * d * ELEM + vis_blocks * tile + rows * k_keep * 4
+                       + BH * nQB * nKB),
+        "tau": dict(bound="hbm", flops=0.0, bytes=rows * k_keep * 4 + rows * 4),
         "compact": dict(bound="hbm", flops=0.0, bytes=2 * BH * nQB * nKB + csr),
         "forward": dict(bound="hbm", flops=4.0 * 64 * 64 * d * nnzb,
                         bytes=nnzb * 2 * tile + 2 * rows * d * ELEM + 2 * rows * 4
@@ -158,6 +163,9 @@ def main():
     ap.add_argument("--grad-mode", default="entmax", choices=["entmax", "reference"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run 3 plain device copies of 256 MiB (the reference kernel "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no collectives or sharding); "
@@ -177,6 +185,13 @@ def main():
     dO = torch.randn(B, H, N, d, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
     idx = torch.arange(N, dtype=torch.int32, device=dev).unsqueeze(0).expand(B * H, N).contiguous()
     q, k, v = (t.clone().requires_grad_(True) for t in (Q, K, V))
+    if args.copy_calibration:
+        src = torch.ones(COPY_BYTES, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     def step():
         q.grad = k.grad = v.grad = None
