@@ -4,14 +4,18 @@
 // Reference: splash_forward_sparse (adasplashattention.cu:244-341), which
 // recomputes each score with one thread per query and accumulates p*v in
 // registers.  Here one 256-thread block (4 waves x 16 query rows) walks the
-// query block's CSR list; per active key block the K tile (row-major) and
-// the V tile (transposed, bf16) are staged in LDS, S^T = K Q^T is formed on
-// MFMA, p = max(u, EPS)^(1/(alpha-1)) with u = (alpha-1) s - tau is applied
-// in registers, and O^T += V^T P^T runs on MFMA with P^T taken directly
-// from the score accumulators.  Row sums of p are kept per lane and reduced
+// query block's CSR list.  The K tile (row-major) and the V tile
+// (transposed for bf16) of each active key block stream through
+// double-buffered LDS (asa_stage.hpp); S^T = K Q^T is formed on MFMA,
+// p = max(u, EPS)^(1/(alpha-1)) with u = (alpha-1) s - tau is applied in
+// registers, and O^T += V^T P^T runs on MFMA with P^T taken directly from
+// the score accumulators.  Row sums of p are kept per lane and reduced
 // across the four lane groups at the end.
+#include <type_traits>
+
 #include "asa_device.hpp"
 #include "asa_launch.hpp"
+#include "asa_stage.hpp"
 #include "asa_tiles.hpp"
 
 namespace asa {
@@ -21,30 +25,40 @@ constexpr int kThreads = 256;
 
 template <typename T, int D> struct FwdSmem;
 template <int D> struct alignas(16) FwdSmem<u16, D> {
-  u16 K[kBlock * Tile<u16, D>::kRs];
-  u16 Vt[D * Tile<u16, D>::kTs];
-  __device__ const u16* v_operand() const { return Vt; }
-  int kid[kBlock];
+  static constexpr int L0 = kRowMajor, L1 = kTransposed;
+  u16 K[2][kBlock * Tile<u16, D>::kRs];
+  u16 Vt[2][D * Tile<u16, D>::kTs];
+  int kid[2][kBlock];
+  int full[2];
+  __device__ u16* k_rm(int b) { return K[b]; }
+  __device__ u16* v_rm(int) { return nullptr; }
+  __device__ u16* v_tr(int b) { return Vt[b]; }
+  __device__ const u16* v_operand(int b) const { return Vt[b]; }
 };
 template <int D> struct alignas(16) FwdSmem<float, D> {
-  float K[kBlock * Tile<float, D>::kRs];
-  float V[kBlock * Tile<float, D>::kRs];
-  __device__ const float* v_operand() const { return V; }
-  int kid[kBlock];
+  static constexpr int L0 = kRowMajor, L1 = kRowMajor;
+  float K[2][kBlock * Tile<float, D>::kRs];
+  float V[2][kBlock * Tile<float, D>::kRs];
+  int kid[2][kBlock];
+  int full[2];
+  __device__ float* k_rm(int b) { return K[b]; }
+  __device__ float* v_rm(int b) { return V[b]; }
+  __device__ float* v_tr(int) { return nullptr; }
+  __device__ const float* v_operand(int b) const { return V[b]; }
 };
 
-template <typename T, int D>
-__device__ __forceinline__ void stage_kv(FwdSmem<T, D>& sm, const T* K, const T* V,
-                                         const int32_t* kidx, int kbase, int NK, int t) {
-  stage_tile<D>(sm.K, static_cast<T*>(nullptr), K, kbase, NK, t, kThreads);
-  if constexpr (sizeof(T) == 2) stage_tile<D>(static_cast<u16*>(nullptr), sm.Vt, V, kbase, NK, t, kThreads);
-  else stage_tile<D>(sm.V, static_cast<T*>(nullptr), V, kbase, NK, t, kThreads);
-  if (t < kBlock) sm.kid[t] = (kbase + t < NK) ? kidx[kbase + t] : 0;
+// Clamp of a score without the operand canonicalisation fmaxf/fminf carry
+// (MFMA results are never signalling NaNs); NaN -> -10 like fmaxf/fminf.
+__device__ __forceinline__ float clamp10(float s) {
+  float r;
+  asm("v_max_f32 %0, %1, %2\n\tv_min_f32 %0, %0, %3" : "=&v"(r) : "v"(s), "s"(-10.0f), "s"(10.0f));
+  return r;
 }
 
 template <typename T, int D, int PC>
 __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   __shared__ FwdSmem<T, D> sm;
+  using St = Stager<T, D, FwdSmem<T, D>::L0, FwdSmem<T, D>::L1>;
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
@@ -61,10 +75,16 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   RowFrag<T, D> qf;
   qf.load(static_cast<const T*>(p.q) + row * D, qok, lane);
   const int qpos = qok ? p.q_idx[row] : 0;
-  const float tau = qok ? p.taus[row] : 0.0f;
+  const float tau = qok ? p.taus[row] : __builtin_inff();  // invalid rows: u < 0
   const float am1 = p.d.alpha - 1.0f;
   const float a = 1.0f / am1;
   const float scale = p.d.scale;
+  // smallest position of the block's valid rows (wave 0 tests tiles with it)
+  int qmin = 0;
+  if (w == 0) {
+    const int qq = qb * kBlock + lane;
+    qmin = wave_reduce_minmax<false>(qq < NQ ? p.q_idx[size_t(bh) * NQ + qq] : INT32_MAX);
+  }
 
   f32x4 o[D / 16];
   for (int db = 0; db < D / 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -73,31 +93,48 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
   const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
   const int e0 = qp[qb], e1 = qp[qb + 1];
-  for (int e = e0; e < e1; ++e) {
+  St st;
+  PosStager ps;
+  auto fetch = [&](int e) {
     const int kbase = ql[e] * kBlock;
-    __syncthreads();
-    stage_kv<T, D>(sm, Kb, Vb, kidx, kbase, NK, t);
-    __syncthreads();
-
+    st.load(Kb, Vb, kbase, NK, t);
+    ps.load(kidx, kbase, NK, INT32_MAX, t);
+  };
+  auto put = [&](int b) {
+    st.store(sm.k_rm(b), nullptr, sm.v_rm(b), sm.v_tr(b), t);
+    ps.store<true>(sm.kid[b], &sm.full[b], qmin, t);
+  };
+  if (e0 < e1) {
+    fetch(e0);
+    put(0);
+    if (e0 + 1 < e1) fetch(e0 + 1);
+  }
+  __syncthreads();
+  for (int e = e0; e < e1; ++e) {
+    const int b = (e - e0) & 1;
     f32x4 acc[4];
-    rows_x_frag<D>(acc, sm.K, qf, lane);
-    for (int f = 0; f < 4; ++f)
-      for (int r = 0; r < 4; ++r) {
-        const int kl = 16 * f + 4 * g + r;
-        const bool vis = qok && (kbase + kl) < NK && sm.kid[kl] <= qpos;
-        float pv = 0.0f;
-        if (vis) {
-          const float s = clamp_score(acc[f][r] * scale);
-          const float u = am1 * s - tau;
-          if (u > 0.0f) {
-            pv = pow_fast<PC>(fmaxf(u, kEps), a);
-            if (!finite(pv)) pv = 0.0f;
-          }
+    rows_x_frag<D>(acc, sm.K[b], qf, lane);
+    // p for every score, then masked: no per-score branches
+    auto weights = [&](auto partial) {
+      for (int f = 0; f < 4; ++f)
+        for (int r = 0; r < 4; ++r) {
+          const float u = am1 * clamp10(acc[f][r] * scale) - tau;
+          float pv = pow_fast<PC>(fmaxf(u, kEps), a);
+          if constexpr (PC != kE0 && PC != kE1 && PC != kE2) pv = finite(pv) ? pv : 0.0f;
+          bool vis = u > 0.0f;
+          if constexpr (decltype(partial)::value) vis = vis && sm.kid[b][16 * f + 4 * g + r] <= qpos;
+          acc[f][r] = vis ? pv : 0.0f;
+          rowsum += acc[f][r];
         }
-        acc[f][r] = pv;
-        rowsum += pv;
-      }
-    tile_t_x_acc<D>(o, sm.v_operand(), acc, lane);
+    };
+    if (sm.full[b] != 0) weights(std::false_type{});
+    else weights(std::true_type{});
+    tile_t_x_acc<D>(o, sm.v_operand(b), acc, lane);
+    if (e + 1 < e1) {
+      put(b ^ 1);
+      if (e + 2 < e1) fetch(e + 2);
+    }
+    __syncthreads();
   }
 
   const float norm = sum_groups(rowsum);
