@@ -33,8 +33,11 @@
 //                                 shift = sum(w dp) / sum(w)
 //   reference (ASA_GRAD_REFERENCE): c = 1 / (sum p + EPS), shift = out . dO,
 //                                 and w = 0 unless u > EPS (:494).
+#include <type_traits>
+
 #include "asa_device.hpp"
 #include "asa_launch.hpp"
+#include "asa_stage.hpp"
 #include "asa_tiles.hpp"
 
 namespace asa {
@@ -60,32 +63,43 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(BackwardParams p) {
   cfac[r] = 1.0f / (p.norms[r] + kEps);
 }
 
+// Clamp of a score without the operand canonicalisation fmaxf/fminf carry
+// (MFMA results are never signalling NaNs); NaN -> -10 like fmaxf/fminf.
+__device__ __forceinline__ float clamp10(float s) {
+  float r;
+  asm("v_max_f32 %0, %1, %2\n\tv_min_f32 %0, %0, %3" : "=&v"(r) : "v"(s), "s"(-10.0f), "s"(10.0f));
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // dQ (query-major)
 // ---------------------------------------------------------------------------
 template <typename T, int D> struct DqSmem;
 template <int D> struct alignas(16) DqSmem<u16, D> {
-  u16 K[kBlock * Tile<u16, D>::kRs];
-  u16 Kt[D * Tile<u16, D>::kTs];
-  u16 V[kBlock * Tile<u16, D>::kRs];
-  int kid[kBlock];
-  __device__ const u16* k_operand() const { return Kt; }
-  __device__ u16* k_transposed() { return Kt; }
+  static constexpr int L0 = kBothLayouts, L1 = kRowMajor;  // K, V
+  u16 K[2][kBlock * Tile<u16, D>::kRs];
+  u16 Kt[2][D * Tile<u16, D>::kTs];
+  u16 V[2][kBlock * Tile<u16, D>::kRs];
+  int kid[2][kBlock];
+  int full[2];
+  __device__ u16* kt(int b) { return Kt[b]; }
+  __device__ const u16* k_operand(int b) const { return Kt[b]; }
 };
 template <int D> struct alignas(16) DqSmem<float, D> {
-  float K[kBlock * Tile<float, D>::kRs];
-  float V[kBlock * Tile<float, D>::kRs];
-  int kid[kBlock];
-  __device__ const float* k_operand() const { return K; }
-  __device__ float* k_transposed() { return nullptr; }
+  static constexpr int L0 = kRowMajor, L1 = kRowMajor;
+  float K[2][kBlock * Tile<float, D>::kRs];
+  float V[2][kBlock * Tile<float, D>::kRs];
+  int kid[2][kBlock];
+  int full[2];
+  __device__ float* kt(int) { return nullptr; }
+  __device__ const float* k_operand(int b) const { return K[b]; }
 };
 
-template <typename T, int D, int AC>
+template <typename T, int D, int AC, bool REF>
 __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
   __shared__ DqSmem<T, D> sm;
-  constexpr int PP = AlphaPow<AC>::P, PW = AlphaPow<AC>::W;
-  (void)PP;
-  const bool ref = p.mode == 1;
+  using St = Stager<T, D, DqSmem<T, D>::L0, DqSmem<T, D>::L1>;
+  constexpr int PW = AlphaPow<AC>::W;
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
@@ -104,14 +118,14 @@ __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
   qf.load(static_cast<const T*>(p.q) + row * D, qok, lane);
   df.load(static_cast<const T*>(p.dout) + row * D, qok, lane);
   const int qpos = qok ? p.q_idx[row] : 0;
-  const float tau = qok ? p.taus[row] : 0.0f;
+  const float tau = qok ? p.taus[row] : __builtin_inff();  // invalid rows: u < 0
   const float alpha = p.d.alpha;
   const float am1 = alpha - 1.0f;
   const float ew = (2.0f - alpha) / am1;
-  const float thr = ref ? kEps : 0.0f;
+  const float thr = REF ? kEps : 0.0f;
   const float norm = qok ? p.norms[row] : 0.0f;
   float cfac, shift;
-  if (ref) {
+  if constexpr (REF) {
     cfac = qok ? p.delta[rows + row] : 0.0f;
     shift = qok ? p.delta[row] : 0.0f;
   } else {
@@ -119,6 +133,11 @@ __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
     shift = 0.0f;
   }
   const float scale = p.d.scale;
+  int qmin = 0;
+  if (w == 0) {
+    const int qq = qb * kBlock + lane;
+    qmin = wave_reduce_minmax<false>(qq < NQ ? p.q_idx[size_t(bh) * NQ + qq] : INT32_MAX);
+  }
 
   f32x4 a1[D / 16], a2[D / 16];
   for (int db = 0; db < D / 16; ++db) a1[db] = a2[db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -127,46 +146,61 @@ __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
   const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
   const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
   const int e0 = qp[qb], e1 = qp[qb + 1];
-  for (int e = e0; e < e1; ++e) {
+  St st;
+  PosStager ps;
+  auto fetch = [&](int e) {
     const int kbase = ql[e] * kBlock;
-    __syncthreads();
-    stage_tile<D>(sm.K, sm.k_transposed(), Kb, kbase, NK, t, kThreads);
-    stage_tile<D>(sm.V, static_cast<T*>(nullptr), Vb, kbase, NK, t, kThreads);
-    if (t < kBlock) sm.kid[t] = (kbase + t < NK) ? kidx[kbase + t] : 0;
-    __syncthreads();
-
+    st.load(Kb, Vb, kbase, NK, t);
+    ps.load(kidx, kbase, NK, INT32_MAX, t);
+  };
+  auto put = [&](int b) {
+    st.store(sm.K[b], sm.kt(b), sm.V[b], nullptr, t);
+    ps.store<true>(sm.kid[b], &sm.full[b], qmin, t);
+  };
+  if (e0 < e1) {
+    fetch(e0);
+    put(0);
+    if (e0 + 1 < e1) fetch(e0 + 1);
+  }
+  __syncthreads();
+  for (int e = e0; e < e1; ++e) {
+    const int b = (e - e0) & 1;
     f32x4 sacc[4], dacc[4];
-    rows_x_frag<D>(sacc, sm.K, qf, lane);
-    rows_x_frag<D>(dacc, sm.V, df, lane);
-    for (int f = 0; f < 4; ++f)
-      for (int r = 0; r < 4; ++r) {
-        const int kl = 16 * f + 4 * g + r;
-        const bool vis = qok && (kbase + kl) < NK && sm.kid[kl] <= qpos;
-        float wv = 0.0f;
-        if (vis) {
-          const float u = am1 * clamp_score(sacc[f][r] * scale) - tau;
-          if (u > thr) {
-            wv = pow_fast<PW>(fmaxf(u, kEps), ew);
-            if (!finite(wv)) wv = 0.0f;
+    rows_x_frag<D>(sacc, sm.K[b], qf, lane);
+    rows_x_frag<D>(dacc, sm.V[b], df, lane);
+    auto weights = [&](auto partial) {
+      for (int f = 0; f < 4; ++f)
+        for (int r = 0; r < 4; ++r) {
+          const float u = am1 * clamp10(sacc[f][r] * scale) - tau;
+          float wv = pow_fast<PW>(fmaxf(u, kEps), ew);
+          if constexpr (PW != kE0 && PW != kE1 && PW != kE2) wv = finite(wv) ? wv : 0.0f;
+          bool vis = u > thr;
+          if constexpr (decltype(partial)::value) vis = vis && sm.kid[b][16 * f + 4 * g + r] <= qpos;
+          wv = vis ? wv : 0.0f;
+          const float dp = dacc[f][r];
+          if constexpr (REF) {
+            const float ds = cfac * wv * (dp - shift);
+            sacc[f][r] = finite(ds) ? ds : 0.0f;
+          } else {
+            sw += wv;
+            swdp += wv * dp;
+            sacc[f][r] = wv * dp;
+            dacc[f][r] = wv;
           }
         }
-        const float dp = dacc[f][r];
-        if (ref) {
-          float ds = cfac * wv * (dp - shift);
-          if (!finite(ds)) ds = 0.0f;
-          sacc[f][r] = ds;
-        } else {
-          sw += wv;
-          swdp += wv * dp;
-          sacc[f][r] = wv * dp;
-          dacc[f][r] = wv;
-        }
-      }
-    tile_t_x_acc<D, true>(a1, sm.k_operand(), sacc, lane);
-    if (!ref) tile_t_x_acc<D, true>(a2, sm.k_operand(), dacc, lane);
+    };
+    if (sm.full[b] != 0) weights(std::false_type{});
+    else weights(std::true_type{});
+    tile_t_x_acc<D, true>(a1, sm.k_operand(b), sacc, lane);
+    if constexpr (!REF) tile_t_x_acc<D, true>(a2, sm.k_operand(b), dacc, lane);
+    if (e + 1 < e1) {
+      put(b ^ 1);
+      if (e + 2 < e1) fetch(e + 2);
+    }
+    __syncthreads();
   }
 
-  if (!ref) {
+  if constexpr (!REF) {
     sw = sum_groups(sw);
     swdp = sum_groups(swdp);
     shift = sw > 0.0f ? swdp / sw : 0.0f;
@@ -178,10 +212,10 @@ __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
   }
   if (qok) {
     T* out = static_cast<T*>(p.dq) + row * D;
-    const float cs = ref ? scale : scale * cfac;
+    const float cs = REF ? scale : scale * cfac;
     for (int db = 0; db < D / 16; ++db)
       for (int r = 0; r < 4; ++r) {
-        const float acc = ref ? a1[db][r] : (a1[db][r] - shift * a2[db][r]);
+        const float acc = REF ? a1[db][r] : (a1[db][r] - shift * a2[db][r]);
         float v = cs * acc;
         if (!finite(v)) v = 0.0f;
         Elem<T>::store(out + 16 * db + 4 * g + r, v);
@@ -194,31 +228,61 @@ __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
 // ---------------------------------------------------------------------------
 template <typename T, int D> struct DkvSmem;
 template <int D> struct alignas(16) DkvSmem<u16, D> {
-  u16 Q[kBlock * Tile<u16, D>::kRs];
-  u16 Qt[D * Tile<u16, D>::kTs];
-  u16 dO[kBlock * Tile<u16, D>::kRs];
-  u16 dOt[D * Tile<u16, D>::kTs];
-  __device__ const u16* q_operand() const { return Qt; }
-  __device__ const u16* do_operand() const { return dOt; }
-  __device__ u16* q_transposed() { return Qt; }
-  __device__ u16* do_transposed() { return dOt; }
+  static constexpr int L0 = kBothLayouts, L1 = kBothLayouts;  // Q, dO
+  u16 Q[2][kBlock * Tile<u16, D>::kRs];
+  u16 Qt[2][D * Tile<u16, D>::kTs];
+  u16 dO[2][kBlock * Tile<u16, D>::kRs];
+  u16 dOt[2][D * Tile<u16, D>::kTs];
+  __device__ u16* qt(int b) { return Qt[b]; }
+  __device__ u16* dot(int b) { return dOt[b]; }
+  __device__ const u16* q_operand(int b) const { return Qt[b]; }
+  __device__ const u16* do_operand(int b) const { return dOt[b]; }
 };
 template <int D> struct alignas(16) DkvSmem<float, D> {
-  float Q[kBlock * Tile<float, D>::kRs];
-  float dO[kBlock * Tile<float, D>::kRs];
-  __device__ const float* q_operand() const { return Q; }
-  __device__ const float* do_operand() const { return dO; }
-  __device__ float* q_transposed() { return nullptr; }
-  __device__ float* do_transposed() { return nullptr; }
+  static constexpr int L0 = kRowMajor, L1 = kRowMajor;
+  float Q[2][kBlock * Tile<float, D>::kRs];
+  float dO[2][kBlock * Tile<float, D>::kRs];
+  __device__ float* qt(int) { return nullptr; }
+  __device__ float* dot(int) { return nullptr; }
+  __device__ const float* q_operand(int b) const { return Q[b]; }
+  __device__ const float* do_operand(int b) const { return dO[b]; }
 };
 
-template <typename T, int D, int AC>
+// Per-query constants of a query tile: tau, 1/(sum p + EPS), shift, c.
+struct alignas(16) QConst {
+  float tau[kBlock], invn[kBlock], shift[kBlock], c[kBlock];
+  int pos[kBlock];
+};
+struct QConstStager {
+  float tau, invn, shift, c;
+  __device__ __forceinline__ void load(const BackwardParams& p, size_t rows, size_t rbase, int qbase,
+                                       int NQ, int t) {
+    if (t < kWave) {
+      const bool ok = qbase + t < NQ;
+      const size_t r = rbase + (ok ? qbase + t : 0);
+      tau = ok ? p.taus[r] : __builtin_inff();  // invalid rows: u < 0
+      invn = ok ? 1.0f / (p.norms[r] + kEps) : 0.0f;
+      shift = ok ? p.delta[r] : 0.0f;
+      c = ok ? p.delta[rows + r] : 0.0f;
+    }
+  }
+  __device__ __forceinline__ void store(QConst& qc, int t) const {
+    if (t < kWave) {
+      qc.tau[t] = tau;
+      qc.invn[t] = invn;
+      qc.shift[t] = shift;
+      qc.c[t] = c;
+    }
+  }
+};
+
+template <typename T, int D, int AC, bool REF>
 __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
   __shared__ DkvSmem<T, D> sm;
-  __shared__ float s_tau[kBlock], s_c[kBlock], s_shift[kBlock], s_invn[kBlock];
-  __shared__ int s_pos[kBlock], s_ok[kBlock];
+  __shared__ QConst qcs[2];
+  __shared__ int full[2];
+  using St = Stager<T, D, DkvSmem<T, D>::L0, DkvSmem<T, D>::L1>;
   constexpr int PP = AlphaPow<AC>::P, PW = AlphaPow<AC>::W;
-  const bool ref = p.mode == 1;
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
@@ -228,9 +292,11 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
   const bool jok = j < NK;
   const size_t krow = size_t(bh) * NK + (jok ? j : 0);
   const size_t rows = size_t(p.d.BH) * NQ;
+  const size_t rbase = size_t(bh) * NQ;
 
   const T* Qb = static_cast<const T*>(p.q) + size_t(bh) * NQ * D;
   const T* dOb = static_cast<const T*>(p.dout) + size_t(bh) * NQ * D;
+  const int32_t* qidx = p.q_idx + size_t(bh) * NQ;
 
   RowFrag<T, D> kf, vf;
   kf.load(static_cast<const T*>(p.k) + krow * D, jok, lane);
@@ -240,8 +306,14 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
   const float am1 = alpha - 1.0f;
   const float a = 1.0f / am1;
   const float ew = (2.0f - alpha) / am1;
-  const float thr = ref ? kEps : 0.0f;
+  const float thr = REF ? kEps : 0.0f;
   const float scale = p.d.scale;
+  // largest position of the block's valid keys (wave 0 tests tiles with it)
+  int kmax = 0;
+  if (w == 0) {
+    const int kk = kb * kBlock + lane;
+    kmax = wave_reduce_minmax<true>(kk < NK ? p.k_idx[size_t(bh) * NK + kk] : INT32_MIN);
+  }
 
   f32x4 ak[D / 16], av[D / 16];
   for (int db = 0; db < D / 16; ++db) ak[db] = av[db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -249,51 +321,66 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
   const int32_t* kp = p.k_ptr + size_t(bh) * (nKB + 1);
   const int32_t* kl = p.k_list + size_t(bh) * nKB * nQB;
   const int e0 = kp[kb], e1 = kp[kb + 1];
-  for (int e = e0; e < e1; ++e) {
+  St st;
+  PosStager ps;
+  QConstStager qs;
+  auto fetch = [&](int e) {
     const int qbase = kl[e] * kBlock;
-    __syncthreads();
-    stage_tile<D>(sm.Q, sm.q_transposed(), Qb, qbase, NQ, t, kThreads);
-    stage_tile<D>(sm.dO, sm.do_transposed(), dOb, qbase, NQ, t, kThreads);
-    if (t < kBlock) {
-      const int qi = qbase + t;
-      const bool ok = qi < NQ;
-      const size_t r = size_t(bh) * NQ + (ok ? qi : 0);
-      s_ok[t] = ok;
-      s_pos[t] = ok ? p.q_idx[r] : 0;
-      s_tau[t] = ok ? p.taus[r] : 0.0f;
-      s_invn[t] = ok ? 1.0f / (p.norms[r] + kEps) : 0.0f;
-      s_shift[t] = ok ? p.delta[r] : 0.0f;
-      s_c[t] = ok ? p.delta[rows + r] : 0.0f;
+    st.load(Qb, dOb, qbase, NQ, t);
+    ps.load(qidx, qbase, NQ, INT32_MAX, t);
+    qs.load(p, rows, rbase, qbase, NQ, t);
+  };
+  auto put = [&](int b) {
+    st.store(sm.Q[b], sm.qt(b), sm.dO[b], sm.dot(b), t);
+    ps.store<false>(qcs[b].pos, &full[b], kmax, t);
+    qs.store(qcs[b], t);
+  };
+  if (e0 < e1) {
+    fetch(e0);
+    put(0);
+    if (e0 + 1 < e1) fetch(e0 + 1);
+  }
+  __syncthreads();
+  for (int e = e0; e < e1; ++e) {
+    const int b = (e - e0) & 1;
+    const QConst& qc = qcs[b];
+    f32x4 sacc[4], dacc[4];
+    rows_x_frag<D>(sacc, sm.Q[b], kf, lane);
+    rows_x_frag<D>(dacc, sm.dO[b], vf, lane);
+    auto grads = [&](auto partial) {
+      for (int f = 0; f < 4; ++f) {
+        // constants of queries 16f + 4g + 0..3
+        const int q4 = 16 * f + 4 * g;
+        const f32x4 tau4 = *reinterpret_cast<const f32x4*>(&qc.tau[q4]);
+        const f32x4 invn4 = *reinterpret_cast<const f32x4*>(&qc.invn[q4]);
+        const f32x4 shift4 = *reinterpret_cast<const f32x4*>(&qc.shift[q4]);
+        const f32x4 c4 = *reinterpret_cast<const f32x4*>(&qc.c[q4]);
+        for (int r = 0; r < 4; ++r) {
+          const float u = am1 * clamp10(sacc[f][r] * scale) - tau4[r];
+          const float ue = fmaxf(u, kEps);
+          float pv = pow_fast<PP>(ue, a);
+          float wv = pow_fast<PW>(ue, ew);
+          if constexpr (PP != kE0 && PP != kE1 && PP != kE2) pv = finite(pv) ? pv : 0.0f;
+          if constexpr (PW != kE0 && PW != kE1 && PW != kE2) wv = finite(wv) ? wv : 0.0f;
+          bool vis = true;
+          if constexpr (decltype(partial)::value) vis = kpos <= qc.pos[q4 + r];
+          const float pn = (vis && u > 0.0f) ? pv * invn4[r] : 0.0f;
+          float ds = c4[r] * wv * (dacc[f][r] - shift4[r]);
+          ds = (vis && u > thr && finite(ds)) ? ds : 0.0f;
+          sacc[f][r] = ds;
+          dacc[f][r] = pn;
+        }
+      }
+    };
+    if (full[b] != 0) grads(std::false_type{});
+    else grads(std::true_type{});
+    tile_t_x_acc<D>(av, sm.do_operand(b), dacc, lane);
+    tile_t_x_acc<D, true>(ak, sm.q_operand(b), sacc, lane);
+    if (e + 1 < e1) {
+      put(b ^ 1);
+      if (e + 2 < e1) fetch(e + 2);
     }
     __syncthreads();
-
-    f32x4 sacc[4], dacc[4];
-    rows_x_frag<D>(sacc, sm.Q, kf, lane);
-    rows_x_frag<D>(dacc, sm.dO, vf, lane);
-    for (int f = 0; f < 4; ++f)
-      for (int r = 0; r < 4; ++r) {
-        const int qi = 16 * f + 4 * g + r;
-        const bool vis = jok && s_ok[qi] && kpos <= s_pos[qi];
-        float pn = 0.0f, ds = 0.0f;
-        if (vis) {
-          const float u = am1 * clamp_score(sacc[f][r] * scale) - s_tau[qi];
-          if (u > 0.0f) {
-            float pv = pow_fast<PP>(fmaxf(u, kEps), a);
-            if (!finite(pv)) pv = 0.0f;
-            pn = pv * s_invn[qi];
-          }
-          if (u > thr) {
-            float wv = pow_fast<PW>(fmaxf(u, kEps), ew);
-            if (!finite(wv)) wv = 0.0f;
-            ds = s_c[qi] * wv * (dacc[f][r] - s_shift[qi]);
-            if (!finite(ds)) ds = 0.0f;
-          }
-        }
-        sacc[f][r] = ds;
-        dacc[f][r] = pn;
-      }
-    tile_t_x_acc<D>(av, sm.do_operand(), dacc, lane);
-    tile_t_x_acc<D, true>(ak, sm.q_operand(), sacc, lane);
   }
 
   if (jok) {
@@ -310,28 +397,36 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
   }
 }
 
-template <typename T, int D>
-hipError_t launch_dq_td(const BackwardParams& p, hipStream_t s) {
+template <typename T, int D, bool REF>
+hipError_t launch_dq_m(const BackwardParams& p, hipStream_t s) {
   dim3 grid(p.d.nQB * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
-    case kA15: hipLaunchKernelGGL((dq_kernel<T, D, kA15>), grid, dim3(kThreads), 0, s, p); break;
-    case kA20: hipLaunchKernelGGL((dq_kernel<T, D, kA20>), grid, dim3(kThreads), 0, s, p); break;
-    case kA125: hipLaunchKernelGGL((dq_kernel<T, D, kA125>), grid, dim3(kThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((dq_kernel<T, D, kAGen>), grid, dim3(kThreads), 0, s, p); break;
+    case kA15: hipLaunchKernelGGL((dq_kernel<T, D, kA15, REF>), grid, dim3(kThreads), 0, s, p); break;
+    case kA20: hipLaunchKernelGGL((dq_kernel<T, D, kA20, REF>), grid, dim3(kThreads), 0, s, p); break;
+    case kA125: hipLaunchKernelGGL((dq_kernel<T, D, kA125, REF>), grid, dim3(kThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL((dq_kernel<T, D, kAGen, REF>), grid, dim3(kThreads), 0, s, p); break;
   }
   return hipGetLastError();
 }
-
 template <typename T, int D>
-hipError_t launch_dkdv_td(const BackwardParams& p, hipStream_t s) {
+hipError_t launch_dq_td(const BackwardParams& p, hipStream_t s) {
+  return p.mode == 1 ? launch_dq_m<T, D, true>(p, s) : launch_dq_m<T, D, false>(p, s);
+}
+
+template <typename T, int D, bool REF>
+hipError_t launch_dkdv_m(const BackwardParams& p, hipStream_t s) {
   dim3 grid(p.d.nKB * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
-    case kA15: hipLaunchKernelGGL((dkdv_kernel<T, D, kA15>), grid, dim3(kThreads), 0, s, p); break;
-    case kA20: hipLaunchKernelGGL((dkdv_kernel<T, D, kA20>), grid, dim3(kThreads), 0, s, p); break;
-    case kA125: hipLaunchKernelGGL((dkdv_kernel<T, D, kA125>), grid, dim3(kThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((dkdv_kernel<T, D, kAGen>), grid, dim3(kThreads), 0, s, p); break;
+    case kA15: hipLaunchKernelGGL((dkdv_kernel<T, D, kA15, REF>), grid, dim3(kThreads), 0, s, p); break;
+    case kA20: hipLaunchKernelGGL((dkdv_kernel<T, D, kA20, REF>), grid, dim3(kThreads), 0, s, p); break;
+    case kA125: hipLaunchKernelGGL((dkdv_kernel<T, D, kA125, REF>), grid, dim3(kThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL((dkdv_kernel<T, D, kAGen, REF>), grid, dim3(kThreads), 0, s, p); break;
   }
   return hipGetLastError();
+}
+template <typename T, int D>
+hipError_t launch_dkdv_td(const BackwardParams& p, hipStream_t s) {
+  return p.mode == 1 ? launch_dkdv_m<T, D, true>(p, s) : launch_dkdv_m<T, D, false>(p, s);
 }
 
 template <typename T, int D>
