@@ -40,6 +40,10 @@ ELEM = 2                 # bf16 bytes
 
 
 COPY_BYTES = 256 << 20   # --copy-calibration copy size
+# HBM bytes per launch of each kernel at this workload, measured with
+# rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), the factors a plain
+# 256 MiB device copy gives (profiles/headline_hbm_traffic.md).
+HBM_TRAFFIC = {'select': 104480800, 'tau': 40939296, 'compact': 2456064, 'forward': 139069312, 'bwd_dq': 174430251, 'bwd_dkdv': 207871317}
 
 
 def effective_flops(B, H, N, d):
@@ -126,10 +130,11 @@ def dense_gpu_baseline(Q, K, V, dO, alpha, scale, iters=40):
     return (time.perf_counter() - t0) * 1e3
 
 
-def cpu_baseline(heads=16, trials=3):
+def cpu_baseline(heads=64, trials=2):
     """The CPU oracle (C restatement of the reference algorithm, OpenMP over
-    rows / heads) on a sample of the headline workload: `heads` of its 64
-    (batch, head) slices, full N=4096, bf16-rounded inputs in fp32."""
+    rows / heads) on the headline workload: `heads` of its 64 (batch, head)
+    slices (all of them by default, about 6 s per trial on 16 cores), full
+    N=4096, bf16-rounded inputs in fp32."""
     import numpy as np
     import torch
 
@@ -151,7 +156,7 @@ def cpu_baseline(heads=16, trials=3):
     return {"value": round(flops / t / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": f"oracle fwd+bwd (entmax grad) on {heads} of 64 (batch,head) slices, "
-                      f"N={N} d={d} k={WORK['k_keep']}, median of {trials}: {t:.2f} s",
+                      f"N={N} d={d} k={WORK['k_keep']}, median of {trials} trials: {t:.2f} s each",
             "ms_per_step_scaled": round(t * 1e3 * 64 / heads, 1)}
 
 
@@ -223,6 +228,7 @@ def main():
         if name in models:
             kernels[name] = roofline_of(models[name], tot / cnt)
             kernels[name]["launches"] = cnt
+            kernels[name]["traffic"] = HBM_TRAFFIC.get(name)
     dominant = max(kernels, key=lambda n: kernels[n]["avg_ms"])
     roof = {kk: kernels[dominant][kk] for kk in ("bound", "achieved", "peak", "unit", "frac",
                                                  "traffic")}
