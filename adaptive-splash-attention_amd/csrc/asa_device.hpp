@@ -153,6 +153,17 @@ __device__ __forceinline__ int xcd_task(int i, int total) {
   return x * base + (x < rem ? x : rem) + j;
 }
 
+// Transposing LDS read (ds_read_b64_tr_b16): in each 16-lane group, lane l
+// supplies the address of 4 consecutive bf16 values; lane i receives value
+// i % 4 of the rows supplied by lanes 4m + i / 4, m = 0..3.
+typedef short short4_lds __attribute__((vector_size(8)));
+__device__ __forceinline__ bf16x4 read_tr16(const u16* p) {
+  typedef __attribute__((address_space(3))) short4_lds lds_v4;
+  const short4_lds v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4*)((__attribute__((address_space(3))) u16*)(p)));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
 // ---------------------------------------------------------------------------
 // Cross-lane moves on the VALU (DPP), no trip through the LDS crossbar.
 //   quad_perm 0xB1 / 0x4E / 0x1B: lane i <- lane i^1 / i^2 / i^3 (in quads)

@@ -10,12 +10,9 @@
 // Work split: a tile is cut into "quads" of 4 consecutive rows x one
 // 16-byte column chunk; the quads of both tiles are dealt to the 256
 // threads (quad index = thread + 256 * i, tile 0's quads first, so that
-// every wave works on one tile at a time).  A quad is written to LDS
-//   - row-major (stride Tile<T, D>::kRs): four 16-byte stores, and/or
-//   - transposed (bf16 only, stride Tile<u16, D>::kTs): the 4 rows of each
-//     of the chunk's 8 columns are packed with v_perm_b32 into one 8-byte
-//     store, so the transposed copy costs 8 stores per quad rather than
-//     32 two-byte stores.
+// every wave works on one tile at a time) and stored row-major (stride
+// Tile<T, D>::kRs).  Products that need a tile transposed read it with the
+// transposing LDS read, so no transposed copy is staged.
 #pragma once
 
 #include "asa_device.hpp"
@@ -23,19 +20,14 @@
 
 namespace asa {
 
-enum StageLayout : int { kRowMajor = 1, kTransposed = 2, kBothLayouts = 3 };
-
-template <typename T, int D, int L0, int L1, int NT = 256>
+template <typename T, int D, int NT = 256>
 struct Stager {
   static constexpr int kEpc = 16 / int(sizeof(T));   // elements per 16-byte chunk
   static constexpr int kCpr = D / kEpc;              // chunks per row
   static constexpr int kQuads = (kBlock / 4) * kCpr; // quads per tile
   static constexpr int kPer = 2 * kQuads / NT;       // quads per thread
   static_assert(2 * kQuads % NT == 0, "quads must divide evenly");
-  static_assert(sizeof(T) == 2 || ((L0 | L1) & kTransposed) == 0,
-                "transposed staging is for bf16 tiles");
   static constexpr int kRs = Tile<T, D>::kRs;
-  static constexpr int kTs = sizeof(T) == 2 ? Tile<u16, D>::kTs : 0;
 
   uint4 r[kPer][4];
 
@@ -56,36 +48,15 @@ struct Stager {
     }
   }
 
-  // Tile 0 to rm0 / tr0, tile 1 to rm1 / tr1 (as the layouts L0, L1 say).
-  __device__ __forceinline__ void store(T* rm0, T* tr0, T* rm1, T* tr1, int t) const {
+  // Tile 0 to dst0, tile 1 to dst1.
+  __device__ __forceinline__ void store(T* dst0, T* dst1, int t) const {
     for (int i = 0; i < kPer; ++i) {
       const int qi = t + i * NT;
       const int job = qi / kQuads, q = qi % kQuads;
       const int rq = q / kCpr, cc = q % kCpr;
-      const int lay = job == 0 ? L0 : L1;
-      T* rm = job == 0 ? rm0 : rm1;
-      T* tr = job == 0 ? tr0 : tr1;
-      if (lay & kRowMajor)
-        for (int j = 0; j < 4; ++j)
-          *reinterpret_cast<uint4*>(rm + (4 * rq + j) * kRs + cc * kEpc) = r[i][j];
-      if constexpr (sizeof(T) == 2) {
-        if (lay & kTransposed) {
-          const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&r[i][0]);
-          const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&r[i][1]);
-          const uint32_t* r2 = reinterpret_cast<const uint32_t*>(&r[i][2]);
-          const uint32_t* r3 = reinterpret_cast<const uint32_t*>(&r[i][3]);
-          for (int m = 0; m < 4; ++m) {
-            // word m of a row holds columns 2m (low half) and 2m+1 (high half)
-            const uint2 lo = {__builtin_amdgcn_perm(r1[m], r0[m], 0x05040100u),
-                              __builtin_amdgcn_perm(r3[m], r2[m], 0x05040100u)};
-            const uint2 hi = {__builtin_amdgcn_perm(r1[m], r0[m], 0x07060302u),
-                              __builtin_amdgcn_perm(r3[m], r2[m], 0x07060302u)};
-            const int col = cc * 8 + 2 * m;
-            *reinterpret_cast<uint2*>(tr + col * kTs + 4 * rq) = lo;
-            *reinterpret_cast<uint2*>(tr + (col + 1) * kTs + 4 * rq) = hi;
-          }
-        }
-      }
+      T* dst = job == 0 ? dst0 : dst1;
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<uint4*>(dst + (4 * rq + j) * kRs + cc * kEpc) = r[i][j];
     }
   }
 };

@@ -1,10 +1,10 @@
 // LDS tiles and the two MFMA tile products used by the attention passes.
 //
-// A "tile" is 64 rows x D columns of a [rows, D] tensor.  bf16 tiles are
-// staged row-major (stride D+8) and, when a product needs the tile as a
-// transposed operand, also column-major (stride 64+8).  fp32 tiles are
-// staged row-major only: the fp32 MFMA takes one element per lane and k
-// slot, which a row-major tile serves without conflicts.
+// A "tile" is 64 rows x D columns of a [rows, D] tensor, staged row-major
+// in LDS (stride D+8 for bf16, D+4 for fp32).  Products that contract over
+// the tile's rows read their bf16 operand with the gfx950 transposing LDS
+// read; the fp32 MFMA takes one element per lane and k slot, which the
+// row-major tile serves directly.
 //
 //   rows_x_frag:  acc[f] (16 tile rows 16f.. x 16 lanes' columns)
 //                 = sum_d Tile[16f + i][d] * Bfrag[d][col]
@@ -21,8 +21,7 @@ namespace asa {
 
 template <typename T, int D> struct Tile;
 template <int D> struct Tile<u16, D> {
-  static constexpr int kRs = D + 8;       // row-major stride
-  static constexpr int kTs = kBlock + 8;  // transposed stride
+  static constexpr int kRs = D + 8;  // row stride (elements)
 };
 template <int D> struct Tile<float, D> {
   static constexpr int kRs = D + 4;
@@ -47,35 +46,6 @@ template <int D> struct RowFrag<float, D> {
       v[j] = ok ? *reinterpret_cast<const f32x4*>(row + 16 * j + 4 * g) : f32x4{};
   }
 };
-
-// Stage rows [row0, row0 + 64) of a [*, D] tensor (rows >= nrows read as 0)
-// with `nthr` threads; either of `rm` / `tr` may be null (bf16).
-template <int D>
-__device__ __forceinline__ void stage_tile(u16* rm, u16* tr, const u16* src, int row0, int nrows,
-                                           int t, int nthr) {
-  constexpr int kChunks = kBlock * D / 8;
-  for (int c = t; c < kChunks; c += nthr) {
-    const int r = c / (D / 8), col = (c % (D / 8)) * 8;
-    uint4 v = {0, 0, 0, 0};
-    if (row0 + r < nrows) v = *reinterpret_cast<const uint4*>(src + size_t(row0 + r) * D + col);
-    if (rm) *reinterpret_cast<uint4*>(rm + r * Tile<u16, D>::kRs + col) = v;
-    if (tr) {
-      const u16* e = reinterpret_cast<const u16*>(&v);
-      for (int i = 0; i < 8; ++i) tr[(col + i) * Tile<u16, D>::kTs + r] = e[i];
-    }
-  }
-}
-template <int D>
-__device__ __forceinline__ void stage_tile(float* rm, float*, const float* src, int row0,
-                                           int nrows, int t, int nthr) {
-  constexpr int kChunks = kBlock * D / 4;
-  for (int c = t; c < kChunks; c += nthr) {
-    const int r = c / (D / 4), col = (c % (D / 4)) * 4;
-    f32x4 v = {0, 0, 0, 0};
-    if (row0 + r < nrows) v = *reinterpret_cast<const f32x4*>(src + size_t(row0 + r) * D + col);
-    *reinterpret_cast<f32x4*>(rm + r * Tile<float, D>::kRs + col) = v;
-  }
-}
 
 template <int D>
 __device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const u16* rm,
@@ -102,15 +72,20 @@ __device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const float* rm,
     }
 }
 
-// bf16: `tr` is the transposed tile.  x is rounded to bf16; with Split,
-// x is carried as the sum of two bf16 terms (hi = bf16(x), lo = bf16(x - hi),
-// 16 significant bits), so that sums with heavy cancellation -- gradient
-// rows whose weights sum to zero against keys that share a common
-// component -- keep fp32-level accuracy at the cost of a second MFMA.
+// bf16: `rm` is the row-major tile.  The A operand (4 consecutive tile rows
+// at one column per lane and half) is read with ds_read_b64_tr_b16: in each
+// 16-lane group, lane l reads the 8 bytes at row key0 + l/4, columns
+// col0 + 4 (l % 4) .. +3, and lane c receives rows key0 .. key0 + 3 of
+// column col0 + c.  x is rounded to bf16; with Split, x is carried as the
+// sum of two bf16 terms (hi = bf16(x), lo = bf16(x - hi), 16 significant
+// bits), so that sums with heavy cancellation -- gradient rows whose
+// weights sum to zero against keys that share a common component -- keep
+// fp32-level accuracy at the cost of a second MFMA.
 template <int D, bool Split = false>
-__device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const u16* tr,
+__device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const u16* rm,
                                              const f32x4 (&x)[4], int lane) {
-  const int g = lane >> 4, c = lane & 15;
+  const int g = lane >> 4, l = lane & 15;
+  constexpr int rs = Tile<u16, D>::kRs;
   for (int cc = 0; cc < 2; ++cc) {
     bf16x8 b, bl;
     for (int r = 0; r < 4; ++r) {
@@ -121,11 +96,12 @@ __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const u16* tr,
         bl[4 + r] = static_cast<__bf16>(x[2 * cc + 1][r] - static_cast<float>(b[4 + r]));
       }
     }
+    // rows 32cc + 4g + 0..3 (low half) and 32cc + 16 + 4g + 0..3 (high half)
+    const u16* base = rm + (32 * cc + 4 * g + (l >> 2)) * rs + 4 * (l & 3);
     bf16x8 a[D / 16];
     for (int db = 0; db < D / 16; ++db) {
-      const u16* p = tr + (16 * db + c) * Tile<u16, D>::kTs + 32 * cc + 4 * g;
-      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
-      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16);
+      const bf16x4 lo = read_tr16(base + 16 * db);
+      const bf16x4 hi = read_tr16(base + 16 * rs + 16 * db);
       a[db] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       o[db] = mfma(a[db], b, o[db]);
     }

@@ -74,31 +74,17 @@ __device__ __forceinline__ float clamp10(float s) {
 // ---------------------------------------------------------------------------
 // dQ (query-major)
 // ---------------------------------------------------------------------------
-template <typename T, int D> struct DqSmem;
-template <int D> struct alignas(16) DqSmem<u16, D> {
-  static constexpr int L0 = kBothLayouts, L1 = kRowMajor;  // K, V
-  u16 K[2][kBlock * Tile<u16, D>::kRs];
-  u16 Kt[2][D * Tile<u16, D>::kTs];
-  u16 V[2][kBlock * Tile<u16, D>::kRs];
+template <typename T, int D> struct alignas(16) DqSmem {
+  T K[2][kBlock * Tile<T, D>::kRs];
+  T V[2][kBlock * Tile<T, D>::kRs];
   int kid[2][kBlock];
   int full[2];
-  __device__ u16* kt(int b) { return Kt[b]; }
-  __device__ const u16* k_operand(int b) const { return Kt[b]; }
-};
-template <int D> struct alignas(16) DqSmem<float, D> {
-  static constexpr int L0 = kRowMajor, L1 = kRowMajor;
-  float K[2][kBlock * Tile<float, D>::kRs];
-  float V[2][kBlock * Tile<float, D>::kRs];
-  int kid[2][kBlock];
-  int full[2];
-  __device__ float* kt(int) { return nullptr; }
-  __device__ const float* k_operand(int b) const { return K[b]; }
 };
 
 template <typename T, int D, int AC, bool REF>
 __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
   __shared__ DqSmem<T, D> sm;
-  using St = Stager<T, D, DqSmem<T, D>::L0, DqSmem<T, D>::L1>;
+  using St = Stager<T, D>;
   constexpr int PW = AlphaPow<AC>::W;
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
@@ -154,7 +140,7 @@ __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
     ps.load(kidx, kbase, NK, INT32_MAX, t);
   };
   auto put = [&](int b) {
-    st.store(sm.K[b], sm.kt(b), sm.V[b], nullptr, t);
+    st.store(sm.K[b], sm.V[b], t);
     ps.store<true>(sm.kid[b], &sm.full[b], qmin, t);
   };
   if (e0 < e1) {
@@ -191,8 +177,8 @@ __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
     };
     if (sm.full[b] != 0) weights(std::false_type{});
     else weights(std::true_type{});
-    tile_t_x_acc<D, true>(a1, sm.k_operand(b), sacc, lane);
-    if constexpr (!REF) tile_t_x_acc<D, true>(a2, sm.k_operand(b), dacc, lane);
+    tile_t_x_acc<D, true>(a1, sm.K[b], sacc, lane);
+    if constexpr (!REF) tile_t_x_acc<D, true>(a2, sm.K[b], dacc, lane);
     if (e + 1 < e1) {
       put(b ^ 1);
       if (e + 2 < e1) fetch(e + 2);
@@ -226,26 +212,9 @@ __global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
 // ---------------------------------------------------------------------------
 // dK, dV (key-major)
 // ---------------------------------------------------------------------------
-template <typename T, int D> struct DkvSmem;
-template <int D> struct alignas(16) DkvSmem<u16, D> {
-  static constexpr int L0 = kBothLayouts, L1 = kBothLayouts;  // Q, dO
-  u16 Q[2][kBlock * Tile<u16, D>::kRs];
-  u16 Qt[2][D * Tile<u16, D>::kTs];
-  u16 dO[2][kBlock * Tile<u16, D>::kRs];
-  u16 dOt[2][D * Tile<u16, D>::kTs];
-  __device__ u16* qt(int b) { return Qt[b]; }
-  __device__ u16* dot(int b) { return dOt[b]; }
-  __device__ const u16* q_operand(int b) const { return Qt[b]; }
-  __device__ const u16* do_operand(int b) const { return dOt[b]; }
-};
-template <int D> struct alignas(16) DkvSmem<float, D> {
-  static constexpr int L0 = kRowMajor, L1 = kRowMajor;
-  float Q[2][kBlock * Tile<float, D>::kRs];
-  float dO[2][kBlock * Tile<float, D>::kRs];
-  __device__ float* qt(int) { return nullptr; }
-  __device__ float* dot(int) { return nullptr; }
-  __device__ const float* q_operand(int b) const { return Q[b]; }
-  __device__ const float* do_operand(int b) const { return dO[b]; }
+template <typename T, int D> struct alignas(16) DkvSmem {
+  T Q[2][kBlock * Tile<T, D>::kRs];
+  T dO[2][kBlock * Tile<T, D>::kRs];
 };
 
 // Per-query constants of a query tile: tau, 1/(sum p + EPS), shift, c.
@@ -281,7 +250,7 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
   __shared__ DkvSmem<T, D> sm;
   __shared__ QConst qcs[2];
   __shared__ int full[2];
-  using St = Stager<T, D, DkvSmem<T, D>::L0, DkvSmem<T, D>::L1>;
+  using St = Stager<T, D>;
   constexpr int PP = AlphaPow<AC>::P, PW = AlphaPow<AC>::W;
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
@@ -331,7 +300,7 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
     qs.load(p, rows, rbase, qbase, NQ, t);
   };
   auto put = [&](int b) {
-    st.store(sm.Q[b], sm.qt(b), sm.dO[b], sm.dot(b), t);
+    st.store(sm.Q[b], sm.dO[b], t);
     ps.store<false>(qcs[b].pos, &full[b], kmax, t);
     qs.store(qcs[b], t);
   };
@@ -374,8 +343,8 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
     };
     if (full[b] != 0) grads(std::false_type{});
     else grads(std::true_type{});
-    tile_t_x_acc<D>(av, sm.do_operand(b), dacc, lane);
-    tile_t_x_acc<D, true>(ak, sm.q_operand(b), sacc, lane);
+    tile_t_x_acc<D>(av, sm.dO[b], dacc, lane);
+    tile_t_x_acc<D, true>(ak, sm.Q[b], sacc, lane);
     if (e + 1 < e1) {
       put(b ^ 1);
       if (e + 2 < e1) fetch(e + 2);

@@ -4,9 +4,9 @@
 // Reference: splash_forward_sparse (adasplashattention.cu:244-341), which
 // recomputes each score with one thread per query and accumulates p*v in
 // registers.  Here one 256-thread block (4 waves x 16 query rows) walks the
-// query block's CSR list.  The K tile (row-major) and the V tile
-// (transposed for bf16) of each active key block stream through
-// double-buffered LDS (asa_stage.hpp); S^T = K Q^T is formed on MFMA,
+// query block's CSR list.  The K and V tiles of each active key block
+// stream through double-buffered LDS (asa_stage.hpp); S^T = K Q^T is formed
+// on MFMA,
 // p = max(u, EPS)^(1/(alpha-1)) with u = (alpha-1) s - tau is applied in
 // registers, and O^T += V^T P^T runs on MFMA with P^T taken directly from
 // the score accumulators.  Row sums of p are kept per lane and reduced
@@ -23,28 +23,11 @@ namespace {
 
 constexpr int kThreads = 256;
 
-template <typename T, int D> struct FwdSmem;
-template <int D> struct alignas(16) FwdSmem<u16, D> {
-  static constexpr int L0 = kRowMajor, L1 = kTransposed;
-  u16 K[2][kBlock * Tile<u16, D>::kRs];
-  u16 Vt[2][D * Tile<u16, D>::kTs];
+template <typename T, int D> struct alignas(16) FwdSmem {
+  T K[2][kBlock * Tile<T, D>::kRs];
+  T V[2][kBlock * Tile<T, D>::kRs];
   int kid[2][kBlock];
   int full[2];
-  __device__ u16* k_rm(int b) { return K[b]; }
-  __device__ u16* v_rm(int) { return nullptr; }
-  __device__ u16* v_tr(int b) { return Vt[b]; }
-  __device__ const u16* v_operand(int b) const { return Vt[b]; }
-};
-template <int D> struct alignas(16) FwdSmem<float, D> {
-  static constexpr int L0 = kRowMajor, L1 = kRowMajor;
-  float K[2][kBlock * Tile<float, D>::kRs];
-  float V[2][kBlock * Tile<float, D>::kRs];
-  int kid[2][kBlock];
-  int full[2];
-  __device__ float* k_rm(int b) { return K[b]; }
-  __device__ float* v_rm(int b) { return V[b]; }
-  __device__ float* v_tr(int) { return nullptr; }
-  __device__ const float* v_operand(int b) const { return V[b]; }
 };
 
 // Clamp of a score without the operand canonicalisation fmaxf/fminf carry
@@ -58,7 +41,7 @@ __device__ __forceinline__ float clamp10(float s) {
 template <typename T, int D, int PC>
 __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   __shared__ FwdSmem<T, D> sm;
-  using St = Stager<T, D, FwdSmem<T, D>::L0, FwdSmem<T, D>::L1>;
+  using St = Stager<T, D>;
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
@@ -101,7 +84,7 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
     ps.load(kidx, kbase, NK, INT32_MAX, t);
   };
   auto put = [&](int b) {
-    st.store(sm.k_rm(b), nullptr, sm.v_rm(b), sm.v_tr(b), t);
+    st.store(sm.K[b], sm.V[b], t);
     ps.store<true>(sm.kid[b], &sm.full[b], qmin, t);
   };
   if (e0 < e1) {
@@ -129,7 +112,7 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
     };
     if (sm.full[b] != 0) weights(std::false_type{});
     else weights(std::true_type{});
-    tile_t_x_acc<D>(o, sm.v_operand(b), acc, lane);
+    tile_t_x_acc<D>(o, sm.V[b], acc, lane);
     if (e + 1 < e1) {
       put(b ^ 1);
       if (e + 2 < e1) fetch(e + 2);
