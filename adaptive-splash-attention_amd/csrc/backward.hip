@@ -81,8 +81,13 @@ template <typename T, int D> struct alignas(16) DqSmem {
   int full[2];
 };
 
+// Three waves per SIMD for bf16 at d = 64: the third wave hides part of the
+// LDS and MFMA latency.
+template <typename T, int D>
+constexpr int dq_waves_per_simd() { return sizeof(T) == 2 && D == 64 ? 3 : 1; }
+
 template <typename T, int D, int AC, bool REF>
-__global__ __launch_bounds__(kThreads) void dq_kernel(BackwardParams p) {
+__global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kernel(BackwardParams p) {
   __shared__ DqSmem<T, D> sm;
   using St = Stager<T, D>;
   constexpr int PW = AlphaPow<AC>::W;
