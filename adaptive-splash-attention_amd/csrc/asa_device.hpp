@@ -206,11 +206,22 @@ __device__ __forceinline__ int wave_reduce_minmax(int v) {
 }
 
 // Reductions across the four lane groups that share a column of a 16x16
-// accumulator (lanes L, L^16, L^32, L^48).
+// accumulator (lanes L, L^16, L^32, L^48), on the VALU: v_permlane16_swap
+// (v_permlane32_swap) applied to a value and itself leaves, in its two
+// results, the lane's value and its partner's at distance 16 (32), in an
+// order that depends on the lane.  The operation is applied to that pair,
+// so for a commutative operation every lane gets a bit-identical result.
+template <typename F>
+__device__ __forceinline__ uint32_t group_reduce_bits(uint32_t v, F op) {
+  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = op(a[0], a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return op(b[0], b[1]);
+}
 __device__ __forceinline__ float sum_groups(float v) {
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  return __uint_as_float(group_reduce_bits(__float_as_uint(v), [](uint32_t x, uint32_t y) {
+    return __float_as_uint(__uint_as_float(x) + __uint_as_float(y));
+  }));
 }
 
 }  // namespace asa

@@ -25,6 +25,7 @@ struct SelectParams {
   int32_t* topk_idx;      // optional
   float* topk_val;        // optional
   float* tkv;             // workspace: sorted top-k values, [k][BH * NQ]
+  int2* kbounds;          // workspace: (min, max) position per key block, [BH * nKB]
   int cap;                // candidate keys per row in LDS (select_capacity)
 };
 
@@ -81,6 +82,7 @@ size_t select_lds_bytes(const Dims& d, bool bf16, bool from_scores, int cap);
 // Candidate keys per row that fit `max_lds` bytes (k + 32 at most; -1 if
 // not even k + 8 fit).
 int select_capacity(const Dims& d, bool bf16, bool from_scores, size_t max_lds);
+hipError_t launch_bounds(const SelectParams& p, hipStream_t s);
 hipError_t launch_tau(const SelectParams& p, hipStream_t s);
 hipError_t launch_compact(const CompactParams& p, hipStream_t s);
 hipError_t launch_forward(const ForwardParams& p, bool bf16, hipStream_t s);

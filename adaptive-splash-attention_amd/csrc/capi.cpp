@@ -92,6 +92,13 @@ asa::Dims dims_of(const Shape& s) {
   return asa::Dims{s.BH, s.NQ, s.NK, s.D, s.k, s.nQB, s.nKB, s.alpha, s.scale};
 }
 
+// Bytes of the sorted top-k values at the start of the forward workspace,
+// rounded up so that the key-block bounds after them are 16-byte aligned.
+size_t tkv_bytes(const Shape& s) {
+  const size_t b = size_t(s.BH) * s.NQ * s.k * sizeof(float);
+  return (b + 15) & ~size_t(15);
+}
+
 void sizes_of(const Shape& s, asa_sizes* z) {
   const size_t rows = size_t(s.BH) * s.NQ;
   const size_t blocks = size_t(s.BH) * s.nQB * s.nKB;
@@ -104,8 +111,9 @@ void sizes_of(const Shape& s, asa_sizes* z) {
   z->k_list = blocks * sizeof(int32_t);
   z->topk_idx = rows * s.k * sizeof(int32_t);
   z->topk_val = rows * s.k * sizeof(float);
-  // forward: the rows' sorted top-k values; backward: two floats per row
-  const size_t fwd_ws = rows * size_t(s.k) * sizeof(float);
+  // forward: the rows' sorted top-k values and the key blocks' position
+  // bounds; backward: two floats per row
+  const size_t fwd_ws = tkv_bytes(s) + size_t(s.BH) * s.nKB * 2 * sizeof(int32_t);
   const size_t bwd_ws = 2 * rows * sizeof(float);
   z->workspace = fwd_ws > bwd_ws ? fwd_ws : bwd_ws;
 }
@@ -157,6 +165,7 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
                hipStream_t s) {
   asa::SelectParams sp{};
   sp.tkv = static_cast<float*>(workspace);
+  sp.kbounds = reinterpret_cast<int2*>(static_cast<char*>(workspace) + tkv_bytes(sh));
   if (int rc = select_cap(sh, scores != nullptr, &sp.cap)) return rc;
   sp.d = dims_of(sh);
   sp.q = q;
@@ -168,6 +177,10 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
   sp.mask = st->mask;
   sp.topk_idx = st->topk_idx;
   sp.topk_val = st->topk_val;
+  asa::profile_begin("bounds", s);
+  hipError_t eb = asa::launch_bounds(sp, s);
+  asa::profile_end(s);
+  if (int rc = check_hip(eb, "bounds kernel launch")) return rc;
   asa::profile_begin(scores ? "select_scores" : "select", s);
   hipError_t e = asa::launch_select(sp, sh.bf16, scores != nullptr, s);
   asa::profile_end(s);

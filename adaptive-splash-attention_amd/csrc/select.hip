@@ -49,17 +49,17 @@ __device__ __forceinline__ int wave_min(int v) { return wave_reduce_minmax<false
 __device__ __forceinline__ int wave_max(int v) { return wave_reduce_minmax<true>(v); }
 // Reductions over the 4 lanes (L, L^16, L^32, L^48) that share a row.
 __device__ __forceinline__ int group_sum(int v) {
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 32, kWave);
-  return v;
+  return int(group_reduce_bits(uint32_t(v), [](uint32_t x, uint32_t y) { return x + y; }));
 }
 __device__ __forceinline__ float group_min(float v) {
-  v = fminf(v, __shfl_xor(v, 16, kWave));
-  return fminf(v, __shfl_xor(v, 32, kWave));
+  return __uint_as_float(group_reduce_bits(__float_as_uint(v), [](uint32_t x, uint32_t y) {
+    return __float_as_uint(fminf(__uint_as_float(x), __uint_as_float(y)));
+  }));
 }
 __device__ __forceinline__ float group_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, kWave));
-  return fmaxf(v, __shfl_xor(v, 32, kWave));
+  return __uint_as_float(group_reduce_bits(__float_as_uint(v), [](uint32_t x, uint32_t y) {
+    return __float_as_uint(fmaxf(__uint_as_float(x), __uint_as_float(y)));
+  }));
 }
 // v_max_f32 without the operand canonicalisation that fmaxf() carries (the
 // inputs are MFMA results or -inf, never signalling NaNs); NaN loses.
@@ -312,7 +312,7 @@ enum SweepMode : int {
 
 // LDS layout, shared by the kernel and the host-side size query.
 struct SelLayout {
-  int tiles, tk, cand, tkey, cnt, ctl, bits, vlist, kvis, total;
+  int tiles, tk, cand, tkey, cnt, ctl, bits, vlist, total;
 };
 __host__ __device__ inline int align_up(int x, int a) { return (x + a - 1) / a * a; }
 __host__ __device__ inline SelLayout sel_layout(int k, int cap, int nKB, int D, int tbytes,
@@ -331,8 +331,7 @@ __host__ __device__ inline SelLayout sel_layout(int k, int cap, int nKB, int D, 
   l.ctl = l.cnt + kBlock * 4;
   l.bits = l.ctl + 16;
   l.vlist = l.bits + align_up((nKB + 31) / 32 * 4, 16);
-  l.kvis = l.vlist + align_up(nKB * 4, 16);
-  l.total = align_up(l.kvis + nKB, 16);
+  l.total = l.vlist + align_up(nKB * 4, 16);
   return l;
 }
 
@@ -353,7 +352,6 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
   uint32_t* s_ctl = reinterpret_cast<uint32_t*>(smem + lay.ctl);
   uint32_t* s_bits = reinterpret_cast<uint32_t*>(smem + lay.bits);
   int32_t* s_vlist = reinterpret_cast<int32_t*>(smem + lay.vlist);
-  uint8_t* s_kvis = smem + lay.kvis;
   constexpr int kTileElems = kBlock * KStage<T, D>::kRs;
 
   const int t = threadIdx.x, w = t >> 6, L = t & 63, g = L >> 4, c = L & 15;
@@ -376,32 +374,19 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
   for (int i = t; i < nbw; i += kThreads) s_bits[i] = 0u;
 
   const int32_t* kidx = p.k_idx + size_t(bh) * NK;
-  // Visibility class of every key block: 0 no key visible to any row of the
-  // block, 1 partially visible, 2 every key visible to every row.  Four
-  // blocks per wave step keep four loads in flight.
-  for (int kt0 = 4 * w; kt0 < nKB; kt0 += 16) {
-    int kid[4];
-    bool kin[4];
-    for (int j = 0; j < 4; ++j) {
-      const int kl = (kt0 + j) * kBlock + L;
-      kin[j] = kt0 + j < nKB && kl < NK;
-      kid[j] = kin[j] ? kidx[kl] : 0;
-    }
-    for (int j = 0; j < 4; ++j) {
-      const int kt = kt0 + j;
-      const int kmin = wave_min(kin[j] ? kid[j] : INT_MAX);
-      const int kmax = wave_max(kin[j] ? kid[j] : INT_MIN);
-      if (kt < nKB && L == 0)
-        s_kvis[kt] = kmin > qmax_blk ? 0 : ((kmax > qmin_blk || (kt + 1) * kBlock > NK) ? 1 : 2);
-    }
-  }
-  __syncthreads();
-  // Visible key blocks in ascending order: entry = block | class << 24.
+  // Visible key blocks in ascending order, entry = block | class << 24, with
+  // class 1 (partially visible: per-key tests needed) or 2 (every key
+  // visible to every row), from the blocks' position bounds.
   if (w == 0) {
+    const int2* kbnd = p.kbounds + size_t(bh) * nKB;
     int n = 0;
     for (int base = 0; base < nKB; base += kWave) {
       const int kt = base + L;
-      const int v = kt < nKB ? s_kvis[kt] : 0;
+      int v = 0;
+      if (kt < nKB) {
+        const int2 kb = kbnd[kt];
+        v = kb.x > qmax_blk ? 0 : ((kb.y > qmin_blk || (kt + 1) * kBlock > NK) ? 1 : 2);
+      }
       const uint64_t m = __ballot(v != 0);
       const int before = __builtin_popcountll(m & ((uint64_t(1) << L) - 1));
       if (v != 0) s_vlist[n + before] = kt | (v << 24);
@@ -662,6 +647,21 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
   }
 }
 
+// Smallest and largest position of every 64-key block of every (batch,
+// head): kbounds[bh * nKB + kb] = (min, max) over the block's keys < NK.
+// One wave per key block.
+__global__ __launch_bounds__(kThreads) void bounds_kernel(SelectParams p) {
+  const int nKB = p.d.nKB, NK = p.d.NK;
+  const int blk = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6);
+  if (blk >= p.d.BH * nKB) return;  // wave-uniform
+  const int bh = blk / nKB, kb = blk % nKB, L = threadIdx.x & 63;
+  const int key = kb * kBlock + L;
+  const int pos = key < NK ? p.k_idx[size_t(bh) * NK + key] : 0;
+  const int mn = wave_min(key < NK ? pos : INT_MAX);
+  const int mx = wave_max(key < NK ? pos : INT_MIN);
+  if (L == 0) p.kbounds[blk] = int2{mn, mx};
+}
+
 // tau of every row from its sorted top-k values (one thread per row):
 // tkv[e * rows + row], e < k.
 template <int AC>
@@ -689,6 +689,7 @@ hipError_t launch_one(const SelectParams& p, hipStream_t s) {
 // larger k, the more candidates a loose floor admits.
 template <typename T, int D, int MODE>
 hipError_t launch_r(const SelectParams& p, hipStream_t s) {
+  if (p.d.k <= 32) return launch_one<T, D, MODE, 2>(p, s);
   if (p.d.k <= 64) return launch_one<T, D, MODE, 4>(p, s);
   return launch_one<T, D, MODE, 8>(p, s);
 }
@@ -703,6 +704,13 @@ int tbytes_of(bool bf16) { return bf16 ? 2 : 4; }
 int dim_of(const Dims& d, bool from_scores) { return from_scores ? 64 : d.D; }
 
 }  // namespace
+
+hipError_t launch_bounds(const SelectParams& p, hipStream_t s) {
+  const int blocks = p.d.BH * p.d.nKB;
+  const int per = kThreads / kWave;
+  hipLaunchKernelGGL(bounds_kernel, dim3(unsigned((blocks + per - 1) / per)), dim3(kThreads), 0, s, p);
+  return hipGetLastError();
+}
 
 hipError_t launch_tau(const SelectParams& p, hipStream_t s) {
   const size_t rows = size_t(p.d.BH) * p.d.NQ;

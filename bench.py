@@ -63,6 +63,7 @@ def kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep):
                        bytes=rows * d * ELEM + vis_blocks * tile + rows * k_keep * 4
                        + BH * nQB * nKB),
         "tau": dict(bound="hbm", flops=0.0, bytes=rows * k_keep * 4 + rows * 4),
+        "bounds": dict(bound="hbm", flops=0.0, bytes=BH * N * 4 + BH * nKB * 8),
         "compact": dict(bound="hbm", flops=0.0, bytes=2 * BH * nQB * nKB + csr),
         "forward": dict(bound="hbm", flops=4.0 * 64 * 64 * d * nnzb,
                         bytes=nnzb * 2 * tile + 2 * rows * d * ELEM + 2 * rows * 4
