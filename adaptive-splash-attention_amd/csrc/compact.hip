@@ -5,9 +5,9 @@
 // (batch, head).  Here one 256-thread block per (batch, head) builds both
 //   query-major:  q_ptr[nQB+1], q_list[nQB*nKB]  (same layout as Qi_ptr/Qi_idx)
 //   key-major:    k_ptr[nKB+1], k_list[nKB*nQB]  (feeds the atomic-free dK/dV)
-// with lists in ascending block order and zero-filled tails.  Row / column
-// counts are computed in parallel, offsets by a block-wide scan, and each
-// row / column is then written by one thread.
+// with lists in ascending block order and zero-filled tails.  A wave takes
+// one row (column) of the mask at a time, 64 entries per step: one load per
+// lane, a ballot, and the set lanes write their block index at their rank.
 #include "asa_device.hpp"
 #include "asa_launch.hpp"
 
@@ -15,78 +15,79 @@ namespace asa {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
 
-// Exclusive scan of cnt[0..n) into ptr[0..n] (ptr[n] = total), in LDS.
-__device__ void block_scan(const int* cnt, int* ptr_lds, int n) {
-  __shared__ int partial[kThreads + 1];
+// Exclusive scan of cnt[0..n) into ptr[0..n] (ptr[n] = total), in LDS, by
+// the first wave, 64 entries per step.
+__device__ void block_scan(const int* cnt, int* ptr, int n) {
   const int t = threadIdx.x;
-  const int per = (n + kThreads - 1) / kThreads;
-  const int b = min(n, t * per), e = min(n, b + per);
-  int s = 0;
-  for (int i = b; i < e; ++i) s += cnt[i];
-  partial[t] = s;
-  __syncthreads();
-  if (t == 0) {
+  if (t < kWave) {
     int run = 0;
-    for (int i = 0; i < kThreads; ++i) {
-      const int v = partial[i];
-      partial[i] = run;
-      run += v;
+    for (int base = 0; base < n; base += kWave) {
+      const int i = base + t;
+      const int v = i < n ? cnt[i] : 0;
+      int x = v;  // inclusive scan over the wave
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int y = __shfl_up(x, o, kWave);
+        if (t >= o) x += y;
+      }
+      if (i < n) ptr[i] = run + x - v;
+      run += __shfl(x, kWave - 1, kWave);
     }
-    partial[kThreads] = run;
+    if (t == 0) ptr[n] = run;
   }
   __syncthreads();
-  int run = partial[t];
-  for (int i = b; i < e; ++i) {
-    ptr_lds[i] = run;
-    run += cnt[i];
+}
+
+// Row i of a row-major [rows, cols] byte mask (stride `rs`, element stride
+// `es`): counts (pass 0) or writes the ascending indices of the set entries
+// at out[0..) (pass 1).  One wave; returns the count.
+__device__ __forceinline__ int scan_line(const uint8_t* m, size_t rs, size_t es, int i, int n,
+                                         int32_t* out, int L) {
+  int c = 0;
+  for (int base = 0; base < n; base += kWave) {
+    const int j = base + L;
+    const bool set = j < n && m[size_t(i) * rs + size_t(j) * es] != 0;
+    const uint64_t bits = __ballot(set);
+    if (out && set) out[c + __builtin_popcountll(bits & ((uint64_t(1) << L) - 1))] = j;
+    c += __builtin_popcountll(bits);
   }
-  if (t == 0) ptr_lds[n] = partial[kThreads];
-  __syncthreads();
+  return c;
 }
 
 __global__ __launch_bounds__(kThreads) void compact_kernel(CompactParams p) {
   extern __shared__ int sm[];
   const int nQB = p.nQB, nKB = p.nKB, bh = blockIdx.x, t = threadIdx.x;
+  const int w = t >> 6, L = t & 63;
   const uint8_t* m = p.mask + size_t(bh) * nQB * nKB;
   int* cnt = sm;                  // max(nQB, nKB)
   int* ptr = sm + max(nQB, nKB);  // max(nQB, nKB) + 1
 
-  // ---- query-major ----
-  for (int i = t; i < nQB; i += kThreads) {
-    int c = 0;
-    for (int j = 0; j < nKB; ++j) c += m[size_t(i) * nKB + j];
-    cnt[i] = c;
+  // ---- query-major: rows of the mask ----
+  for (int i = w; i < nQB; i += kWaves) {
+    const int c = scan_line(m, nKB, 1, i, nKB, nullptr, L);
+    if (L == 0) cnt[i] = c;
   }
   __syncthreads();
   block_scan(cnt, ptr, nQB);
   int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
   int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
   for (int i = t; i <= nQB; i += kThreads) qp[i] = ptr[i];
-  for (int i = t; i < nQB; i += kThreads) {
-    int w = ptr[i];
-    for (int j = 0; j < nKB; ++j)
-      if (m[size_t(i) * nKB + j]) ql[w++] = j;
-  }
+  for (int i = w; i < nQB; i += kWaves) scan_line(m, nKB, 1, i, nKB, ql + ptr[i], L);
   for (int e = ptr[nQB] + t; e < nQB * nKB; e += kThreads) ql[e] = 0;
   __syncthreads();
 
-  // ---- key-major ----
-  for (int j = t; j < nKB; j += kThreads) {
-    int c = 0;
-    for (int i = 0; i < nQB; ++i) c += m[size_t(i) * nKB + j];
-    cnt[j] = c;
+  // ---- key-major: columns of the mask ----
+  for (int j = w; j < nKB; j += kWaves) {
+    const int c = scan_line(m, 1, nKB, j, nQB, nullptr, L);
+    if (L == 0) cnt[j] = c;
   }
   __syncthreads();
   block_scan(cnt, ptr, nKB);
   int32_t* kp = p.k_ptr + size_t(bh) * (nKB + 1);
   int32_t* kl = p.k_list + size_t(bh) * nKB * nQB;
   for (int j = t; j <= nKB; j += kThreads) kp[j] = ptr[j];
-  for (int j = t; j < nKB; j += kThreads) {
-    int w = ptr[j];
-    for (int i = 0; i < nQB; ++i)
-      if (m[size_t(i) * nKB + j]) kl[w++] = i;
-  }
+  for (int j = w; j < nKB; j += kWaves) scan_line(m, 1, nKB, j, nQB, kl + ptr[j], L);
   for (int e = ptr[nKB] + t; e < nQB * nKB; e += kThreads) kl[e] = 0;
 }
 

@@ -130,18 +130,18 @@ __device__ __forceinline__ void segment_sort_desc(uint64_t (&v)[8], int lane) {
   });
 }
 
-// tau from the sorted top-k values of one row, tk[j * stride + lq] (best first),
-// following the reference recurrence step by step
+// tau from the sorted top-k values of one row (best first), s(j) for
+// j < k, following the reference recurrence step by step
 // (adasplashattention.cu:51-125): bracket from the extreme kept values,
 // midpoint start, up to five rounds of {f, f', f'' over the leading positive
 // terms; exit when |f| < 1e-4; Halley step with the reference's f''
 // coefficient a(a + 1 - alpha); bracket midpoint when the step leaves the
 // bracket; bracket update from f at the new point; clamp}.  No contraction,
-// powers via pow_exact: bit-identical to the CPU oracle on equal inputs.
-// The sorted values are read four at a time so that one LDS round trip
-// serves four terms.
-template <int AC>
-__device__ float entmax_tau(const float* tk, size_t stride, size_t lq, int k, float alpha_in) {
+// powers in the exponent classes of alpha (pow_exact_c): bit-identical to
+// the CPU oracle on equal inputs.  KMAX > 0: the caller guarantees k <= KMAX
+// and s(j) is a compile-time-indexed register, so the loops are unrolled.
+template <int AC, int KMAX, typename S>
+__device__ float entmax_tau(S s, int k, float alpha_in) {
 #pragma clang fp contract(off)
   constexpr int PA = AlphaPow<AC>::P, P1 = AlphaPow<AC>::W, P2 = AlphaPow<AC>::V;
   const float alpha = fmaxf(1.05f, fminf(alpha_in, 3.0f));
@@ -150,22 +150,18 @@ __device__ float entmax_tau(const float* tk, size_t stride, size_t lq, int k, fl
   const float e1 = (2.0f - alpha) * a;
   const float e2 = (3.0f - 2.0f * alpha) * a;
   const float c2 = a * ((a + 1.0f) - alpha);
-  const float top = tk[lq];
-  const float bottom = tk[size_t(k - 1) * stride + lq];
+  const float top = s(0);
+  const float bottom = s(k - 1);
   float lo = am1 * bottom - 2.0f;
   float hi = am1 * top + 2.0f;
   float tau = 0.5f * (lo + hi);
   for (int it = 0; it < 5; ++it) {
     float f = -1.0f, df = 0.0f, d2f = 0.0f;
-    float buf[4];
-    for (int j = 0; j < k; ++j) {
-      if ((j & 3) == 0)
-        for (int i = 0; i < 4; ++i) buf[i] = tk[size_t(min(j + i, k - 1)) * stride + lq];
-      float sj = buf[0];
-      for (int i = 1; i < 4; ++i)
-        if (i == (j & 3)) sj = buf[i];
-      const float u = am1 * sj - tau;
-      if (u <= 0.0f) break;
+    // one term of f, f', f''; false once the terms end
+    auto term = [&](int j) {
+      if (j >= k) return false;
+      const float u = am1 * s(j) - tau;
+      if (u <= 0.0f) return false;
       const float ue = fmaxf(u, kEps);
       float t = pow_exact_c<PA>(ue, a);
       if (!finite(t)) t = 0.0f;
@@ -174,6 +170,15 @@ __device__ float entmax_tau(const float* tk, size_t stride, size_t lq, int k, fl
       if (finite(t1)) df = df + t1;
       const float t2 = c2 * pow_exact_c<P2>(ue, e2);
       if (finite(t2)) d2f = d2f + t2;
+      return true;
+    };
+    if constexpr (KMAX > 0) {
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j)
+        if (!term(j)) break;
+    } else {
+      for (int j = 0; term(j); ++j) {
+      }
     }
     if (fabsf(f) < 1e-4f) break;
     float next = tau;
@@ -183,16 +188,21 @@ __device__ float entmax_tau(const float* tk, size_t stride, size_t lq, int k, fl
     }
     if (!(next >= lo && next <= hi)) next = 0.5f * (lo + hi);
     float gsum = -1.0f;
-    for (int j = 0; j < k; ++j) {
-      if ((j & 3) == 0)
-        for (int i = 0; i < 4; ++i) buf[i] = tk[size_t(min(j + i, k - 1)) * stride + lq];
-      float sj = buf[0];
-      for (int i = 1; i < 4; ++i)
-        if (i == (j & 3)) sj = buf[i];
-      const float u = am1 * sj - next;
-      if (u <= 0.0f) break;
+    auto gterm = [&](int j) {
+      if (j >= k) return false;
+      const float u = am1 * s(j) - next;
+      if (u <= 0.0f) return false;
       const float t = pow_exact_c<PA>(fmaxf(u, kEps), a);
       if (finite(t)) gsum = gsum + t;
+      return true;
+    };
+    if constexpr (KMAX > 0) {
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j)
+        if (!gterm(j)) break;
+    } else {
+      for (int j = 0; gterm(j); ++j) {
+      }
     }
     if (gsum > 0.0f) lo = next;
     else hi = next;
@@ -664,12 +674,21 @@ __global__ __launch_bounds__(kThreads) void bounds_kernel(SelectParams p) {
 
 // tau of every row from its sorted top-k values (one thread per row):
 // tkv[e * rows + row], e < k.
-template <int AC>
+template <int AC, int KMAX>
 __global__ __launch_bounds__(kThreads) void tau_kernel(SelectParams p) {
   const size_t rows = size_t(p.d.BH) * p.d.NQ;
   const size_t r = size_t(blockIdx.x) * kThreads + threadIdx.x;
   if (r >= rows) return;
-  p.taus[r] = entmax_tau<AC>(p.tkv, rows, r, p.d.k, p.d.alpha);
+  const int k = p.d.k;
+  const float* v = p.tkv + r;
+  if constexpr (KMAX > 0) {
+    float reg[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) reg[j] = j < k ? v[size_t(j) * rows] : 0.0f;
+    p.taus[r] = entmax_tau<AC, KMAX>([&](int j) { return reg[j]; }, k, p.d.alpha);
+  } else {
+    p.taus[r] = entmax_tau<AC, 0>([&](int j) { return v[size_t(j) * rows]; }, k, p.d.alpha);
+  }
 }
 
 template <typename T, int D, int MODE, int R>
@@ -715,11 +734,24 @@ hipError_t launch_bounds(const SelectParams& p, hipStream_t s) {
 hipError_t launch_tau(const SelectParams& p, hipStream_t s) {
   const size_t rows = size_t(p.d.BH) * p.d.NQ;
   const dim3 grid(unsigned((rows + kThreads - 1) / kThreads));
+  const bool reg = p.d.k <= 32;  // the row's values fit in registers
   switch (alpha_class_of(p.d.alpha)) {
-    case kA15: hipLaunchKernelGGL(tau_kernel<kA15>, grid, dim3(kThreads), 0, s, p); break;
-    case kA20: hipLaunchKernelGGL(tau_kernel<kA20>, grid, dim3(kThreads), 0, s, p); break;
-    case kA125: hipLaunchKernelGGL(tau_kernel<kA125>, grid, dim3(kThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL(tau_kernel<kAGen>, grid, dim3(kThreads), 0, s, p); break;
+    case kA15:
+      if (reg) hipLaunchKernelGGL((tau_kernel<kA15, 32>), grid, dim3(kThreads), 0, s, p);
+      else hipLaunchKernelGGL((tau_kernel<kA15, 0>), grid, dim3(kThreads), 0, s, p);
+      break;
+    case kA20:
+      if (reg) hipLaunchKernelGGL((tau_kernel<kA20, 32>), grid, dim3(kThreads), 0, s, p);
+      else hipLaunchKernelGGL((tau_kernel<kA20, 0>), grid, dim3(kThreads), 0, s, p);
+      break;
+    case kA125:
+      if (reg) hipLaunchKernelGGL((tau_kernel<kA125, 32>), grid, dim3(kThreads), 0, s, p);
+      else hipLaunchKernelGGL((tau_kernel<kA125, 0>), grid, dim3(kThreads), 0, s, p);
+      break;
+    default:
+      if (reg) hipLaunchKernelGGL((tau_kernel<kAGen, 32>), grid, dim3(kThreads), 0, s, p);
+      else hipLaunchKernelGGL((tau_kernel<kAGen, 0>), grid, dim3(kThreads), 0, s, p);
+      break;
   }
   return hipGetLastError();
 }
