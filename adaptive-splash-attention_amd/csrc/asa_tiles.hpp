@@ -12,7 +12,10 @@
 //                 += sum_r Tile[r][16db + i] * X[r][col]
 //                 where X is given in the accumulator layout of rows_x_frag
 //                 (the row index r plays the MFMA k role; lane group g holds
-//                 rows 16f + 4g + 0..3 of each block f).
+//                 rows 16f + 4g + 0..3 of each block f).  Template bounds
+//                 [CC0, CC1) restrict it to the row halves 32cc..32cc+31
+//                 (blocks f = 2cc, 2cc+1), so a caller can feed each half as
+//                 soon as it is formed.
 #pragma once
 
 #include "asa_device.hpp"
@@ -81,12 +84,12 @@ __device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const float* rm,
 // bits), so that sums with heavy cancellation -- gradient rows whose
 // weights sum to zero against keys that share a common component -- keep
 // fp32-level accuracy at the cost of a second MFMA.
-template <int D, bool Split = false>
+template <int D, bool Split = false, int CC0 = 0, int CC1 = 2>
 __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const u16* rm,
                                              const f32x4 (&x)[4], int lane) {
   const int g = lane >> 4, l = lane & 15;
   constexpr int rs = Tile<u16, D>::kRs;
-  for (int cc = 0; cc < 2; ++cc) {
+  for (int cc = CC0; cc < CC1; ++cc) {
     bf16x8 b, bl;
     for (int r = 0; r < 4; ++r) {
       b[r] = static_cast<__bf16>(x[2 * cc][r]);
@@ -112,11 +115,11 @@ __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const u16* rm,
   }
 }
 // fp32: `rm` is the row-major tile (exact operands; Split has no effect).
-template <int D, bool Split = false>
+template <int D, bool Split = false, int CC0 = 0, int CC1 = 2>
 __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const float* rm,
                                              const f32x4 (&x)[4], int lane) {
   const int g = lane >> 4, c = lane & 15;
-  for (int f = 0; f < 4; ++f)
+  for (int f = 2 * CC0; f < 2 * CC1; ++f)
     for (int r = 0; r < 4; ++r) {
       const float* p = rm + (16 * f + 4 * g + r) * Tile<float, D>::kRs + c;
       for (int db = 0; db < D / 16; ++db) o[db] = mfma(p[16 * db], x[f][r], o[db]);

@@ -81,8 +81,8 @@ template <typename T, int D> struct alignas(16) DqSmem {
   int full[2];
 };
 
-// Three waves per SIMD for bf16 at d = 64: the third wave hides part of the
-// LDS and MFMA latency.
+// Three waves per SIMD for bf16 at d = 64 (dQ and dK/dV): the third wave
+// hides part of the LDS and MFMA latency.
 template <typename T, int D>
 constexpr int dq_waves_per_simd() { return sizeof(T) == 2 && D == 64 ? 3 : 1; }
 
@@ -251,7 +251,7 @@ struct QConstStager {
 };
 
 template <typename T, int D, int AC, bool REF>
-__global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
+__global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dkdv_kernel(BackwardParams p) {
   __shared__ DkvSmem<T, D> sm;
   __shared__ QConst qcs[2];
   __shared__ int full[2];
@@ -321,8 +321,8 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
     f32x4 sacc[4], dacc[4];
     rows_x_frag<D>(sacc, sm.Q[b], kf, lane);
     rows_x_frag<D>(dacc, sm.dO[b], vf, lane);
-    auto grads = [&](auto partial) {
-      for (int f = 0; f < 4; ++f) {
+    auto grads = [&](auto partial, int fb) {
+      for (int f = fb; f < fb + 2; ++f) {
         // constants of queries 16f + 4g + 0..3
         const int q4 = 16 * f + 4 * g;
         const f32x4 tau4 = *reinterpret_cast<const f32x4*>(&qc.tau[q4]);
@@ -346,10 +346,18 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(BackwardParams p) {
         }
       }
     };
-    if (full[b] != 0) grads(std::false_type{});
-    else grads(std::true_type{});
-    tile_t_x_acc<D>(av, sm.dO[b], dacc, lane);
-    tile_t_x_acc<D, true>(ak, sm.Q[b], sacc, lane);
+    const bool tile_full = full[b] != 0;
+    // two halves (score rows 16f.., f = 0,1 then 2,3): each half's P and ds
+    // feed their products before the next half is formed, which keeps the
+    // register footprint within three waves per SIMD
+    if (tile_full) grads(std::false_type{}, 0);
+    else grads(std::true_type{}, 0);
+    tile_t_x_acc<D, false, 0, 1>(av, sm.dO[b], dacc, lane);
+    tile_t_x_acc<D, true, 0, 1>(ak, sm.Q[b], sacc, lane);
+    if (tile_full) grads(std::false_type{}, 2);
+    else grads(std::true_type{}, 2);
+    tile_t_x_acc<D, false, 1, 2>(av, sm.dO[b], dacc, lane);
+    tile_t_x_acc<D, true, 1, 2>(ak, sm.Q[b], sacc, lane);
     if (e + 1 < e1) {
       put(b ^ 1);
       if (e + 2 < e1) fetch(e + 2);
