@@ -43,7 +43,7 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # HBM bytes per launch of each kernel at this workload, measured with
 # rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), the factors a plain
 # 256 MiB device copy gives (profiles/headline_hbm_traffic.md).
-HBM_TRAFFIC = {'select': 104480800, 'tau': 40939296, 'compact': 2456064, 'forward': 139069312, 'bwd_dq': 174430251, 'bwd_dkdv': 207871317}
+HBM_TRAFFIC = {'bounds': 1107968, 'select': 104310512, 'tau': 34701568, 'compact': 2464256, 'forward': 139069984, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
 
 
 def effective_flops(B, H, N, d):
