@@ -1,5 +1,11 @@
 """Autograd wiring and the functional form of splash attention.
 
+Under ``torch.compile``, ``splash_attention`` calls the ``adasplash::forward``
+custom operator (library.py), whose autograd formula runs
+``adasplash::backward``; eagerly it uses ``SplashAttentionFunction``, the
+same pairing as a plain autograd function, which skips the operator
+dispatch.
+
 The reference exposes only separate native forward/backward calls and no
 autograd wrapper (adasplashattention.cu:702-705); its README promises an
 ``AdaptiveSplashAttention`` module (README.md:102-124).  Here the forward
@@ -12,7 +18,7 @@ from __future__ import annotations
 import torch
 from torch.autograd.function import once_differentiable
 
-from . import ops
+from . import library, ops
 
 
 class SplashAttentionFunction(torch.autograd.Function):
@@ -46,6 +52,9 @@ def splash_attention(Q, K, V, Q_idx=None, K_idx=None, alpha: float = 1.5, k_keep
     """
     if grad_mode not in ops.GRAD_MODES:
         raise ValueError(f"grad_mode must be one of {sorted(ops.GRAD_MODES)}")
+    if torch.compiler.is_compiling():
+        return library.attention(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode)
+    # eager: the autograd function, without the custom-operator dispatch
     Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     if sm_scale is None:
         sm_scale = Q.size(-1) ** -0.5

@@ -82,8 +82,9 @@ def _index(idx, BH: int, N: int, B: int, H: int, device, name: str) -> torch.Ten
     return idx.contiguous()
 
 
-def check_inputs(Q, K, V, Q_idx=None, K_idx=None):
-    """Validate and normalise (Q, K, V, Q_idx, K_idx); returns contiguous tensors."""
+def check_shapes(Q, K, V, k_keep=None):
+    """The reference's argument checks (adasplashattention.cu:542-558) that
+    need no tensor data: ranks, shapes, dtypes, head dimension, device."""
     for name, t in (("Q", Q), ("K", K), ("V", V)):
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"{name} must be a tensor")
@@ -109,6 +110,15 @@ def check_inputs(Q, K, V, Q_idx=None, K_idx=None):
         raise RuntimeError("Tensors must be on CUDA device")
     if K.device != Q.device or V.device != Q.device:
         raise RuntimeError("All tensors must be on same device")
+    if k_keep is not None and not (1 <= int(k_keep) <= MAX_K_KEEP):
+        raise ValueError(f"k_keep {k_keep} out of range [1, {MAX_K_KEEP}]")
+
+
+def check_inputs(Q, K, V, Q_idx=None, K_idx=None):
+    """Validate and normalise (Q, K, V, Q_idx, K_idx); returns contiguous tensors."""
+    check_shapes(Q, K, V)
+    B, H, NQ, _ = Q.shape
+    NK = K.shape[2]
     BH = B * H
     qi = _index(Q_idx, BH, NQ, B, H, Q.device, "Q_idx")
     ki = _index(K_idx, BH, NK, B, H, Q.device, "K_idx")

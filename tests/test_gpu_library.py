@@ -1,0 +1,40 @@
+"""The custom operators on the GPU: opcheck, and torch.compile (graph
+capture through the fake implementations, aot_eager backend) giving the
+eager result bit for bit."""
+import pytest
+import torch
+
+import splash_attention as sa
+from splash_attention import library
+from tests._util import causal_idx, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def test_opcheck_forward(dev):
+    print("[lib] opcheck forward fp32 1x2x128x64", flush=True)
+    Q, K, V, _ = make_inputs(1, 2, 128, 128, 64, seed=11)
+    args = (Q.to(dev), K.to(dev), V.to(dev), None, None, 1.5, 8, 0.125, "entmax")
+    torch.library.opcheck(library.forward_op, args,
+                          test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_compile_matches_eager(dev, dtype):
+    print(f"[lib] torch.compile aot_eager {dtype}", flush=True)
+    B, H, N, d = 1, 2, 192, 64
+    Q, K, V, dO = make_inputs(B, H, N, N, d, seed=12, dtype=dtype)
+    idx = causal_idx(B * H, N).to(dev)
+    attn = sa.AdaptiveSplashAttention(head_dim=64, alpha=1.5, k_keep=16, sm_scale=0.125)
+
+    def run(fn):
+        q, k, v = (t.to(dev).requires_grad_(True) for t in (Q, K, V))
+        out = fn(q, k, v, idx, idx)
+        out.backward(dO.to(dev))
+        torch.cuda.synchronize()
+        return [x.detach().cpu() for x in (out, q.grad, k.grad, v.grad)]
+
+    eager = run(attn)
+    compiled = run(torch.compile(attn, backend="aot_eager", fullgraph=True))
+    for a, b in zip(eager, compiled):
+        assert torch.equal(a, b)

@@ -1,0 +1,23 @@
+"""torch.library registration (CPU): the custom operators exist and their
+fake implementations give the shapes and dtypes the kernels produce."""
+import torch
+
+import splash_attention  # noqa: F401  (registers adasplash::forward / ::backward)
+
+
+def test_ops_registered():
+    assert hasattr(torch.ops.adasplash, "forward")
+    assert hasattr(torch.ops.adasplash, "backward")
+
+
+def test_fake_shapes_on_meta_tensors():
+    Q = torch.empty(2, 3, 200, 64, device="meta", dtype=torch.bfloat16)
+    K = torch.empty(2, 3, 130, 64, device="meta", dtype=torch.bfloat16)
+    outs = torch.ops.adasplash.forward(Q, K, K, None, None, 1.5, 8, 0.125, "entmax")
+    shapes = [(tuple(o.shape), o.dtype) for o in outs]
+    assert shapes == [((2, 3, 200, 64), torch.bfloat16), ((6, 200), torch.float32),
+                      ((6, 200), torch.float32), ((6, 4, 3), torch.uint8), ((6, 5), torch.int32),
+                      ((6, 12), torch.int32), ((6, 4), torch.int32), ((6, 12), torch.int32)]
+    g = torch.ops.adasplash.backward(Q, K, K, None, None, outs[0], outs[0], *outs[1:], 1.5, 8,
+                                     0.125, "entmax")
+    assert [tuple(x.shape) for x in g] == [(2, 3, 200, 64), (2, 3, 130, 64), (2, 3, 130, 64)]
