@@ -1,0 +1,192 @@
+"""Benchmark CLI with the metric set of the reference notebook.
+
+The reference's harness (AdaSplashNotebook.ipynb, ``BenchmarkResult`` and
+``benchmark_single_config``, nb:1688-1830) times its extension against a
+dense attention and reports, per configuration: both times, the speed-up,
+MSE / max absolute error / cosine similarity of the outputs, and the GPU
+memory each one allocates.  This module reports the same fields for
+``splash_attention`` against either
+
+* ``entmax``  -- dense exact alpha-entmax attention in PyTorch (materialised
+  scores, tau by bisection to float precision), the function the sparse
+  attention approximates, or
+* ``vanilla`` -- the notebook's ``vanilla_attention`` formula (softmax of
+  scores / alpha, raised to alpha, renormalised), kept for comparison with
+  the notebook's numbers.
+
+Inputs follow the notebook's conventions: N(0, 1) * ``--input-scale``
+(the notebook used 0.1), causal int32 ``arange`` positions, sm_scale =
+1/sqrt(d).  ``--backward`` times forward + backward instead of the forward.
+
+    python -m splash_attention.benchmark --config 1x4x2048x64 --config 1x4x4096x64
+"""
+from __future__ import annotations
+
+import argparse
+import gc
+import json
+import math
+import time
+
+import torch
+
+from .function import splash_attention
+
+
+def dense_entmax_attention(Q, K, V, alpha: float, sm_scale: float, iters: int = 40):
+    """Exact alpha-entmax attention over causal scores (fp32 math); tau by
+    bisection on [max - 1, max] of (alpha-1) * scores, iters steps."""
+    q, k, v = (t.float() for t in (Q, K, V))
+    S = torch.matmul(q, k.transpose(-1, -2).contiguous()) * sm_scale
+    NQ, NK = S.shape[-2:]
+    causal = torch.ones(NQ, NK, device=S.device, dtype=torch.bool).tril_(NK - NQ)
+    z = (S * (alpha - 1.0)).masked_fill(~causal, -float("inf"))
+    a = 1.0 / (alpha - 1.0)
+    with torch.no_grad():
+        hi = z.amax(-1, keepdim=True)
+        lo = hi - 1.0
+        for _ in range(iters):
+            mid = 0.5 * (lo + hi)
+            f = (z - mid).clamp(min=0).pow(a).sum(-1, keepdim=True) - 1.0
+            lo = torch.where(f > 0, mid, lo)
+            hi = torch.where(f > 0, hi, mid)
+        tau = 0.5 * (lo + hi)
+    P = (z - tau).clamp(min=0).pow(a)
+    P = P / P.sum(-1, keepdim=True)
+    return torch.matmul(P, v).to(Q.dtype)
+
+
+def vanilla_attention(Q, K, V, alpha: float, sm_scale: float):
+    """The notebook's comparison formula (nb:1715-1743): causal softmax of
+    scores / alpha, raised to the power alpha and renormalised."""
+    q, k, v = (t.float() for t in (Q, K, V))
+    S = torch.matmul(q, k.transpose(-1, -2).contiguous()) * sm_scale
+    NQ, NK = S.shape[-2:]
+    S = S.masked_fill(~torch.ones(NQ, NK, device=S.device, dtype=torch.bool).tril_(NK - NQ),
+                      -float("inf"))
+    W = torch.softmax(S / alpha, dim=-1) if alpha != 1.0 else torch.softmax(S, dim=-1)
+    if alpha != 1.0:
+        W = torch.pow(W + 1e-8, alpha)
+        W = W / W.sum(-1, keepdim=True)
+    return torch.matmul(W, v).to(Q.dtype)
+
+
+BASELINES = {"entmax": dense_entmax_attention, "vanilla": vanilla_attention}
+
+
+def _time(fn, warmup: int, trials: int) -> tuple[float, float]:
+    """(median ms, peak MB allocated above the starting point) of fn()."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    gc.collect()
+    torch.cuda.empty_cache()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    times = []
+    for _ in range(trials):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    peak = (torch.cuda.max_memory_allocated() - base) / 2 ** 20
+    times.sort()
+    return times[len(times) // 2], peak
+
+
+def run_config(B: int, H: int, N: int, d: int, alpha: float = 1.5, k_keep: int = 8,
+               dtype: torch.dtype = torch.float32, baseline: str = "entmax",
+               backward: bool = False, input_scale: float = 0.1, warmup: int = 3,
+               trials: int = 10, seed: int = 42) -> dict:
+    """Benchmark one [B, H, N, d] configuration; returns the notebook's fields."""
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(seed)
+    Q, K, V, dO = (torch.randn(B, H, N, d, generator=g).mul_(input_scale).to(dtype).to(dev)
+                   for _ in range(4))
+    idx = torch.arange(N, device=dev, dtype=torch.int32).unsqueeze(0).expand(B * H, N).contiguous()
+    sm_scale = 1.0 / math.sqrt(d)
+    dense = BASELINES[baseline]
+
+    def make(fn):
+        def step():
+            if backward:
+                q, k, v = (t.detach().requires_grad_(True) for t in (Q, K, V))
+                fn(q, k, v).backward(dO)
+            else:
+                with torch.no_grad():
+                    fn(Q, K, V)
+        return step
+
+    sp = lambda q, k, v: splash_attention(q, k, v, idx, idx, alpha, k_keep, sm_scale)
+    dn = lambda q, k, v: dense(q, k, v, alpha, sm_scale)
+    t_dense, m_dense = _time(make(dn), warmup, trials)
+    t_splash, m_splash = _time(make(sp), warmup, trials)
+    with torch.no_grad():
+        a = sp(Q, K, V).float().flatten()
+        b = dn(Q, K, V).float().flatten()
+    mse = float(torch.mean((a - b) ** 2))
+    max_err = float((a - b).abs().max())
+    cos = float(torch.nn.functional.cosine_similarity(a, b, dim=0))
+    return {
+        "config_name": f"{B}x{H}x{N}x{d}", "B": B, "H": H, "NQ": N, "NK": N, "d": d,
+        "alpha": alpha, "k_keep": k_keep, "dtype": str(dtype).replace("torch.", ""),
+        "baseline": baseline, "pass": "fwd+bwd" if backward else "fwd",
+        "vanilla_time": round(t_dense, 4), "splash_time": round(t_splash, 4),
+        "speedup": round(t_dense / t_splash, 3),
+        "mse_error": mse, "max_error": max_err, "cosine_similarity": cos,
+        "vanilla_memory": round(m_dense, 2), "splash_memory": round(m_splash, 2),
+        "memory_saving": round(m_dense / m_splash, 3) if m_splash > 0 else None,
+    }
+
+
+def parse_config(s: str) -> tuple[int, int, int, int]:
+    parts = s.lower().split("x")
+    if len(parts) != 4:
+        raise argparse.ArgumentTypeError(f"config {s!r} must be BxHxNxd, e.g. 1x4x2048x64")
+    try:
+        return tuple(int(p) for p in parts)  # type: ignore[return-value]
+    except ValueError as e:
+        raise argparse.ArgumentTypeError(f"config {s!r}: {e}") from None
+
+
+def build_parser() -> argparse.ArgumentParser:
+    ap = argparse.ArgumentParser(prog="python -m splash_attention.benchmark",
+                                 description="splash attention vs dense attention, "
+                                             "the reference notebook's metric set")
+    ap.add_argument("--config", type=parse_config, action="append",
+                    help="BxHxNxd (repeatable); default 1x4x1024x64, 1x4x2048x64, 1x4x4096x64")
+    ap.add_argument("--alpha", type=float, default=1.5)
+    ap.add_argument("--k-keep", type=int, default=8)
+    ap.add_argument("--dtype", choices=["fp32", "bf16"], default="fp32")
+    ap.add_argument("--baseline", choices=sorted(BASELINES), default="entmax")
+    ap.add_argument("--backward", action="store_true", help="time forward + backward")
+    ap.add_argument("--input-scale", type=float, default=0.1)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--trials", type=int, default=10)
+    ap.add_argument("--json", action="store_true", help="one JSON object per line")
+    return ap
+
+
+def main(argv=None) -> list[dict]:
+    args = build_parser().parse_args(argv)
+    configs = args.config or [(1, 4, 1024, 64), (1, 4, 2048, 64), (1, 4, 4096, 64)]
+    dtype = {"fp32": torch.float32, "bf16": torch.bfloat16}[args.dtype]
+    results = []
+    for B, H, N, d in configs:
+        r = run_config(B, H, N, d, args.alpha, args.k_keep, dtype, args.baseline, args.backward,
+                       args.input_scale, args.warmup, args.trials)
+        results.append(r)
+        if args.json:
+            print(json.dumps(r), flush=True)
+        else:
+            print(f"{r['config_name']:>14} {r['pass']:>7} {args.baseline:>7}: "
+                  f"{r['vanilla_time']:9.3f} ms vs splash {r['splash_time']:8.3f} ms "
+                  f"(x{r['speedup']:.1f})  mse {r['mse_error']:.2e}  max {r['max_error']:.2e}  "
+                  f"cos {r['cosine_similarity']:.6f}  mem {r['vanilla_memory']:.0f} / "
+                  f"{r['splash_memory']:.0f} MB", flush=True)
+    return results
+
+
+if __name__ == "__main__":
+    main()

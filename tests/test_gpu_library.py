@@ -38,3 +38,22 @@ def test_compile_matches_eager(dev, dtype):
     compiled = run(torch.compile(attn, backend="aot_eager", fullgraph=True))
     for a, b in zip(eager, compiled):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("baseline,backward", [("entmax", False), ("vanilla", True)])
+def test_benchmark_cli_fields(dev, baseline, backward):
+    """The notebook's metric set (nb:1688-1712) for one small config.  No
+    closeness is asserted: the reference's tau recurrence (kept here) does
+    not converge on rows with fewer visible keys than k_keep (the -1e6
+    sentinel enters the bracket), so it differs from exact entmax there."""
+    from splash_attention import benchmark
+
+    print(f"[lib] benchmark cli {baseline} backward={backward}", flush=True)
+    r = benchmark.run_config(1, 2, 256, 64, 1.5, 8, torch.float32, baseline, backward,
+                             input_scale=1.0, warmup=1, trials=2)
+    for key in ("vanilla_time", "splash_time", "speedup", "mse_error", "max_error",
+                "cosine_similarity", "vanilla_memory", "splash_memory"):
+        assert key in r
+    assert r["splash_time"] > 0 and r["vanilla_time"] > 0
+    assert -1.0 <= r["cosine_similarity"] <= 1.0 + 1e-6
+    assert r["mse_error"] >= 0 and r["max_error"] >= 0

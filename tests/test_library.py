@@ -21,3 +21,18 @@ def test_fake_shapes_on_meta_tensors():
     g = torch.ops.adasplash.backward(Q, K, K, None, None, outs[0], outs[0], *outs[1:], 1.5, 8,
                                      0.125, "entmax")
     assert [tuple(x.shape) for x in g] == [(2, 3, 200, 64), (2, 3, 130, 64), (2, 3, 130, 64)]
+
+
+def test_benchmark_cli_parsing():
+    import argparse
+
+    import pytest
+
+    from splash_attention import benchmark
+
+    assert benchmark.parse_config("1x4x2048x64") == (1, 4, 2048, 64)
+    with pytest.raises(argparse.ArgumentTypeError):
+        benchmark.parse_config("1x4x2048")
+    args = benchmark.build_parser().parse_args(["--config", "2x2x256x64", "--baseline", "vanilla",
+                                                "--backward", "--dtype", "bf16"])
+    assert args.config == [(2, 2, 256, 64)] and args.baseline == "vanilla" and args.backward
