@@ -29,16 +29,19 @@ def np32(t):
     return t.numpy()
 
 
-def rel_err(a, b) -> float:
-    """max |a - b| / max |b| (a, b array-like)."""
+def rel_err(a, b, floor: float = 1e-30) -> float:
+    """max |a - b| / max(max |b|, floor) (a, b array-like)."""
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
-    den = max(float(np.abs(b).max()) if b.size else 0.0, 1e-30)
+    den = max(float(np.abs(b).max()) if b.size else 0.0, floor)
     return float(np.abs(a - b).max()) / den if a.size else 0.0
 
 
-def assert_close(name, got, want, tol):
-    e = rel_err(got, want)
+def assert_close(name, got, want, tol, floor: float = 1e-30):
+    """Max-norm relative error within tol; `floor` bounds the denominator
+    from below for tensors that are zero in exact arithmetic (e.g. dQ of a
+    row with one visible key), where it is the tensor's natural scale."""
+    e = rel_err(got, want, floor)
     assert e <= tol, f"{name}: max relative error {e:.3e} > {tol:.1e}"
     return e
 
