@@ -10,8 +10,8 @@
 // Work split: a tile is cut into "quads" of 4 consecutive rows x one
 // 16-byte column chunk; the quads of both tiles are dealt to the 256
 // threads (quad index = thread + 256 * i, tile 0's quads first, so that
-// every wave works on one tile at a time) and stored row-major (stride
-// Tile<T, D>::kRs).  Products that need a tile transposed read it with the
+// every wave works on one tile at a time) and stored in the tile layout
+// (row stride Tile<T, D>::kRs, chunk swizzle Tile<T, D>::sw).  Products that need a tile transposed read it with the
 // transposing LDS read, so no transposed copy is staged.
 #pragma once
 
@@ -55,8 +55,9 @@ struct Stager {
       const int job = qi / kQuads, q = qi % kQuads;
       const int rq = q / kCpr, cc = q % kCpr;
       T* dst = job == 0 ? dst0 : dst1;
-      for (int j = 0; j < 4; ++j)
-        *reinterpret_cast<uint4*>(dst + (4 * rq + j) * kRs + cc * kEpc) = r[i][j];
+      // the chunk swizzle depends on row bits 2-3: constant over the quad
+      T* d = dst + 4 * rq * kRs + ((cc * kEpc) ^ Tile<T, D>::sw(4 * rq));
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(d + j * kRs) = r[i][j];
     }
   }
 };

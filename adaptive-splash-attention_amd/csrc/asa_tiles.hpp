@@ -1,7 +1,7 @@
 // LDS tiles and the two MFMA tile products used by the attention passes.
 //
 // A "tile" is 64 rows x D columns of a [rows, D] tensor, staged row-major
-// in LDS (stride D+8 for bf16, D+4 for fp32).  Products that contract over
+// in LDS (stride D+8 with swizzled 16-byte chunks for bf16, D+4 for fp32).  Products that contract over
 // the tile's rows read their bf16 operand with the gfx950 transposing LDS
 // read; the fp32 MFMA takes one element per lane and k slot, which the
 // row-major tile serves directly.
@@ -23,11 +23,24 @@
 namespace asa {
 
 template <typename T, int D> struct Tile;
+// bf16: row stride D + 8 elements (a 16-byte pad per row), and the index of
+// each 16-byte chunk of row r XORed with bit 2 ^ bit 3 of r.  Measured on
+// gfx950 (64 x 64 tiles, 16 waves per CU), per wave instruction:
+//   ds_read_b128, 16 lanes x one chunk of 16 consecutive rows (rows_x_frag):
+//     2.05 ns with the swizzle, 3.55 ns without (a 2-way bank conflict);
+//   ds_read_b64_tr_b16 (tile_t_x_acc): 2.37 ns either way (conflict-free);
+//   ds_write_b128 of the staging quads: 5.6 ns either way (write-rate bound).
+// A 32-byte pad removes the read conflict without the swizzle but costs
+// 4 KiB of LDS per tile pair, one resident block per CU in the forward pass.
+// The XOR mask (in elements, sw(row)) depends on row bits 2 and 3 only, so
+// it is constant per lane in every access pattern here.
 template <int D> struct Tile<u16, D> {
   static constexpr int kRs = D + 8;  // row stride (elements)
+  __host__ __device__ static constexpr int sw(int row) { return 8 * (((row >> 2) ^ (row >> 3)) & 1); }
 };
 template <int D> struct Tile<float, D> {
   static constexpr int kRs = D + 4;
+  __host__ __device__ static constexpr int sw(int) { return 0; }
 };
 
 // B-operand fragment of one row per lane (lane column c16 <- `row`),
@@ -54,11 +67,13 @@ template <int D>
 __device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const u16* rm,
                                             const RowFrag<u16, D>& b, int lane) {
   const int g = lane >> 4, c = lane & 15;
+  // row 16f + c, chunk 4s + g (swizzled by row bits 2-3, i.e. by c)
+  const u16* base = rm + c * Tile<u16, D>::kRs + ((8 * g) ^ Tile<u16, D>::sw(c));
   for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < D / 32; ++s)
     for (int f = 0; f < 4; ++f) {
       const bf16x8 a =
-          *reinterpret_cast<const bf16x8*>(rm + (16 * f + c) * Tile<u16, D>::kRs + 32 * s + 8 * g);
+          *reinterpret_cast<const bf16x8*>(base + 16 * f * Tile<u16, D>::kRs + 32 * s);
       acc[f] = mfma(a, b.v[s], acc[f]);
     }
 }
@@ -99,8 +114,9 @@ __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const u16* rm,
         bl[4 + r] = static_cast<__bf16>(x[2 * cc + 1][r] - static_cast<float>(b[4 + r]));
       }
     }
-    // rows 32cc + 4g + 0..3 (low half) and 32cc + 16 + 4g + 0..3 (high half)
-    const u16* base = rm + (32 * cc + 4 * g + (l >> 2)) * rs + 4 * (l & 3);
+    // rows 32cc + 4g + 0..3 (low half) and 32cc + 16 + 4g + 0..3 (high
+    // half); the chunk swizzle depends on g only (row bits 2-3)
+    const u16* base = rm + (32 * cc + 4 * g + (l >> 2)) * rs + ((4 * (l & 3)) ^ Tile<u16, D>::sw(4 * g));
     bf16x8 a[D / 16];
     for (int db = 0; db < D / 16; ++db) {
       const bf16x4 lo = read_tr16(base + 16 * db);

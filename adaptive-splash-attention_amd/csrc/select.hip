@@ -228,11 +228,14 @@ __device__ __forceinline__ float sweep_floor(float th, bool exact, float scale) 
 }
 
 
-// K tile of 64 keys in LDS: row-major with a padded row stride, filled by
-// all 256 threads in 16-byte chunks (consecutive threads, consecutive
-// chunks of a row: coalesced global reads).
+// K tile of 64 keys in LDS, in the attention passes' tile layout (padded
+// row stride, swizzled 16-byte chunks: Tile<T, D>), filled by all 256
+// threads in 16-byte chunks (consecutive threads, consecutive chunks of a
+// row: coalesced global reads).  The scores are formed by rows_x_frag, the
+// attention passes' score product with the same operands and accumulation
+// order, so every pass sees bit-identical scores.
 template <typename T, int D> struct KStage {
-  static constexpr int kRs = sizeof(T) == 2 ? D + 8 : D + 4;   // elements per LDS row
+  static constexpr int kRs = Tile<T, D>::kRs;                   // elements per LDS row
   static constexpr int kRowChunks = D * int(sizeof(T)) / 16;    // 16-byte chunks per row
   static constexpr int kPerThread = kBlock * kRowChunks / kThreads;
   static_assert(kBlock * kRowChunks % kThreads == 0, "tile chunks must divide the block");
@@ -251,53 +254,10 @@ template <typename T, int D> struct KStage {
     for (int j = 0; j < kPerThread; ++j) {
       const int ch = t + j * kThreads, row = ch / kRowChunks;
       const int col = (ch % kRowChunks) * (16 / int(sizeof(T)));
-      *reinterpret_cast<uint4*>(buf + row * kRs + col) = r[j];
+      *reinterpret_cast<uint4*>(buf + row * kRs + (col ^ Tile<T, D>::sw(row))) = r[j];
     }
   }
 };
-
-// Q^T operand fragment of the lane's query row (column c of the products).
-template <typename T, int D> struct QFrag;
-template <int D> struct QFrag<u16, D> {
-  bf16x8 v[D / 32];
-  __device__ void load(const u16* row, bool ok, int g) {
-    for (int s = 0; s < D / 32; ++s)
-      v[s] = ok ? *reinterpret_cast<const bf16x8*>(row + 32 * s + 8 * g) : bf16x8{};
-  }
-};
-template <int D> struct QFrag<float, D> {
-  f32x4 v[D / 16];
-  __device__ void load(const float* row, bool ok, int g) {
-    for (int j = 0; j < D / 16; ++j)
-      v[j] = ok ? *reinterpret_cast<const f32x4*>(row + 16 * j + 4 * g) : f32x4{};
-  }
-};
-
-// acc[f] = S^T block of keys 16f.. x the wave's 16 rows, from the LDS tile.
-// Same operands and accumulation order as the attention passes' score
-// products, so every pass sees bit-identical scores.
-template <int D>
-__device__ __forceinline__ void tile_scores(f32x4 (&acc)[4], const u16* buf, const QFrag<u16, D>& q,
-                                            int g, int c) {
-  constexpr int rs = KStage<u16, D>::kRs;
-  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < D / 32; ++s)
-    for (int f = 0; f < 4; ++f) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(buf + (16 * f + c) * rs + 32 * s + 8 * g);
-      acc[f] = mfma(a, q.v[s], acc[f]);
-    }
-}
-template <int D>
-__device__ __forceinline__ void tile_scores(f32x4 (&acc)[4], const float* buf,
-                                            const QFrag<float, D>& q, int g, int c) {
-  constexpr int rs = KStage<float, D>::kRs;
-  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < D / 16; ++j)
-    for (int f = 0; f < 4; ++f) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(buf + (16 * f + c) * rs + 16 * j + 4 * g);
-      for (int r = 0; r < 4; ++r) acc[f] = mfma(a[r], q.v[j][r], acc[f]);
-    }
-}
 
 // acc[b >> 2][b & 3] for a per-lane index b in [0, 16): a select tree on
 // the index bits instead of a dynamically indexed register array.
@@ -407,10 +367,10 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
   __syncthreads();
   const int nvis = int(s_ctl[1]);
 
-  QFrag<T, D> qf;
+  RowFrag<T, D> qf;  // Q^T operand: the lane's query row (column c of the products)
   const T* Kb = nullptr;
   if constexpr (kTiles) {
-    qf.load(static_cast<const T*>(p.q) + grow * D, rowok, g);
+    qf.load(static_cast<const T*>(p.q) + grow * D, rowok, L);
     Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
   }
   KStage<T, D> ks;
@@ -427,7 +387,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
           acc[f][r] = rowok && key < NK ? clamp_score(p.scores[grow * NK + key]) : 0.0f;
         }
     } else {
-      tile_scores<D>(acc, buf, qf, g, c);
+      rows_x_frag<D>(acc, buf, qf, L);
       if constexpr (MODE == kExactScores)
         for (int f = 0; f < 4; ++f)
           for (int r = 0; r < 4; ++r) acc[f][r] = clamp_score(acc[f][r] * scale);
