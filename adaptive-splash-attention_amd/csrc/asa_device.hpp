@@ -115,9 +115,46 @@ __device__ __forceinline__ float pow_fast(float x, float e) {
 
 __device__ __forceinline__ bool finite(float x) { return __builtin_isfinite(x); }
 
-// Score clamp of the reference (adasplashattention.cu:195-197): NaN -> -10.
+// Score clamp of the reference (adasplashattention.cu:195-197): one
+// v_med3_f32, which returns the lower bound for a NaN input, as
+// fmaxf(NaN, -10) does (NaN -> -10).
 __device__ __forceinline__ float clamp_score(float s) {
-  return fminf(fmaxf(s, -10.0f), 10.0f);
+  return __builtin_amdgcn_fmed3f(s, -10.0f, 10.0f);
+}
+
+// max(u, 0) for u = (alpha - 1) clamp_score(scale s) - tau, the argument of
+// every per-score power (adasplashattention.cu:307-312), in two
+// instructions per score: v = med3(c s - tau, lo, hi) with
+// c = (alpha - 1) scale, lo = max(-10 (alpha - 1) - tau, 0) and
+// hi = max(10 (alpha - 1) - tau, 0).  It equals max(u, 0) up to the rounding
+// of the fused product (c s - tau is rounded once); a NaN score gives lo,
+// which is what the clamp's NaN -> -10 gives.  Rows that get no weight use
+// c = lo = hi = 0, so v = 0 for every score.
+struct ClippedU {
+  float c, nt, lo, hi;
+  __device__ __forceinline__ ClippedU(float am1, float scale, float tau, bool valid) {
+    c = valid ? am1 * scale : 0.0f;
+    nt = valid ? -tau : 0.0f;
+    lo = valid ? fmaxf(fmaf(-10.0f, am1, nt), 0.0f) : 0.0f;
+    hi = valid ? fmaxf(fmaf(10.0f, am1, nt), 0.0f) : 0.0f;
+  }
+  __device__ __forceinline__ float operator()(float s) const {
+    return __builtin_amdgcn_fmed3f(fmaf(c, s, nt), lo, hi);
+  }
+};
+
+// v^e for v = max(u, 0) from ClippedU: 0 where v = 0, like the reference's
+// (u > 0) ? max(u, EPS)^e : 0.  The positive integer classes give 0 at v = 0
+// by themselves; they drop the EPS floor, which changes a weight by at most
+// EPS = 1e-8.  Other classes keep the floor and zero non-finite results.
+template <int PC>
+__device__ __forceinline__ float pow_clipped(float v, float e) {
+  if constexpr (PC == kE1 || PC == kE2 || PC == kE3 || PC == kE4) {
+    return pow_fast<PC>(v, e);
+  } else {
+    const float r = v > 0.0f ? pow_fast<PC>(fmaxf(v, kEps), e) : 0.0f;
+    return finite(r) ? r : 0.0f;
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -63,27 +63,29 @@ template <int D> struct RowFrag<float, D> {
   }
 };
 
-template <int D>
+// [F0, F1) restricts the product to row blocks f = F0..F1-1 (16 rows each);
+// the other entries of acc are left alone.
+template <int D, int F0 = 0, int F1 = 4>
 __device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const u16* rm,
                                             const RowFrag<u16, D>& b, int lane) {
   const int g = lane >> 4, c = lane & 15;
   // row 16f + c, chunk 4s + g (swizzled by row bits 2-3, i.e. by c)
   const u16* base = rm + c * Tile<u16, D>::kRs + ((8 * g) ^ Tile<u16, D>::sw(c));
-  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int f = F0; f < F1; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < D / 32; ++s)
-    for (int f = 0; f < 4; ++f) {
+    for (int f = F0; f < F1; ++f) {
       const bf16x8 a =
           *reinterpret_cast<const bf16x8*>(base + 16 * f * Tile<u16, D>::kRs + 32 * s);
       acc[f] = mfma(a, b.v[s], acc[f]);
     }
 }
-template <int D>
+template <int D, int F0 = 0, int F1 = 4>
 __device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const float* rm,
                                             const RowFrag<float, D>& b, int lane) {
   const int g = lane >> 4, c = lane & 15;
-  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int f = F0; f < F1; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < D / 16; ++j)
-    for (int f = 0; f < 4; ++f) {
+    for (int f = F0; f < F1; ++f) {
       const f32x4 a =
           *reinterpret_cast<const f32x4*>(rm + (16 * f + c) * Tile<float, D>::kRs + 16 * j + 4 * g);
       for (int r = 0; r < 4; ++r) acc[f] = mfma(a[r], b.v[j][r], acc[f]);

@@ -63,14 +63,6 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(BackwardParams p) {
   cfac[r] = 1.0f / (p.norms[r] + kEps);
 }
 
-// Clamp of a score without the operand canonicalisation fmaxf/fminf carry
-// (MFMA results are never signalling NaNs); NaN -> -10 like fmaxf/fminf.
-__device__ __forceinline__ float clamp10(float s) {
-  float r;
-  asm("v_max_f32 %0, %1, %2\n\tv_min_f32 %0, %0, %3" : "=&v"(r) : "v"(s), "s"(-10.0f), "s"(10.0f));
-  return r;
-}
-
 // ---------------------------------------------------------------------------
 // dQ (query-major)
 // ---------------------------------------------------------------------------
@@ -109,11 +101,10 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
   qf.load(static_cast<const T*>(p.q) + row * D, qok, lane);
   df.load(static_cast<const T*>(p.dout) + row * D, qok, lane);
   const int qpos = qok ? p.q_idx[row] : 0;
-  const float tau = qok ? p.taus[row] : __builtin_inff();  // invalid rows: u < 0
   const float alpha = p.d.alpha;
   const float am1 = alpha - 1.0f;
   const float ew = (2.0f - alpha) / am1;
-  const float thr = REF ? kEps : 0.0f;
+  const ClippedU clip(am1, p.d.scale, qok ? p.taus[row] : 0.0f, qok);  // invalid rows: w = 0
   const float norm = qok ? p.norms[row] : 0.0f;
   float cfac, shift;
   if constexpr (REF) {
@@ -162,12 +153,11 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
     auto weights = [&](auto partial) {
       for (int f = 0; f < 4; ++f)
         for (int r = 0; r < 4; ++r) {
-          const float u = am1 * clamp10(sacc[f][r] * scale) - tau;
-          float wv = pow_fast<PW>(fmaxf(u, kEps), ew);
-          if constexpr (PW != kE0 && PW != kE1 && PW != kE2) wv = finite(wv) ? wv : 0.0f;
-          bool vis = u > thr;
-          if constexpr (decltype(partial)::value) vis = vis && sm.kid[b][16 * f + 4 * g + r] <= qpos;
-          wv = vis ? wv : 0.0f;
+          const float v = clip(sacc[f][r]);  // max(u, 0)
+          float wv = pow_clipped<PW>(v, ew);
+          if constexpr (REF) wv = v > kEps ? wv : 0.0f;  // the reference's u > EPS
+          if constexpr (decltype(partial)::value)
+            wv = sm.kid[b][16 * f + 4 * g + r] <= qpos ? wv : 0.0f;
           const float dp = dacc[f][r];
           if constexpr (REF) {
             const float ds = cfac * wv * (dp - shift);
@@ -222,30 +212,37 @@ template <typename T, int D> struct alignas(16) DkvSmem {
   T dO[2][kBlock * Tile<T, D>::kRs];
 };
 
-// Per-query constants of a query tile: tau, 1/(sum p + EPS), shift, c.
+// Per-query constants of a query tile: the ClippedU terms -tau, lo, hi;
+// 1/(sum p + EPS); the gradient factor c and -c * shift, so that
+// c (dp - shift) is one fma.
 struct alignas(16) QConst {
-  float tau[kBlock], invn[kBlock], shift[kBlock], c[kBlock];
+  float nt[kBlock], lo[kBlock], hi[kBlock], invn[kBlock], c[kBlock], cs[kBlock];
   int pos[kBlock];
 };
 struct QConstStager {
-  float tau, invn, shift, c;
+  float nt, lo, hi, invn, c, cs;
   __device__ __forceinline__ void load(const BackwardParams& p, size_t rows, size_t rbase, int qbase,
-                                       int NQ, int t) {
+                                       int NQ, float am1, int t) {
     if (t < kWave) {
       const bool ok = qbase + t < NQ;
       const size_t r = rbase + (ok ? qbase + t : 0);
-      tau = ok ? p.taus[r] : __builtin_inff();  // invalid rows: u < 0
+      const ClippedU u(am1, p.d.scale, ok ? p.taus[r] : 0.0f, ok);  // invalid rows: p = w = 0
+      nt = u.nt;
+      lo = u.lo;
+      hi = u.hi;
       invn = ok ? 1.0f / (p.norms[r] + kEps) : 0.0f;
-      shift = ok ? p.delta[r] : 0.0f;
       c = ok ? p.delta[rows + r] : 0.0f;
+      cs = ok ? -c * p.delta[r] : 0.0f;
     }
   }
   __device__ __forceinline__ void store(QConst& qc, int t) const {
     if (t < kWave) {
-      qc.tau[t] = tau;
+      qc.nt[t] = nt;
+      qc.lo[t] = lo;
+      qc.hi[t] = hi;
       qc.invn[t] = invn;
-      qc.shift[t] = shift;
       qc.c[t] = c;
+      qc.cs[t] = cs;
     }
   }
 };
@@ -280,8 +277,8 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dkdv_ke
   const float am1 = alpha - 1.0f;
   const float a = 1.0f / am1;
   const float ew = (2.0f - alpha) / am1;
-  const float thr = REF ? kEps : 0.0f;
   const float scale = p.d.scale;
+  const float cu = am1 * scale;  // ClippedU's c (uniform)
   // largest position of the block's valid keys (wave 0 tests tiles with it)
   int kmax = 0;
   if (w == 0) {
@@ -302,7 +299,7 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dkdv_ke
     const int qbase = kl[e] * kBlock;
     st.load(Qb, dOb, qbase, NQ, t);
     ps.load(qidx, qbase, NQ, INT32_MAX, t);
-    qs.load(p, rows, rbase, qbase, NQ, t);
+    qs.load(p, rows, rbase, qbase, NQ, am1, t);
   };
   auto put = [&](int b) {
     st.store(sm.Q[b], sm.dO[b], t);
@@ -319,41 +316,47 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dkdv_ke
     const int b = (e - e0) & 1;
     const QConst& qc = qcs[b];
     f32x4 sacc[4], dacc[4];
-    rows_x_frag<D>(sacc, sm.Q[b], kf, lane);
-    rows_x_frag<D>(dacc, sm.dO[b], vf, lane);
     auto grads = [&](auto partial, int fb) {
       for (int f = fb; f < fb + 2; ++f) {
         // constants of queries 16f + 4g + 0..3
         const int q4 = 16 * f + 4 * g;
-        const f32x4 tau4 = *reinterpret_cast<const f32x4*>(&qc.tau[q4]);
+        const f32x4 nt4 = *reinterpret_cast<const f32x4*>(&qc.nt[q4]);
+        const f32x4 lo4 = *reinterpret_cast<const f32x4*>(&qc.lo[q4]);
+        const f32x4 hi4 = *reinterpret_cast<const f32x4*>(&qc.hi[q4]);
         const f32x4 invn4 = *reinterpret_cast<const f32x4*>(&qc.invn[q4]);
-        const f32x4 shift4 = *reinterpret_cast<const f32x4*>(&qc.shift[q4]);
         const f32x4 c4 = *reinterpret_cast<const f32x4*>(&qc.c[q4]);
+        const f32x4 cs4 = *reinterpret_cast<const f32x4*>(&qc.cs[q4]);
         for (int r = 0; r < 4; ++r) {
-          const float u = am1 * clamp10(sacc[f][r] * scale) - tau4[r];
-          const float ue = fmaxf(u, kEps);
-          float pv = pow_fast<PP>(ue, a);
-          float wv = pow_fast<PW>(ue, ew);
-          if constexpr (PP != kE0 && PP != kE1 && PP != kE2) pv = finite(pv) ? pv : 0.0f;
-          if constexpr (PW != kE0 && PW != kE1 && PW != kE2) wv = finite(wv) ? wv : 0.0f;
-          bool vis = true;
-          if constexpr (decltype(partial)::value) vis = kpos <= qc.pos[q4 + r];
-          const float pn = (vis && u > 0.0f) ? pv * invn4[r] : 0.0f;
-          float ds = c4[r] * wv * (dacc[f][r] - shift4[r]);
-          ds = (vis && u > thr && finite(ds)) ? ds : 0.0f;
+          // max(u, 0) of ClippedU with the query's terms
+          const float v = __builtin_amdgcn_fmed3f(fmaf(cu, sacc[f][r], nt4[r]), lo4[r], hi4[r]);
+          float pn = pow_clipped<PP>(v, a) * invn4[r];
+          float wv = pow_clipped<PW>(v, ew);
+          if constexpr (REF) wv = v > kEps ? wv : 0.0f;  // the reference's u > EPS
+          float ds = wv * fmaf(c4[r], dacc[f][r], cs4[r]);
+          ds = finite(ds) ? ds : 0.0f;
+          if constexpr (decltype(partial)::value) {
+            const bool vis = kpos <= qc.pos[q4 + r];
+            pn = vis ? pn : 0.0f;
+            ds = vis ? ds : 0.0f;
+          }
           sacc[f][r] = ds;
           dacc[f][r] = pn;
         }
       }
     };
     const bool tile_full = full[b] != 0;
-    // two halves (score rows 16f.., f = 0,1 then 2,3): each half's P and ds
-    // feed their products before the next half is formed, which keeps the
-    // register footprint within three waves per SIMD
+    // two halves (score rows 16f.., f = 0,1 then 2,3): each half's scores,
+    // P and ds are formed and fed to their products before the next half
+    // is started, which keeps the register footprint within three waves
+    // per SIMD
+    rows_x_frag<D, 0, 2>(sacc, sm.Q[b], kf, lane);
+    rows_x_frag<D, 0, 2>(dacc, sm.dO[b], vf, lane);
     if (tile_full) grads(std::false_type{}, 0);
     else grads(std::true_type{}, 0);
     tile_t_x_acc<D, false, 0, 1>(av, sm.dO[b], dacc, lane);
     tile_t_x_acc<D, true, 0, 1>(ak, sm.Q[b], sacc, lane);
+    rows_x_frag<D, 2, 4>(sacc, sm.Q[b], kf, lane);
+    rows_x_frag<D, 2, 4>(dacc, sm.dO[b], vf, lane);
     if (tile_full) grads(std::false_type{}, 2);
     else grads(std::true_type{}, 2);
     tile_t_x_acc<D, false, 1, 2>(av, sm.dO[b], dacc, lane);

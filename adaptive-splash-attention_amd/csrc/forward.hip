@@ -8,7 +8,8 @@
 // stream through double-buffered LDS (asa_stage.hpp); S^T = K Q^T is formed
 // on MFMA,
 // p = max(u, EPS)^(1/(alpha-1)) with u = (alpha-1) s - tau is applied in
-// registers, and O^T += V^T P^T runs on MFMA with P^T taken directly from
+// registers (clamp, scale and tau folded into one fma and one median,
+// ClippedU), and O^T += V^T P^T runs on MFMA with P^T taken directly from
 // the score accumulators.  Row sums of p are kept per lane and reduced
 // across the four lane groups at the end.
 #include <type_traits>
@@ -30,14 +31,6 @@ template <typename T, int D> struct alignas(16) FwdSmem {
   int full[2];
 };
 
-// Clamp of a score without the operand canonicalisation fmaxf/fminf carry
-// (MFMA results are never signalling NaNs); NaN -> -10 like fmaxf/fminf.
-__device__ __forceinline__ float clamp10(float s) {
-  float r;
-  asm("v_max_f32 %0, %1, %2\n\tv_min_f32 %0, %0, %3" : "=&v"(r) : "v"(s), "s"(-10.0f), "s"(10.0f));
-  return r;
-}
-
 template <typename T, int D, int PC>
 __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   __shared__ FwdSmem<T, D> sm;
@@ -58,10 +51,9 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   RowFrag<T, D> qf;
   qf.load(static_cast<const T*>(p.q) + row * D, qok, lane);
   const int qpos = qok ? p.q_idx[row] : 0;
-  const float tau = qok ? p.taus[row] : __builtin_inff();  // invalid rows: u < 0
   const float am1 = p.d.alpha - 1.0f;
   const float a = 1.0f / am1;
-  const float scale = p.d.scale;
+  const ClippedU clip(am1, p.d.scale, qok ? p.taus[row] : 0.0f, qok);  // invalid rows: p = 0
   // smallest position of the block's valid rows (wave 0 tests tiles with it)
   int qmin = 0;
   if (w == 0) {
@@ -101,13 +93,11 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
     auto weights = [&](auto partial) {
       for (int f = 0; f < 4; ++f)
         for (int r = 0; r < 4; ++r) {
-          const float u = am1 * clamp10(acc[f][r] * scale) - tau;
-          float pv = pow_fast<PC>(fmaxf(u, kEps), a);
-          if constexpr (PC != kE0 && PC != kE1 && PC != kE2) pv = finite(pv) ? pv : 0.0f;
-          bool vis = u > 0.0f;
-          if constexpr (decltype(partial)::value) vis = vis && sm.kid[b][16 * f + 4 * g + r] <= qpos;
-          acc[f][r] = vis ? pv : 0.0f;
-          rowsum += acc[f][r];
+          float pv = pow_clipped<PC>(clip(acc[f][r]), a);
+          if constexpr (decltype(partial)::value)
+            pv = sm.kid[b][16 * f + 4 * g + r] <= qpos ? pv : 0.0f;
+          acc[f][r] = pv;
+          rowsum += pv;
         }
     };
     if (sm.full[b] != 0) weights(std::false_type{});
