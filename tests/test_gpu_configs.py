@@ -158,3 +158,25 @@ def test_c5_long_sinks(dev):
     _identities("c5", st.norms, grads, dO, 2e-2)
     _row_sample_check("c5", out, st.taus, grads, Q, K, V, dO, idx, idx, 1.25, 128, scale, (3,),
                       (0, 16384, 32704), H)
+
+
+@pytest.mark.parametrize("d,alpha,k,causal", [(128, 2.0, 64, False), (64, 1.5, 32, True)])
+def test_clustered_full_gradients(dev, d, alpha, k, causal):
+    """Clustered keys and queries (the configs[3] generator) at a size the
+    oracle covers whole: every gradient, including dK, whose bf16 product
+    takes ds rounded once.  With clustered keys the dQ sum cancels heavily
+    (each row's ds sums to zero), which its hi/lo operand split absorbs."""
+    print(f"[cfg] clustered 1x2x2048x{d} alpha {alpha} k {k} causal={causal}", flush=True)
+    B, H, N = 1, 2, 2048
+    Q, K, V, dO = _clustered(B, H, N, d, seed=5)
+    ki = causal_idx(B * H, N)
+    qi = ki.clone() if causal else torch.full((B * H, N), N - 1, dtype=torch.int32)
+    scale = d ** -0.5
+    out, st, grads = _run(dev, Q, K, V, dO, qi, ki, alpha, k, scale)
+    own, fw, og = oracle_at_gpu_tau(np32(Q), np32(K), np32(V), np32(dO), qi.numpy(), ki.numpy(),
+                                    alpha, scale, k, st.taus.cpu().numpy())
+    np.testing.assert_array_equal(st.mask.cpu().numpy(), own.mask)
+    assert_close("clustered out", np32(out), fw.out, 2e-2)
+    for nm, g, w in zip(("dQ", "dK", "dV"), grads, og):
+        assert_close(f"clustered {nm}", np32(g), w, 2e-2)
+    _identities("clustered", st.norms, grads, dO, 2e-2)
