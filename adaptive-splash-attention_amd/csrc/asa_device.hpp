@@ -18,6 +18,7 @@ namespace asa {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16;
 
@@ -31,6 +32,14 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 __device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// A packed bf16 pair with the given bits, held in a scalar register that
+// the compiler cannot fold into an inline constant.  The empty asm is not
+// volatile, so it is no scheduling barrier and can be hoisted out of loops.
+__device__ __forceinline__ bf16x2 opaque_bf16x2(uint32_t bits) {
+  asm("" : "+s"(bits));
+  return __builtin_bit_cast(bf16x2, bits);
 }
 
 __device__ __forceinline__ float bf16_to_f32(u16 h) {

@@ -106,16 +106,26 @@ __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const u16* rm,
                                              const f32x4 (&x)[4], int lane) {
   const int g = lane >> 4, l = lane & 15;
   constexpr int rs = Tile<u16, D>::kRs;
+  // x - hi is exact in fp32; it is formed from the packed hi pair by
+  // v_dot2c_f32_bf16 (x + hi.lo * -1 + hi.hi * 0), one instruction per value.
+  // The (-1, 0) and (0, -1) pairs are passed in scalar registers: as an
+  // inline constant the compiler encodes (-1, 0) as the float -1.0, whose
+  // bits the instruction reads as the pair (0, -1) (measured on gfx950).
+  const bf16x2 kNegLo = opaque_bf16x2(0x0000bf80u);
+  const bf16x2 kNegHi = opaque_bf16x2(0xbf800000u);
   for (int cc = CC0; cc < CC1; ++cc) {
     bf16x8 b, bl;
-    for (int r = 0; r < 4; ++r) {
-      b[r] = static_cast<__bf16>(x[2 * cc][r]);
-      b[4 + r] = static_cast<__bf16>(x[2 * cc + 1][r]);
-      if (Split) {
-        bl[r] = static_cast<__bf16>(x[2 * cc][r] - static_cast<float>(b[r]));
-        bl[4 + r] = static_cast<__bf16>(x[2 * cc + 1][r] - static_cast<float>(b[4 + r]));
+    for (int h = 0; h < 2; ++h)
+      for (int r = 0; r < 4; r += 2) {
+        const float x0 = x[2 * cc + h][r], x1 = x[2 * cc + h][r + 1];
+        const bf16x2 hp = {static_cast<__bf16>(x0), static_cast<__bf16>(x1)};
+        b[4 * h + r] = hp[0];
+        b[4 * h + r + 1] = hp[1];
+        if (Split) {
+          bl[4 * h + r] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(hp, kNegLo, x0, false));
+          bl[4 * h + r + 1] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(hp, kNegHi, x1, false));
+        }
       }
-    }
     // rows 32cc + 4g + 0..3 (low half) and 32cc + 16 + 4g + 0..3 (high
     // half); the chunk swizzle depends on g only (row bits 2-3)
     const u16* base = rm + (32 * cc + 4 * g + (l >> 2)) * rs + ((4 * (l & 3)) ^ Tile<u16, D>::sw(4 * g));
