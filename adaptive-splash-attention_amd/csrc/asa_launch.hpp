@@ -13,6 +13,16 @@ struct Dims {
   float scale;
 };
 
+// Support-list buffers shared by the forward (writer) and the backward.
+struct SupportLists {
+  uint32_t* key;
+  float* val;
+  float* ds;       // backward: ds of every entry (written by the dQ pass)
+  int32_t* off;
+  int32_t* cnt;
+  int cap;         // entries per wave region
+};
+
 struct SelectParams {
   Dims d;
   const void* q;          // MFMA path
@@ -50,6 +60,15 @@ struct ForwardParams {
   const int32_t* q_list;
   void* out;
   float* norms;
+  // Support lists (optional: sup_key == nullptr emits nothing).  Every wave
+  // of a query block (16 rows) owns a region of sup_cap entries at
+  // ((bh * nQB + qb) * 4 + w) * sup_cap; entry = key index | row-in-wave << 28
+  // in sup_key and v = max(u, 0) in sup_val, for every score of the forward
+  // with u > 0, in (tile, score slot, lane) order.  sup_off[(bh * nQB * nKB
+  // + e) * 4 + w] = the wave's entry count before tile e (the head's
+  // q_list position e); sup_cnt[(bh * nQB + qb) * 4 + w] = its total, which
+  // may exceed sup_cap (then only the first sup_cap entries were written).
+  SupportLists sup;
 };
 
 struct BackwardParams {

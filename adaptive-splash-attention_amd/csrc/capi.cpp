@@ -56,6 +56,8 @@ int validate(const asa_problem* p, Shape* sh) {
                 p->heads);
   if (p->nq < 1 || p->nk < 1)
     return fail(ASA_ERR_INVALID_ARGUMENT, "nq (%d) and nk (%d) must be >= 1", p->nq, p->nk);
+  if (p->nk >= (1 << 28))
+    return fail(ASA_ERR_INVALID_ARGUMENT, "nk (%d) must be below 2^28", p->nk);
   if (p->head_dim > 128)
     return fail(ASA_ERR_INVALID_ARGUMENT, "Head dimension too large (%d > 128)", p->head_dim);
   if (p->head_dim != 64 && p->head_dim != 128)
@@ -99,6 +101,18 @@ size_t tkv_bytes(const Shape& s) {
   return (b + 15) & ~size_t(15);
 }
 
+// Byte offset of the support entries' ds in the backward workspace (after
+// the two floats per row), 16-byte aligned.
+size_t bwd_ds_offset(const Shape& s) {
+  return (2 * size_t(s.BH) * s.NQ * sizeof(float) + 15) & ~size_t(15);
+}
+
+// Support-list entries per wave region (16 query rows).
+int support_cap(const Shape& s) { return 16 * (s.k * 2 > 64 ? s.k * 2 : 64); }
+size_t support_entries(const Shape& s) {
+  return size_t(s.BH) * s.nQB * 4 * size_t(support_cap(s));
+}
+
 void sizes_of(const Shape& s, asa_sizes* z) {
   const size_t rows = size_t(s.BH) * s.NQ;
   const size_t blocks = size_t(s.BH) * s.nQB * s.nKB;
@@ -111,10 +125,14 @@ void sizes_of(const Shape& s, asa_sizes* z) {
   z->k_list = blocks * sizeof(int32_t);
   z->topk_idx = rows * s.k * sizeof(int32_t);
   z->topk_val = rows * s.k * sizeof(float);
+  z->sup_key = support_entries(s) * sizeof(uint32_t);
+  z->sup_val = support_entries(s) * sizeof(float);
+  z->sup_off = blocks * 4 * sizeof(int32_t);
+  z->sup_cnt = size_t(s.BH) * s.nQB * 4 * sizeof(int32_t);
   // forward: the rows' sorted top-k values and the key blocks' position
-  // bounds; backward: two floats per row
+  // bounds; backward: two floats per row, then ds of every support entry
   const size_t fwd_ws = tkv_bytes(s) + size_t(s.BH) * s.nKB * 2 * sizeof(int32_t);
-  const size_t bwd_ws = 2 * rows * sizeof(float);
+  const size_t bwd_ws = bwd_ds_offset(s) + support_entries(s) * sizeof(float);
   z->workspace = fwd_ws > bwd_ws ? fwd_ws : bwd_ws;
 }
 
@@ -125,7 +143,25 @@ int check_state(const asa_state* st, bool need_norms) {
     return fail(ASA_ERR_INVALID_ARGUMENT, "a required state buffer is NULL");
   if ((st->topk_idx == nullptr) != (st->topk_val == nullptr))
     return fail(ASA_ERR_INVALID_ARGUMENT, "topk_idx and topk_val must be both set or both NULL");
+  const int nsup = (st->sup_key != nullptr) + (st->sup_val != nullptr) + (st->sup_off != nullptr) +
+                   (st->sup_cnt != nullptr);
+  if (nsup != 0 && nsup != 4)
+    return fail(ASA_ERR_INVALID_ARGUMENT,
+                "sup_key, sup_val, sup_off and sup_cnt must be all set or all NULL");
   return ASA_OK;
+}
+
+asa::SupportLists support_of(const Shape& sh, const asa_state* st, float* ds) {
+  asa::SupportLists l{};
+  if (st->sup_key) {
+    l.key = st->sup_key;
+    l.val = st->sup_val;
+    l.ds = ds;
+    l.off = st->sup_off;
+    l.cnt = st->sup_cnt;
+    l.cap = support_cap(sh);
+  }
+  return l;
 }
 
 // Candidate capacity per row of the select kernel on the current device
@@ -273,6 +309,7 @@ int asa_forward(const asa_problem* p, const void* q, const void* k, const void* 
   fp.q_list = st->q_list;
   fp.out = out;
   fp.norms = st->norms;
+  fp.sup = support_of(sh, st, nullptr);
   asa::profile_begin("forward", s);
   hipError_t e = asa::launch_forward(fp, sh.bf16, s);
   asa::profile_end(s);

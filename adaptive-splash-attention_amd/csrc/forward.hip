@@ -31,7 +31,7 @@ template <typename T, int D> struct alignas(16) FwdSmem {
   int full[2];
 };
 
-template <typename T, int D, int PC>
+template <typename T, int D, int PC, bool EMIT>
 __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   __shared__ FwdSmem<T, D> sm;
   using St = Stager<T, D>;
@@ -65,6 +65,18 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   for (int db = 0; db < D / 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
   float rowsum = 0.0f;
 
+  // Support emission: this wave's region and its entry count (wave-uniform).
+  const size_t wreg = (size_t(bh) * nQB + qb) * 4 + w;
+  uint32_t* skey = nullptr;
+  float* sval = nullptr;
+  int32_t* soff = nullptr;
+  int nw = 0;
+  if constexpr (EMIT) {
+    skey = p.sup.key + wreg * p.sup.cap;
+    sval = p.sup.val + wreg * p.sup.cap;
+    soff = p.sup.off + size_t(bh) * nQB * nKB * 4 + w;
+  }
+
   const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
   const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
   const int e0 = qp[qb], e1 = qp[qb + 1];
@@ -89,15 +101,37 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
     const int b = (e - e0) & 1;
     f32x4 acc[4];
     rows_x_frag<D>(acc, sm.K[b], qf, lane);
+    uint32_t ebase = 0;  // entry of score slot (f, r): ebase + 16 f + r
+    if constexpr (EMIT) {
+      if (lane == 0) soff[size_t(e) * 4] = nw;
+      ebase = (uint32_t(c16) << 28) | uint32_t(ql[e] * kBlock + 4 * g);
+    }
     // p for every score, then masked: no per-score branches
     auto weights = [&](auto partial) {
       for (int f = 0; f < 4; ++f)
         for (int r = 0; r < 4; ++r) {
-          float pv = pow_clipped<PC>(clip(acc[f][r]), a);
+          float v = clip(acc[f][r]);  // max(u, 0)
           if constexpr (decltype(partial)::value)
-            pv = sm.kid[b][16 * f + 4 * g + r] <= qpos ? pv : 0.0f;
+            v = sm.kid[b][16 * f + 4 * g + r] <= qpos ? v : 0.0f;
+          const float pv = pow_clipped<PC>(v, a);
           acc[f][r] = pv;
           rowsum += pv;
+          if constexpr (EMIT) {
+            // the wave's entries of this slot, in lane order after the
+            // entries so far
+            const uint64_t m = __ballot(v > 0.0f);
+            if (m != 0) {
+              if (v > 0.0f) {
+                const int pos = nw + int(__builtin_amdgcn_mbcnt_hi(
+                                         uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+                if (pos < p.sup.cap) {
+                  skey[pos] = ebase + uint32_t(16 * f + r);
+                  sval[pos] = v;
+                }
+              }
+              nw += __builtin_popcountll(m);
+            }
+          }
         }
     };
     if (sm.full[b] != 0) weights(std::false_type{});
@@ -122,18 +156,25 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
       }
     if (g == 0) p.norms[row] = norm;
   }
+  if constexpr (EMIT) {
+    if (lane == 0) p.sup.cnt[wreg] = nw;
+  }
 }
 
-template <typename T, int D>
-hipError_t launch_td(const ForwardParams& p, hipStream_t s) {
+template <typename T, int D, bool EMIT>
+hipError_t launch_tde(const ForwardParams& p, hipStream_t s) {
   dim3 grid(p.d.nQB * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
-    case kA15: hipLaunchKernelGGL((forward_kernel<T, D, kE2>), grid, dim3(kThreads), 0, s, p); break;
-    case kA20: hipLaunchKernelGGL((forward_kernel<T, D, kE1>), grid, dim3(kThreads), 0, s, p); break;
-    case kA125: hipLaunchKernelGGL((forward_kernel<T, D, kE4>), grid, dim3(kThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((forward_kernel<T, D, kEGen>), grid, dim3(kThreads), 0, s, p); break;
+    case kA15: hipLaunchKernelGGL((forward_kernel<T, D, kE2, EMIT>), grid, dim3(kThreads), 0, s, p); break;
+    case kA20: hipLaunchKernelGGL((forward_kernel<T, D, kE1, EMIT>), grid, dim3(kThreads), 0, s, p); break;
+    case kA125: hipLaunchKernelGGL((forward_kernel<T, D, kE4, EMIT>), grid, dim3(kThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL((forward_kernel<T, D, kEGen, EMIT>), grid, dim3(kThreads), 0, s, p); break;
   }
   return hipGetLastError();
+}
+template <typename T, int D>
+hipError_t launch_td(const ForwardParams& p, hipStream_t s) {
+  return p.sup.key ? launch_tde<T, D, true>(p, s) : launch_tde<T, D, false>(p, s);
 }
 
 }  // namespace

@@ -39,7 +39,8 @@ __version__ = "0.1.0"
 def forward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, k_keep: int = 8):
     """Reference-compatible native forward (adasplashattention.cu:537-609)."""
     Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
-    out, _ = ops.splash_forward(Q, K, V, qi, ki, ops.clamp_alpha(alpha), k_keep, sm_scale)
+    out, _ = ops.splash_forward(Q, K, V, qi, ki, ops.clamp_alpha(alpha), k_keep, sm_scale,
+                                with_support=False)
     return out
 
 

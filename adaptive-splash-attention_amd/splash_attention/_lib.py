@@ -12,7 +12,7 @@ import threading
 
 from . import _build
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 ASA_OK = 0
 ASA_ERR_INVALID_ARGUMENT = 1
@@ -65,13 +65,17 @@ class State(ctypes.Structure):
         ("k_list", ctypes.c_void_p),
         ("topk_idx", ctypes.c_void_p),
         ("topk_val", ctypes.c_void_p),
+        ("sup_key", ctypes.c_void_p),
+        ("sup_val", ctypes.c_void_p),
+        ("sup_off", ctypes.c_void_p),
+        ("sup_cnt", ctypes.c_void_p),
     ]
 
 
 class Sizes(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in (
         "taus", "norms", "mask", "q_ptr", "q_list", "k_ptr", "k_list", "topk_idx", "topk_val",
-        "workspace")]
+        "sup_key", "sup_val", "sup_off", "sup_cnt", "workspace")]
 
 
 class ASAError(RuntimeError):

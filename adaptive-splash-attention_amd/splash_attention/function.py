@@ -24,7 +24,9 @@ from . import library, ops
 class SplashAttentionFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode):
-        out, st = ops.splash_forward(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale)
+        # support lists only when a backward can follow
+        out, st = ops.splash_forward(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale,
+                                     with_support=any(ctx.needs_input_grad[:3]))
         ctx.params = (alpha, k_keep, sm_scale, grad_mode)
         ctx.save_for_backward(Q, K, V, Q_idx, K_idx, out, *st.tensors())
         return out
@@ -34,7 +36,7 @@ class SplashAttentionFunction(torch.autograd.Function):
     def backward(ctx, dout):
         Q, K, V, Q_idx, K_idx, out, *state = ctx.saved_tensors
         alpha, k_keep, sm_scale, grad_mode = ctx.params
-        st = ops.SplashState(*state)
+        st = ops.SplashState.from_tensors(state)
         dQ, dK, dV = ops.splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st, alpha, k_keep,
                                          sm_scale, grad_mode)
         return dQ, dK, dV, None, None, None, None, None, None

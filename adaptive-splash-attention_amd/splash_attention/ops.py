@@ -37,17 +37,37 @@ class SplashState:
     k_list: torch.Tensor     # [BH, nKB*nQB] int32
     topk_idx: torch.Tensor | None = None  # [BH, NQ, k] int32
     topk_val: torch.Tensor | None = None  # [BH, NQ, k] float32
+    # support lists (asa_state.sup_*): the (row, key) pairs with u > 0
+    sup_key: torch.Tensor | None = None   # [BH*nQB*4, cap] int32 (uint32 bits)
+    sup_val: torch.Tensor | None = None   # [BH*nQB*4, cap] float32
+    sup_off: torch.Tensor | None = None   # [BH, nQB*nKB, 4] int32
+    sup_cnt: torch.Tensor | None = None   # [BH*nQB*4] int32
+
+    SUPPORT = ("sup_key", "sup_val", "sup_off", "sup_cnt")
 
     def c_struct(self) -> _lib.State:
         def ptr(t):
             return None if t is None else t.data_ptr()
         return _lib.State(ptr(self.taus), ptr(self.norms), ptr(self.mask), ptr(self.q_ptr),
                           ptr(self.q_list), ptr(self.k_ptr), ptr(self.k_list),
-                          ptr(self.topk_idx), ptr(self.topk_val))
+                          ptr(self.topk_idx), ptr(self.topk_val), ptr(self.sup_key),
+                          ptr(self.sup_val), ptr(self.sup_off), ptr(self.sup_cnt))
 
     def tensors(self) -> tuple:
-        return (self.taus, self.norms, self.mask, self.q_ptr, self.q_list, self.k_ptr,
+        """The tensors a backward needs (support lists included when present)."""
+        base = (self.taus, self.norms, self.mask, self.q_ptr, self.q_list, self.k_ptr,
                 self.k_list)
+        if self.sup_key is None:
+            return base
+        return base + tuple(getattr(self, n) for n in self.SUPPORT)
+
+    @classmethod
+    def from_tensors(cls, ts) -> "SplashState":
+        st = cls(*ts[:7])
+        if len(ts) > 7:
+            for n, t in zip(cls.SUPPORT, ts[7:]):
+                setattr(st, n, t)
+        return st
 
 
 def clamp_alpha(alpha: float) -> float:
@@ -142,7 +162,8 @@ def make_problem(B, H, NQ, NK, d, dtype, alpha, k_keep, sm_scale) -> _lib.Proble
                         float(sm_scale), _DTYPES[dtype] if isinstance(dtype, torch.dtype) else dtype)
 
 
-def alloc_state(p: _lib.Problem, device, with_topk: bool = False) -> SplashState:
+def alloc_state(p: _lib.Problem, device, with_topk: bool = False,
+                with_support: bool = False) -> SplashState:
     BH = p.batch * p.heads
     nQB = -(-p.nq // BLOCK_M)
     nKB = -(-p.nk // BLOCK_N)
@@ -160,7 +181,19 @@ def alloc_state(p: _lib.Problem, device, with_topk: bool = False) -> SplashState
     if with_topk:
         st.topk_idx = torch.empty((BH, p.nq, p.k_keep), **i32)
         st.topk_val = torch.empty((BH, p.nq, p.k_keep), **f32)
+    if with_support:
+        cap = support_capacity(p)
+        st.sup_key = torch.empty((BH * nQB * 4, cap), **i32)
+        st.sup_val = torch.empty((BH * nQB * 4, cap), **f32)
+        st.sup_off = torch.empty((BH, nQB * nKB, 4), **i32)
+        st.sup_cnt = torch.empty((BH * nQB * 4,), **i32)
     return st
+
+
+def support_capacity(p: _lib.Problem) -> int:
+    """Support-list entries per 16-row wave region (asa_state.sup_key)."""
+    nQB = -(-p.nq // BLOCK_M)
+    return _lib.query_sizes(p).sup_key // (4 * p.batch * p.heads * nQB * 4)
 
 
 def workspace(p: _lib.Problem, device) -> torch.Tensor:
@@ -170,12 +203,14 @@ def workspace(p: _lib.Problem, device) -> torch.Tensor:
 
 
 def splash_forward(Q, K, V, Q_idx, K_idx, alpha: float, k_keep: int, sm_scale=None,
-                   with_topk: bool = False):
-    """Forward pass; returns (out, SplashState).  Inputs as check_inputs() returns them."""
+                   with_topk: bool = False, with_support: bool = True):
+    """Forward pass; returns (out, SplashState).  Inputs as check_inputs() returns them.
+    with_support records the rows' support lists for a sparse backward (skip
+    it for inference)."""
     lib = _lib.load()
     B, H, NQ, d = Q.shape
     p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale)
-    st = alloc_state(p, Q.device, with_topk)
+    st = alloc_state(p, Q.device, with_topk, with_support)
     out = torch.empty_like(Q)
     ws = workspace(p, Q.device)
     cst = st.c_struct()
