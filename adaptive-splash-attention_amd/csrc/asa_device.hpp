@@ -34,6 +34,11 @@ __device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Rank of the calling lane among the set lanes of m below it.
+__device__ __forceinline__ int lane_rank(uint64_t m) {
+  return int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+}
+
 // A packed bf16 pair with the given bits, held in a scalar register that
 // the compiler cannot fold into an inline constant.  The empty asm is not
 // volatile, so it is no scheduling barrier and can be hoisted out of loops.

@@ -13,14 +13,15 @@ struct Dims {
   float scale;
 };
 
-// Support-list buffers shared by the forward (writer) and the backward.
-struct SupportLists {
-  uint32_t* key;
-  float* val;
-  float* ds;       // backward: ds of every entry (written by the dQ pass)
-  int32_t* off;
-  int32_t* cnt;
-  int cap;         // entries per wave region
+// Support masks written by the forward and read by the backward: for the
+// tile at the head's q_list position e (query block qb, key block kb), bit
+// 4 f + r of
+//   mask[((bh * nQB * nKB + e) * 4 + w) * 64 + 4 c + g]
+// is set iff u > 0 for row qb * 64 + 16 w + c and key kb * 64 + 16 f + 4 g + r
+// (w, c < 16, g, f, r < 4): a row's four masks of a tile form one 8-byte
+// word, a tile's masks 512 bytes.
+struct SupportMasks {
+  uint16_t* mask;  // nullptr: no masks (the backward runs the dense passes)
 };
 
 struct SelectParams {
@@ -60,15 +61,15 @@ struct ForwardParams {
   const int32_t* q_list;
   void* out;
   float* norms;
-  // Support lists (optional: sup_key == nullptr emits nothing).  Every wave
-  // of a query block (16 rows) owns a region of sup_cap entries at
-  // ((bh * nQB + qb) * 4 + w) * sup_cap; entry = key index | row-in-wave << 28
-  // in sup_key and v = max(u, 0) in sup_val, for every score of the forward
-  // with u > 0, in (tile, score slot, lane) order.  sup_off[(bh * nQB * nKB
-  // + e) * 4 + w] = the wave's entry count before tile e (the head's
-  // q_list position e); sup_cnt[(bh * nQB + qb) * 4 + w] = its total, which
-  // may exceed sup_cap (then only the first sup_cap entries were written).
-  SupportLists sup;
+  // Support masks (optional: sup.mask == nullptr writes none).
+  SupportMasks sup;
+};
+
+// Per-row constants of the support-mask backward, written by its dQ pass
+// for its dK/dV pass: ClippedU's nt, lo, hi; 1/(sum p + EPS); the gradient
+// factor c and cs = -c shift (ds = w (c dp + cs)).
+struct alignas(16) RowRec {
+  float nt, lo, hi, invn, c, cs, pad0, pad1;
 };
 
 struct BackwardParams {
@@ -83,6 +84,7 @@ struct BackwardParams {
   const int32_t* k_idx;
   const float* taus;
   const float* norms;
+  const uint8_t* mask;
   const int32_t* q_ptr;
   const int32_t* q_list;
   const int32_t* k_ptr;
@@ -91,6 +93,9 @@ struct BackwardParams {
   void* dq;
   void* dk;
   void* dv;
+  SupportMasks sup;  // mask == nullptr: dense passes
+  RowRec* rowrec;    // workspace [BH * NQ] (support-mask passes)
+  int32_t* posmap;   // workspace [BH, nQB * nKB] (support-mask dK/dV pass)
 };
 
 // Each launcher returns the launch status; `name` receives the kernel's
@@ -108,6 +113,8 @@ hipError_t launch_forward(const ForwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_delta(const BackwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_dq(const BackwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BackwardParams& p, bool bf16, hipStream_t s);
+hipError_t launch_bwd_dq_sparse(const BackwardParams& p, bool bf16, hipStream_t s);
+hipError_t launch_bwd_dkdv_sparse(const BackwardParams& p, bool bf16, hipStream_t s);
 
 // Kernel-timing hooks implemented in capi.cpp (no-ops unless profiling).
 void profile_begin(const char* name, hipStream_t s);

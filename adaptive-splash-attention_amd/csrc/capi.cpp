@@ -101,16 +101,15 @@ size_t tkv_bytes(const Shape& s) {
   return (b + 15) & ~size_t(15);
 }
 
-// Byte offset of the support entries' ds in the backward workspace (after
-// the two floats per row), 16-byte aligned.
-size_t bwd_ds_offset(const Shape& s) {
+// Byte offset of the per-row records of the support-mask backward in its
+// workspace (after the two floats per row), 16-byte aligned.
+size_t bwd_rec_offset(const Shape& s) {
   return (2 * size_t(s.BH) * s.NQ * sizeof(float) + 15) & ~size_t(15);
 }
 
-// Support-list entries per wave region (16 query rows).
-int support_cap(const Shape& s) { return 16 * (s.k * 2 > 64 ? s.k * 2 : 64); }
-size_t support_entries(const Shape& s) {
-  return size_t(s.BH) * s.nQB * 4 * size_t(support_cap(s));
+// Then the tile position map of the support-mask dK/dV pass.
+size_t bwd_map_offset(const Shape& s) {
+  return bwd_rec_offset(s) + size_t(s.BH) * s.NQ * sizeof(asa::RowRec);
 }
 
 void sizes_of(const Shape& s, asa_sizes* z) {
@@ -125,14 +124,12 @@ void sizes_of(const Shape& s, asa_sizes* z) {
   z->k_list = blocks * sizeof(int32_t);
   z->topk_idx = rows * s.k * sizeof(int32_t);
   z->topk_val = rows * s.k * sizeof(float);
-  z->sup_key = support_entries(s) * sizeof(uint32_t);
-  z->sup_val = support_entries(s) * sizeof(float);
-  z->sup_off = blocks * 4 * sizeof(int32_t);
-  z->sup_cnt = size_t(s.BH) * s.nQB * 4 * sizeof(int32_t);
+  z->sup_mask = blocks * 256 * sizeof(uint16_t);
   // forward: the rows' sorted top-k values and the key blocks' position
-  // bounds; backward: two floats per row, then ds of every support entry
+  // bounds; backward: two floats per row, a 32-byte record per row and an
+  // int per tile
   const size_t fwd_ws = tkv_bytes(s) + size_t(s.BH) * s.nKB * 2 * sizeof(int32_t);
-  const size_t bwd_ws = bwd_ds_offset(s) + support_entries(s) * sizeof(float);
+  const size_t bwd_ws = bwd_map_offset(s) + blocks * sizeof(int32_t);
   z->workspace = fwd_ws > bwd_ws ? fwd_ws : bwd_ws;
 }
 
@@ -143,25 +140,7 @@ int check_state(const asa_state* st, bool need_norms) {
     return fail(ASA_ERR_INVALID_ARGUMENT, "a required state buffer is NULL");
   if ((st->topk_idx == nullptr) != (st->topk_val == nullptr))
     return fail(ASA_ERR_INVALID_ARGUMENT, "topk_idx and topk_val must be both set or both NULL");
-  const int nsup = (st->sup_key != nullptr) + (st->sup_val != nullptr) + (st->sup_off != nullptr) +
-                   (st->sup_cnt != nullptr);
-  if (nsup != 0 && nsup != 4)
-    return fail(ASA_ERR_INVALID_ARGUMENT,
-                "sup_key, sup_val, sup_off and sup_cnt must be all set or all NULL");
   return ASA_OK;
-}
-
-asa::SupportLists support_of(const Shape& sh, const asa_state* st, float* ds) {
-  asa::SupportLists l{};
-  if (st->sup_key) {
-    l.key = st->sup_key;
-    l.val = st->sup_val;
-    l.ds = ds;
-    l.off = st->sup_off;
-    l.cnt = st->sup_cnt;
-    l.cap = support_cap(sh);
-  }
-  return l;
 }
 
 // Candidate capacity per row of the select kernel on the current device
@@ -309,7 +288,7 @@ int asa_forward(const asa_problem* p, const void* q, const void* k, const void* 
   fp.q_list = st->q_list;
   fp.out = out;
   fp.norms = st->norms;
-  fp.sup = support_of(sh, st, nullptr);
+  fp.sup.mask = st->sup_mask;
   asa::profile_begin("forward", s);
   hipError_t e = asa::launch_forward(fp, sh.bf16, s);
   asa::profile_end(s);
@@ -345,6 +324,7 @@ int asa_backward(const asa_problem* p, int32_t grad_mode, const void* q, const v
   bp.k_idx = k_idx;
   bp.taus = st->taus;
   bp.norms = st->norms;
+  bp.mask = st->mask;
   bp.q_ptr = st->q_ptr;
   bp.q_list = st->q_list;
   bp.k_ptr = st->k_ptr;
@@ -353,6 +333,9 @@ int asa_backward(const asa_problem* p, int32_t grad_mode, const void* q, const v
   bp.dq = dq;
   bp.dk = dk;
   bp.dv = dv;
+  bp.sup.mask = st->sup_mask;
+  bp.rowrec = reinterpret_cast<asa::RowRec*>(static_cast<char*>(workspace) + bwd_rec_offset(sh));
+  bp.posmap = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + bwd_map_offset(sh));
 
   hipError_t e;
   if (grad_mode == ASA_GRAD_REFERENCE) {
@@ -360,6 +343,18 @@ int asa_backward(const asa_problem* p, int32_t grad_mode, const void* q, const v
     e = asa::launch_bwd_delta(bp, sh.bf16, s);
     asa::profile_end(s);
     if (int rc = check_hip(e, "backward delta kernel launch")) return rc;
+  }
+  if (bp.sup.mask) {
+    // support masks: only the listed (row, key) pairs
+    asa::profile_begin("bwd_dq_sparse", s);
+    e = asa::launch_bwd_dq_sparse(bp, sh.bf16, s);
+    asa::profile_end(s);
+    if (int rc = check_hip(e, "backward sparse dQ kernel launch")) return rc;
+    asa::profile_begin("bwd_dkdv_sparse", s);
+    e = asa::launch_bwd_dkdv_sparse(bp, sh.bf16, s);
+    asa::profile_end(s);
+    if (int rc = check_hip(e, "backward sparse dK/dV kernel launch")) return rc;
+    return ok();
   }
   asa::profile_begin("bwd_dq", s);
   e = asa::launch_bwd_dq(bp, sh.bf16, s);

@@ -65,17 +65,9 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   for (int db = 0; db < D / 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
   float rowsum = 0.0f;
 
-  // Support emission: this wave's region and its entry count (wave-uniform).
-  const size_t wreg = (size_t(bh) * nQB + qb) * 4 + w;
-  uint32_t* skey = nullptr;
-  float* sval = nullptr;
-  int32_t* soff = nullptr;
-  int nw = 0;
-  if constexpr (EMIT) {
-    skey = p.sup.key + wreg * p.sup.cap;
-    sval = p.sup.val + wreg * p.sup.cap;
-    soff = p.sup.off + size_t(bh) * nQB * nKB * 4 + w;
-  }
+  // Support masks: this wave's 64 lanes x 16 bits for each tile.
+  uint16_t* smask = nullptr;
+  if constexpr (EMIT) smask = p.sup.mask + size_t(bh) * nQB * nKB * 256 + w * 64 + 4 * c16 + g;
 
   const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
   const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
@@ -101,37 +93,29 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
     const int b = (e - e0) & 1;
     f32x4 acc[4];
     rows_x_frag<D>(acc, sm.K[b], qf, lane);
-    uint32_t ebase = 0;  // entry of score slot (f, r): ebase + 16 f + r
-    if constexpr (EMIT) {
-      if (lane == 0) soff[size_t(e) * 4] = nw;
-      ebase = (uint32_t(c16) << 28) | uint32_t(ql[e] * kBlock + 4 * g);
-    }
-    // p for every score, then masked: no per-score branches
+    // p for every score, then masked: no per-score branches.  With support
+    // masks, v = max(u, 0) of all 16 scores is formed first and the lane's
+    // 16-bit mask of v > 0 is stored before the powers are taken.
     auto weights = [&](auto partial) {
       for (int f = 0; f < 4; ++f)
         for (int r = 0; r < 4; ++r) {
           float v = clip(acc[f][r]);  // max(u, 0)
           if constexpr (decltype(partial)::value)
             v = sm.kid[b][16 * f + 4 * g + r] <= qpos ? v : 0.0f;
-          const float pv = pow_clipped<PC>(v, a);
+          acc[f][r] = v;
+        }
+      if constexpr (EMIT) {
+        // bit 4f + r <- u > 0 for key 16f + 4g + r of the lane's row
+        uint32_t m = 0;
+        for (int f = 3; f >= 0; --f)
+          for (int r = 3; r >= 0; --r) m = 2u * m + (acc[f][r] > 0.0f ? 1u : 0u);
+        smask[size_t(e) * 256] = uint16_t(m);
+      }
+      for (int f = 0; f < 4; ++f)
+        for (int r = 0; r < 4; ++r) {
+          const float pv = pow_clipped<PC>(acc[f][r], a);
           acc[f][r] = pv;
           rowsum += pv;
-          if constexpr (EMIT) {
-            // the wave's entries of this slot, in lane order after the
-            // entries so far
-            const uint64_t m = __ballot(v > 0.0f);
-            if (m != 0) {
-              if (v > 0.0f) {
-                const int pos = nw + int(__builtin_amdgcn_mbcnt_hi(
-                                         uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
-                if (pos < p.sup.cap) {
-                  skey[pos] = ebase + uint32_t(16 * f + r);
-                  sval[pos] = v;
-                }
-              }
-              nw += __builtin_popcountll(m);
-            }
-          }
         }
     };
     if (sm.full[b] != 0) weights(std::false_type{});
@@ -156,9 +140,6 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
       }
     if (g == 0) p.norms[row] = norm;
   }
-  if constexpr (EMIT) {
-    if (lane == 0) p.sup.cnt[wreg] = nw;
-  }
 }
 
 template <typename T, int D, bool EMIT>
@@ -174,7 +155,7 @@ hipError_t launch_tde(const ForwardParams& p, hipStream_t s) {
 }
 template <typename T, int D>
 hipError_t launch_td(const ForwardParams& p, hipStream_t s) {
-  return p.sup.key ? launch_tde<T, D, true>(p, s) : launch_tde<T, D, false>(p, s);
+  return p.sup.mask ? launch_tde<T, D, true>(p, s) : launch_tde<T, D, false>(p, s);
 }
 
 }  // namespace

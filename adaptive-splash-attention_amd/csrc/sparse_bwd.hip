@@ -1,0 +1,472 @@
+// Support-mask backward: dQ, dK, dV over the (row, key) pairs the forward
+// weighted with u > 0 (its support masks, asa_state.sup_mask), instead of
+// over whole 64 x 64 tiles.
+//
+// Every backward term lives on a row's support: the weights p,
+// w = u^((2-a)/(a-1)) and both gradient modes' ds vanish where u <= 0 (the
+// reference backward, adasplashattention.cu:343-535, visits every key and
+// multiplies by those zeros).  With a few tens of supported keys per row
+// against thousands of visible ones, the dense tile passes spend almost
+// all their work on zeros.  These kernels visit only the listed pairs, in
+// a fixed order (no atomics: the results are deterministic), and form
+// every sum in fp32.  A listed pair's score is recomputed in fp32 from the
+// gathered rows (the forward formed it on MFMA; the two differ by rounding
+// only, and a pair whose recomputed u is not positive gets zero weight).
+//
+//   dQ pass    one 256-thread block per query block, one wave per 16 rows,
+//              a group of lanes (16 bytes of the head dimension each) per
+//              row.  Phase A walks the row's tile masks and lists its keys
+//              in LDS; phase B gathers K_j and V_j for the listed keys in
+//              lock-step batches: s = q.k_j, w, dp = dO.v_j, and the fp32
+//              sums A = sum w dp k_j, B = sum w k_j, sum w, sum w dp give
+//              dQ = scale c (A - shift B).  It also writes each row's
+//              constants for the dK/dV pass.
+//   dK/dV pass one block per slice of a key block, one lane group per key.
+//              Phase A walks the key block's query tiles (key-major CSR):
+//              the tile's masks give, by one ballot per key, the rows that
+//              list the key, appended to the key's list in LDS in row
+//              order; phase B gathers q_i and dO_i for the listed rows:
+//              dK_j += ds q_i, dV_j += P dO_i.
+#include <type_traits>
+
+#include "asa_device.hpp"
+#include "asa_launch.hpp"
+#include "asa_tiles.hpp"
+
+namespace asa {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowList = 64;   // keys listed per row before a dQ phase B
+constexpr int kKeyList = 128;  // rows listed per key before a dK/dV phase B
+constexpr int kBatch = 4;      // entries whose gathers are in flight together
+constexpr int kChunk = 16;     // tiles whose masks are fetched together
+
+// 16 bytes of a row: raw (as loaded) and as floats.
+template <typename T> struct Chunk;
+template <> struct Chunk<u16> {
+  static constexpr int E = 8;
+  static __device__ __forceinline__ uint4 raw(const u16* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ void unpack(const uint4& v, float (&x)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  static __device__ __forceinline__ void load(const u16* p, float (&x)[8]) { unpack(raw(p), x); }
+  static __device__ __forceinline__ void store(u16* p, const float (&x)[8]) {
+    uint32_t w[4];
+    for (int i = 0; i < 4; ++i)
+      w[i] = uint32_t(f32_to_bf16(x[2 * i])) | (uint32_t(f32_to_bf16(x[2 * i + 1])) << 16);
+    *reinterpret_cast<uint4*>(p) = uint4{w[0], w[1], w[2], w[3]};
+  }
+};
+template <> struct Chunk<float> {
+  static constexpr int E = 4;
+  static __device__ __forceinline__ uint4 raw(const float* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ void unpack(const uint4& v, float (&x)[4]) {
+    x[0] = __uint_as_float(v.x);
+    x[1] = __uint_as_float(v.y);
+    x[2] = __uint_as_float(v.z);
+    x[3] = __uint_as_float(v.w);
+  }
+  static __device__ __forceinline__ void load(const float* p, float (&x)[4]) { unpack(raw(p), x); }
+  static __device__ __forceinline__ void store(float* p, const float (&x)[4]) {
+    *reinterpret_cast<float4*>(p) = float4{x[0], x[1], x[2], x[3]};
+  }
+};
+
+// Sum over aligned groups of G lanes (G a power of two <= 32) by lane
+// exchanges: each step adds a lane's value and its partner's, so every lane
+// of a group gets a bit-identical sum.
+template <int G>
+__device__ __forceinline__ float group_lanes_sum(float v) {
+  auto x = [](float a, auto m) {
+    constexpr int M = decltype(m)::value;
+    return __uint_as_float(lane_xor<M>(__float_as_uint(a)));
+  };
+  if constexpr (G >= 2) v += x(v, std::integral_constant<int, 1>{});
+  if constexpr (G >= 4) v += x(v, std::integral_constant<int, 2>{});
+  if constexpr (G >= 8) v += x(v, std::integral_constant<int, 4>{});
+  if constexpr (G >= 16) v += x(v, std::integral_constant<int, 8>{});
+  if constexpr (G >= 32) v += x(v, std::integral_constant<int, 16>{});
+  return v;
+}
+
+template <int E>
+__device__ __forceinline__ float dot(const float (&a)[E], const float (&b)[E]) {
+  float s = 0.0f;
+  for (int e = 0; e < E; ++e) s = fmaf(a[e], b[e], s);
+  return s;
+}
+
+// Maximum of a lane-group-uniform value over the wave's groups of G lanes.
+template <int G>
+__device__ __forceinline__ int groups_max(int v) {
+  for (int o = G; o < kWave; o <<= 1) v = max(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Position map: posmap[bh][qb * nKB + kb] = the head's q_list position of
+// the tile (qb, kb), for every active tile (the dK/dV pass finds the
+// tile's masks through it).  One wave per query block.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void posmap_kernel(BackwardParams p) {
+  const int nQB = p.d.nQB, nKB = p.d.nKB;
+  const int t = threadIdx.x, lane = t & 63;
+  const int task = blockIdx.x * (kThreads / kWave) + (t >> 6);
+  if (task >= nQB * p.d.BH) return;
+  const int qb = task % nQB, bh = task / nQB;
+  const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
+  const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
+  int32_t* pm = p.posmap + size_t(bh) * nQB * nKB + size_t(qb) * nKB;
+  for (int e = qp[qb] + lane; e < qp[qb + 1]; e += kWave) pm[ql[e]] = e;
+}
+
+// ---------------------------------------------------------------------------
+// dQ
+// ---------------------------------------------------------------------------
+template <typename T, int D, int AC, bool REF>
+__global__ __launch_bounds__(kThreads, 3) void dq_sparse_kernel(BackwardParams p) {
+  using C = Chunk<T>;
+  constexpr int E = C::E;
+  constexpr int LPR = D / E;          // lanes per row (16 bytes each)
+  constexpr int RPR = kWave / LPR;    // rows per round of a wave
+  constexpr int PW = AlphaPow<AC>::W;
+  __shared__ int s_list[4][RPR][kRowList];
+  __shared__ uint64_t s_mw[4][kChunk][16];  // mask words of a chunk of tiles: [tile][row]
+  __shared__ int s_kb[4][kChunk];           // first key of each tile
+  const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
+  const int qb = task % nQB, bh = task / nQB;
+  const int sub = lane % LPR, grp = lane / LPR;
+
+  const float alpha = p.d.alpha, am1 = alpha - 1.0f, ew = (2.0f - alpha) / am1;
+  const float scale = p.d.scale;
+  const size_t rows = size_t(p.d.BH) * NQ;
+  const T* Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
+  const T* Vb = static_cast<const T*>(p.v) + size_t(bh) * NK * D;
+  const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
+  const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
+  const int e0 = qp[qb], e1 = qp[qb + 1];
+  // the wave's masks of tile e: row c's word at + e * 256 + 4 c
+  const uint16_t* wmask = p.sup.mask + size_t(bh) * nQB * nKB * 256 + w * 64;
+  int* list = s_list[w][grp];
+  auto weight = [&](float v) {
+    float wv = pow_clipped<PW>(v, ew);
+    if constexpr (REF) wv = v > kEps ? wv : 0.0f;  // the reference's u > EPS
+    return wv;
+  };
+
+  for (int r0 = 0; r0 < 16; r0 += RPR) {
+    const int rr = r0 + grp;  // row within the wave
+    const int qrow = qb * kBlock + 16 * w + rr;
+    const bool ok = qrow < NQ;
+    const size_t row = size_t(bh) * NQ + (ok ? qrow : 0);
+    float qv[E], dO[E];
+    if (ok) {
+      C::load(static_cast<const T*>(p.q) + row * D + sub * E, qv);
+      C::load(static_cast<const T*>(p.dout) + row * D + sub * E, dO);
+    } else {
+      for (int x = 0; x < E; ++x) qv[x] = dO[x] = 0.0f;
+    }
+    const ClippedU clip(am1, scale, ok ? p.taus[row] : 0.0f, ok);
+
+    float a1[E], a2[E];
+    for (int x = 0; x < E; ++x) a1[x] = a2[x] = 0.0f;
+    float sw = 0.0f, swdp = 0.0f;
+
+    // phase B: the listed keys, kBatch at a time in every row group
+    auto drain = [&](int cnt) {
+      const int nmax = groups_max<LPR>(cnt);
+      for (int q = 0; q < nmax; q += kBatch) {
+        int key[kBatch];
+        bool val[kBatch];
+        uint4 kraw[kBatch], vraw[kBatch];
+        for (int u = 0; u < kBatch; ++u) {
+          val[u] = q + u < cnt;
+          key[u] = val[u] ? list[q + u] : 0;
+        }
+        for (int u = 0; u < kBatch; ++u) {
+          kraw[u] = C::raw(Kb + size_t(key[u]) * D + sub * E);
+          vraw[u] = C::raw(Vb + size_t(key[u]) * D + sub * E);
+        }
+        for (int u = 0; u < kBatch; ++u) {
+          float kr[E], vr[E];
+          C::unpack(kraw[u], kr);
+          C::unpack(vraw[u], vr);
+          const float s = group_lanes_sum<LPR>(dot<E>(qv, kr));
+          const float dp = group_lanes_sum<LPR>(dot<E>(dO, vr));
+          if (val[u]) {
+            const float wv = weight(clip(s));
+            sw += wv;
+            const float wdp = wv * dp;
+            swdp += wdp;
+            for (int x = 0; x < E; ++x) {
+              a1[x] = fmaf(wdp, kr[x], a1[x]);
+              a2[x] = fmaf(wv, kr[x], a2[x]);
+            }
+          }
+        }
+      }
+    };
+
+    for (int c0 = e0; c0 < e1; c0 += kChunk) {
+      const int nt = min(kChunk, e1 - c0);
+      // the chunk's mask words: 4 tiles (16 rows each) per wave load
+      for (int s4 = 0; s4 < kChunk; s4 += 4) {
+        const int tt = s4 + (lane >> 4);
+        if (tt < nt)
+          s_mw[w][tt][lane & 15] =
+              *reinterpret_cast<const uint64_t*>(wmask + size_t(c0 + tt) * 256 + 4 * (lane & 15));
+      }
+      if (lane < nt) s_kb[w][lane] = ql[c0 + lane] * kBlock;
+      // phase A over the chunk: list up to kRowList keys per row (tile
+      // order, then g, f, r), drain, continue where the list filled up
+      int tt = 0, kbase = 0;
+      uint64_t bits = 0;
+      bool more = ok;
+      while (__any(more)) {
+        int cnt = 0;
+        while (more && cnt < kRowList) {
+          if (bits == 0) {
+            if (tt >= nt) {
+              more = false;
+              break;
+            }
+            bits = s_mw[w][tt][rr];
+            kbase = s_kb[w][tt];
+            ++tt;
+            continue;
+          }
+          const int b = __builtin_ctzll(bits);
+          bits &= bits - 1;
+          // bit 16 g + 4 f + r -> key 16 f + 4 g + r
+          if (sub == 0) list[cnt] = kbase + 16 * ((b >> 2) & 3) + 4 * (b >> 4) + (b & 3);
+          ++cnt;
+        }
+        drain(cnt);
+      }
+    }
+
+    if (ok) {
+      const float norm = p.norms[row];
+      float cfac, shift;
+      if constexpr (REF) {
+        cfac = p.delta[rows + row];
+        shift = p.delta[row];
+      } else {
+        cfac = static_cast<float>(pow(static_cast<double>(norm + kEps), static_cast<double>(alpha) - 2.0));
+        shift = sw > 0.0f ? swdp / sw : 0.0f;
+        if (!finite(shift)) shift = 0.0f;
+      }
+      // dQ_i = scale c (A - shift B) = scale sum_j c w_j (dp_j - shift) k_j
+      const float cs = scale * cfac;
+      float o[E];
+      for (int x = 0; x < E; ++x) {
+        const float v = cs * fmaf(-shift, a2[x], a1[x]);
+        o[x] = finite(v) ? v : 0.0f;
+      }
+      C::store(static_cast<T*>(p.dq) + row * D + sub * E, o);
+      if (sub == 0)
+        p.rowrec[row] = RowRec{clip.nt, clip.lo, clip.hi, 1.0f / (norm + kEps), cfac, -cfac * shift,
+                               0.0f, 0.0f};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV
+// ---------------------------------------------------------------------------
+template <typename T, int D> constexpr int keys_per_block() { return 4 * (kWave / (D / Chunk<T>::E)); }
+
+template <typename T, int D, int AC, bool REF>
+__global__ __launch_bounds__(kThreads, 3) void dkdv_sparse_kernel(BackwardParams p) {
+  using C = Chunk<T>;
+  constexpr int E = C::E;
+  constexpr int LPR = D / E;          // lanes per key (16 bytes each)
+  constexpr int KPW = kWave / LPR;    // keys per wave
+  constexpr int KPB = 4 * KPW;        // keys per block
+  constexpr int SLICES = kBlock / KPB;
+  constexpr int PP = AlphaPow<AC>::P, PW = AlphaPow<AC>::W;
+  __shared__ int s_list[4][KPW][kKeyList];
+  __shared__ int s_cnt[4][KPW];
+  const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int task = xcd_task(blockIdx.x, nKB * SLICES * p.d.BH);
+  const int slice = task % SLICES, kb = (task / SLICES) % nKB, bh = task / (SLICES * nKB);
+  const int sub = lane % LPR, grp = lane / LPR;
+  const int jb = slice * KPB + w * KPW;  // first key (within the block) of this wave
+  const int j = kb * kBlock + jb + grp;  // this group's key
+  const bool jok = j < NK;
+  const size_t krow = size_t(bh) * NK + (jok ? j : 0);
+
+  const float alpha = p.d.alpha, am1 = alpha - 1.0f;
+  const float a = 1.0f / am1, ew = (2.0f - alpha) / am1;
+  const float cu = am1 * p.d.scale;  // ClippedU's c
+  const size_t rbase = size_t(bh) * NQ;
+  const T* Qb = static_cast<const T*>(p.q) + rbase * D;
+  const T* dOb = static_cast<const T*>(p.dout) + rbase * D;
+  const RowRec* rec = p.rowrec + rbase;
+  const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
+  const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
+  const int32_t* kp = p.k_ptr + size_t(bh) * (nKB + 1);
+  const int32_t* kl = p.k_list + size_t(bh) * nKB * nQB;
+  const uint16_t* hmask = p.sup.mask + size_t(bh) * nQB * nKB * 256;
+
+  float kv[E], vv[E];
+  if (jok) {
+    C::load(static_cast<const T*>(p.k) + krow * D + sub * E, kv);
+    C::load(static_cast<const T*>(p.v) + krow * D + sub * E, vv);
+  } else {
+    for (int x = 0; x < E; ++x) kv[x] = vv[x] = 0.0f;
+  }
+  float dk[E], dv[E];
+  for (int x = 0; x < E; ++x) dk[x] = dv[x] = 0.0f;
+
+  const int* mylist = s_list[w][grp];
+  // phase B: this group's listed rows, kBatch at a time in every group
+  auto drain = [&]() {
+    const int cnt = s_cnt[w][grp];
+    const int nmax = groups_max<LPR>(cnt);
+    for (int q = 0; q < nmax; q += kBatch) {
+      int r[kBatch];
+      bool val[kBatch];
+      uint4 qraw[kBatch], graw[kBatch];
+      RowRec rc[kBatch];
+      for (int u = 0; u < kBatch; ++u) {
+        val[u] = q + u < cnt;
+        r[u] = val[u] ? mylist[q + u] : 0;
+      }
+      for (int u = 0; u < kBatch; ++u) {
+        qraw[u] = C::raw(Qb + size_t(r[u]) * D + sub * E);
+        graw[u] = C::raw(dOb + size_t(r[u]) * D + sub * E);
+        rc[u] = rec[r[u]];
+      }
+      for (int u = 0; u < kBatch; ++u) {
+        float qr[E], gr[E];
+        C::unpack(qraw[u], qr);
+        C::unpack(graw[u], gr);
+        const float s = group_lanes_sum<LPR>(dot<E>(qr, kv));
+        const float dp = group_lanes_sum<LPR>(dot<E>(gr, vv));
+        if (val[u]) {
+          const float v = __builtin_amdgcn_fmed3f(fmaf(cu, s, rc[u].nt), rc[u].lo, rc[u].hi);
+          const float pn = pow_clipped<PP>(v, a) * rc[u].invn;
+          float wv = pow_clipped<PW>(v, ew);
+          if constexpr (REF) wv = v > kEps ? wv : 0.0f;  // the reference's u > EPS
+          float ds = wv * fmaf(rc[u].c, dp, rc[u].cs);
+          ds = finite(ds) ? ds : 0.0f;
+          for (int x = 0; x < E; ++x) {
+            dk[x] = fmaf(ds, qr[x], dk[x]);
+            dv[x] = fmaf(pn, gr[x], dv[x]);
+          }
+        }
+      }
+    }
+  };
+
+  // phase A over the key block's query tiles (ascending query blocks),
+  // kTileGroup tiles at a time with their loads in flight together:
+  // lane L <-> row L of a tile
+  constexpr int kTileGroup = 8;
+  if (lane < KPW) s_cnt[w][lane] = 0;
+  const int32_t* pm = p.posmap + size_t(bh) * nQB * nKB + kb;  // tile (qb, kb) at + qb * nKB
+  const int x0 = kp[kb], x1 = kp[kb + 1];
+  for (int c0 = x0; c0 < x1; c0 += kTileGroup) {
+    const int nt = min(kTileGroup, x1 - c0);
+    const int my_qb = lane < nt ? kl[c0 + lane] : 0;
+    const int my_e = lane < nt ? pm[size_t(my_qb) * nKB] : 0;
+    uint64_t word[kTileGroup];
+    for (int u = 0; u < kTileGroup; ++u) {
+      const int e = __shfl(my_e, u, kWave);
+      word[u] = u < nt ? *reinterpret_cast<const uint64_t*>(hmask + size_t(e) * 256 +
+                                                             (lane >> 4) * 64 + 4 * (lane & 15))
+                       : 0ull;
+    }
+    for (int u = 0; u < kTileGroup; ++u) {
+      if (u >= nt) break;
+      // room for a whole tile in every list of the wave, else drain first
+      bool room = true;
+      for (int k = 0; k < KPW; ++k) room = room && s_cnt[w][k] + kWave <= kKeyList;
+      if (!room) {
+        drain();
+        if (lane < KPW) s_cnt[w][lane] = 0;
+      }
+      // row L's four masks: bit 16 g + 4 f + r <-> key 16 f + 4 g + r
+      const int row = __shfl(my_qb, u, kWave) * kBlock + lane;
+      for (int k = 0; k < KPW; ++k) {
+        const int key = jb + k;
+        const int bit = 16 * ((key >> 2) & 3) + 4 * (key >> 4) + (key & 3);
+        const bool on = ((word[u] >> bit) & 1u) != 0;
+        const uint64_t col = __ballot(on);
+        if (col == 0) continue;
+        const int cl = s_cnt[w][k];
+        if (on) s_list[w][k][cl + lane_rank(col)] = row;
+        if (lane == 0) s_cnt[w][k] = cl + __builtin_popcountll(col);
+      }
+    }
+  }
+  drain();
+
+  if (jok) {
+    for (int x = 0; x < E; ++x) {
+      const float vk = p.d.scale * dk[x];
+      dk[x] = finite(vk) ? vk : 0.0f;
+      dv[x] = finite(dv[x]) ? dv[x] : 0.0f;
+    }
+    C::store(static_cast<T*>(p.dk) + krow * D + sub * E, dk);
+    C::store(static_cast<T*>(p.dv) + krow * D + sub * E, dv);
+  }
+}
+
+template <typename T, int D, bool REF, bool DKDV>
+hipError_t launch_sparse_m(const BackwardParams& p, hipStream_t s) {
+  const dim3 grid(DKDV ? p.d.nKB * (kBlock / keys_per_block<T, D>()) * p.d.BH : p.d.nQB * p.d.BH);
+  auto go = [&](auto ac) {
+    constexpr int AC = decltype(ac)::value;
+    if constexpr (DKDV)
+      hipLaunchKernelGGL((dkdv_sparse_kernel<T, D, AC, REF>), grid, dim3(kThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((dq_sparse_kernel<T, D, AC, REF>), grid, dim3(kThreads), 0, s, p);
+  };
+  switch (alpha_class_of(p.d.alpha)) {
+    case kA15: go(std::integral_constant<int, kA15>{}); break;
+    case kA20: go(std::integral_constant<int, kA20>{}); break;
+    case kA125: go(std::integral_constant<int, kA125>{}); break;
+    default: go(std::integral_constant<int, kAGen>{}); break;
+  }
+  return hipGetLastError();
+}
+template <bool DKDV>
+hipError_t launch_sparse(const BackwardParams& p, bool bf16, hipStream_t s) {
+  const bool ref = p.mode == 1;
+  if (bf16) {
+    if (p.d.D == 64)
+      return ref ? launch_sparse_m<u16, 64, true, DKDV>(p, s) : launch_sparse_m<u16, 64, false, DKDV>(p, s);
+    if (p.d.D == 128)
+      return ref ? launch_sparse_m<u16, 128, true, DKDV>(p, s) : launch_sparse_m<u16, 128, false, DKDV>(p, s);
+  } else {
+    if (p.d.D == 64)
+      return ref ? launch_sparse_m<float, 64, true, DKDV>(p, s) : launch_sparse_m<float, 64, false, DKDV>(p, s);
+    if (p.d.D == 128)
+      return ref ? launch_sparse_m<float, 128, true, DKDV>(p, s) : launch_sparse_m<float, 128, false, DKDV>(p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_bwd_dq_sparse(const BackwardParams& p, bool bf16, hipStream_t s) {
+  return launch_sparse<false>(p, bf16, s);
+}
+hipError_t launch_bwd_dkdv_sparse(const BackwardParams& p, bool bf16, hipStream_t s) {
+  const int waves = p.d.nQB * p.d.BH, per = kThreads / kWave;
+  hipLaunchKernelGGL(posmap_kernel, dim3((waves + per - 1) / per), dim3(kThreads), 0, s, p);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  return launch_sparse<true>(p, bf16, s);
+}
+
+}  // namespace asa

@@ -65,17 +65,14 @@ class State(ctypes.Structure):
         ("k_list", ctypes.c_void_p),
         ("topk_idx", ctypes.c_void_p),
         ("topk_val", ctypes.c_void_p),
-        ("sup_key", ctypes.c_void_p),
-        ("sup_val", ctypes.c_void_p),
-        ("sup_off", ctypes.c_void_p),
-        ("sup_cnt", ctypes.c_void_p),
+        ("sup_mask", ctypes.c_void_p),
     ]
 
 
 class Sizes(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in (
         "taus", "norms", "mask", "q_ptr", "q_list", "k_ptr", "k_list", "topk_idx", "topk_val",
-        "sup_key", "sup_val", "sup_off", "sup_cnt", "workspace")]
+        "sup_mask", "workspace")]
 
 
 class ASAError(RuntimeError):

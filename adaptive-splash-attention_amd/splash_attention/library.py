@@ -8,7 +8,7 @@ shape-only fake implementations and an autograd formula, so that
 graph break and without looking inside the kernels.
 
 The forward returns the attention output and the selection state (tau, row
-sums, block mask, both CSR lists, the rows' support lists); the autograd
+sums, block mask, both CSR lists, the rows' support masks); the autograd
 formula saves that state for the backward, as the eager autograd function
 does.
 """
@@ -32,11 +32,9 @@ def _nblocks(n: int, b: int) -> int:
 @torch.library.custom_op(f"{_NS}::forward", mutates_args=(), device_types="cuda")
 def forward_op(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx: Optional[Tensor],
                alpha: float, k_keep: int, sm_scale: float, grad_mode: str
-               ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
-                          Tensor, Tensor, Tensor]:
+               ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """out, taus, norms, mask, q_ptr, q_list, k_ptr, k_list and the support
-    lists sup_key, sup_val, sup_off, sup_cnt (grad_mode is recorded for the
-    backward only)."""
+    masks sup_mask (grad_mode is recorded for the backward only)."""
     q, k, v, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     out, st = ops.splash_forward(q, k, v, qi, ki, alpha, k_keep, sm_scale, with_support=True)
     return (out, *st.tensors())
@@ -50,32 +48,29 @@ def _forward_fake(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode):
     nQB, nKB = _nblocks(NQ, ops.BLOCK_M), _nblocks(NK, ops.BLOCK_N)
     f32 = dict(dtype=torch.float32, device=Q.device)
     i32 = dict(dtype=torch.int32, device=Q.device)
-    cap = ops.support_capacity(ops.make_problem(B, H, NQ, NK, d, Q.dtype, alpha, k_keep, sm_scale))
     return (torch.empty_like(Q, memory_format=torch.contiguous_format),
             torch.empty((BH, NQ), **f32), torch.empty((BH, NQ), **f32),
             torch.empty((BH, nQB, nKB), dtype=torch.uint8, device=Q.device),
             torch.empty((BH, nQB + 1), **i32), torch.empty((BH, nQB * nKB), **i32),
             torch.empty((BH, nKB + 1), **i32), torch.empty((BH, nKB * nQB), **i32),
-            torch.empty((BH * nQB * 4, cap), **i32), torch.empty((BH * nQB * 4, cap), **f32),
-            torch.empty((BH, nQB * nKB, 4), **i32), torch.empty((BH * nQB * 4,), **i32))
+            torch.empty((BH, nQB * nKB, 4, 64), dtype=torch.int16, device=Q.device))
 
 
 @torch.library.custom_op(f"{_NS}::backward", mutates_args=(), device_types="cuda")
 def backward_op(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx: Optional[Tensor],
                 out: Tensor, dout: Tensor, taus: Tensor, norms: Tensor, mask: Tensor,
-                q_ptr: Tensor, q_list: Tensor, k_ptr: Tensor, k_list: Tensor, sup_key: Tensor,
-                sup_val: Tensor, sup_off: Tensor, sup_cnt: Tensor, alpha: float,
+                q_ptr: Tensor, q_list: Tensor, k_ptr: Tensor, k_list: Tensor, sup_mask: Tensor,
+                alpha: float,
                 k_keep: int, sm_scale: float, grad_mode: str) -> tuple[Tensor, Tensor, Tensor]:
     """dQ, dK, dV from the state a matching forward_op returned."""
     q, k, v, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
-    st = ops.SplashState.from_tensors((taus, norms, mask, q_ptr, q_list, k_ptr, k_list, sup_key,
-                                       sup_val, sup_off, sup_cnt))
+    st = ops.SplashState.from_tensors((taus, norms, mask, q_ptr, q_list, k_ptr, k_list, sup_mask))
     return ops.splash_backward(q, k, v, qi, ki, out, dout, st, alpha, k_keep, sm_scale, grad_mode)
 
 
 @backward_op.register_fake
 def _backward_fake(Q, K, V, Q_idx, K_idx, out, dout, taus, norms, mask, q_ptr, q_list, k_ptr,
-                   k_list, sup_key, sup_val, sup_off, sup_cnt, alpha, k_keep, sm_scale, grad_mode):
+                   k_list, sup_mask, alpha, k_keep, sm_scale, grad_mode):
     c = torch.contiguous_format
     return (torch.empty_like(Q, memory_format=c), torch.empty_like(K, memory_format=c),
             torch.empty_like(V, memory_format=c))

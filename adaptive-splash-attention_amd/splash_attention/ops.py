@@ -37,27 +37,24 @@ class SplashState:
     k_list: torch.Tensor     # [BH, nKB*nQB] int32
     topk_idx: torch.Tensor | None = None  # [BH, NQ, k] int32
     topk_val: torch.Tensor | None = None  # [BH, NQ, k] float32
-    # support lists (asa_state.sup_*): the (row, key) pairs with u > 0
-    sup_key: torch.Tensor | None = None   # [BH*nQB*4, cap] int32 (uint32 bits)
-    sup_val: torch.Tensor | None = None   # [BH*nQB*4, cap] float32
-    sup_off: torch.Tensor | None = None   # [BH, nQB*nKB, 4] int32
-    sup_cnt: torch.Tensor | None = None   # [BH*nQB*4] int32
+    # support masks (asa_state.sup_mask): the (row, key) pairs with u > 0,
+    # 16 bits per (tile, 16-row wave, lane) as uint16 bit patterns
+    sup_mask: torch.Tensor | None = None  # [BH, nQB*nKB, 4, 64] int16
 
-    SUPPORT = ("sup_key", "sup_val", "sup_off", "sup_cnt")
+    SUPPORT = ("sup_mask",)
 
     def c_struct(self) -> _lib.State:
         def ptr(t):
             return None if t is None else t.data_ptr()
         return _lib.State(ptr(self.taus), ptr(self.norms), ptr(self.mask), ptr(self.q_ptr),
                           ptr(self.q_list), ptr(self.k_ptr), ptr(self.k_list),
-                          ptr(self.topk_idx), ptr(self.topk_val), ptr(self.sup_key),
-                          ptr(self.sup_val), ptr(self.sup_off), ptr(self.sup_cnt))
+                          ptr(self.topk_idx), ptr(self.topk_val), ptr(self.sup_mask))
 
     def tensors(self) -> tuple:
         """The tensors a backward needs (support lists included when present)."""
         base = (self.taus, self.norms, self.mask, self.q_ptr, self.q_list, self.k_ptr,
                 self.k_list)
-        if self.sup_key is None:
+        if self.sup_mask is None:
             return base
         return base + tuple(getattr(self, n) for n in self.SUPPORT)
 
@@ -182,18 +179,8 @@ def alloc_state(p: _lib.Problem, device, with_topk: bool = False,
         st.topk_idx = torch.empty((BH, p.nq, p.k_keep), **i32)
         st.topk_val = torch.empty((BH, p.nq, p.k_keep), **f32)
     if with_support:
-        cap = support_capacity(p)
-        st.sup_key = torch.empty((BH * nQB * 4, cap), **i32)
-        st.sup_val = torch.empty((BH * nQB * 4, cap), **f32)
-        st.sup_off = torch.empty((BH, nQB * nKB, 4), **i32)
-        st.sup_cnt = torch.empty((BH * nQB * 4,), **i32)
+        st.sup_mask = torch.empty((BH, nQB * nKB, 4, 64), device=device, dtype=torch.int16)
     return st
-
-
-def support_capacity(p: _lib.Problem) -> int:
-    """Support-list entries per 16-row wave region (asa_state.sup_key)."""
-    nQB = -(-p.nq // BLOCK_M)
-    return _lib.query_sizes(p).sup_key // (4 * p.batch * p.heads * nQB * 4)
 
 
 def workspace(p: _lib.Problem, device) -> torch.Tensor:
@@ -205,8 +192,8 @@ def workspace(p: _lib.Problem, device) -> torch.Tensor:
 def splash_forward(Q, K, V, Q_idx, K_idx, alpha: float, k_keep: int, sm_scale=None,
                    with_topk: bool = False, with_support: bool = True):
     """Forward pass; returns (out, SplashState).  Inputs as check_inputs() returns them.
-    with_support records the rows' support lists for a sparse backward (skip
-    it for inference)."""
+    with_support records the rows' support masks for the sparse backward
+    (skip it for inference)."""
     lib = _lib.load()
     B, H, NQ, d = Q.shape
     p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale)

@@ -100,21 +100,19 @@ typedef struct asa_problem {
  *                                   best first, -1 in empty slots
  *   topk_val float   [BH, nq, k_keep] optional (NULL): matching scores,
  *                                   -1e6 in empty slots
- * Support lists, optional (all four NULL, or all set).  When set, the
- * forward records every (row, key) pair it weights with u = (alpha-1) s -
- * tau > 0 -- the rows' exact supports, on which every backward term lives
- * -- and the backward then visits only those pairs.  Each 16-row quarter
- * of a query block ("wave region", index wr = (bh * nQB + qb) * 4 + w,
- * rows qb*64 + 16w ..) owns cap = 16 * max(64, 2 * k_keep) entries:
- *   sup_key  uint32  [BH*nQB*4, cap] key index | (row - qb*64 - 16w) << 28
- *   sup_val  float   [BH*nQB*4, cap] max(u, 0) of that pair
- *   sup_off  int32   [BH, nQB*nKB, 4] entries of region w before the tile
- *                                   at the head's q_list position e
- *   sup_cnt  int32   [BH*nQB*4]     entries of each region; a count above
- *                                   cap means the list overflowed, and the
- *                                   backward computes that query block
- *                                   densely instead.
- * Without them the backward computes every active block densely.          */
+ * Support masks, optional (NULL: not written, and the backward computes
+ * every active block densely):
+ *   sup_mask uint16  [BH, nQB*nKB, 4, 64]  for the tile at the head's q_list
+ *                                   position e (query block qb, key block
+ *                                   kb), bit 4f + r of element [e][w][4c + g]
+ *                                   is set iff the forward weighted row
+ *                                   qb*64 + 16w + c, key kb*64 + 16f + 4g + r
+ *                                   with u = (alpha-1) s - tau > 0
+ *                                   (w, c < 16; g, f, r < 4).  These are
+ *                                   the rows' exact supports, on which
+ *                                   every backward term lives: with them
+ *                                   the backward visits only those pairs.
+ */
 typedef struct asa_state {
   float *taus;
   float *norms;
@@ -125,17 +123,14 @@ typedef struct asa_state {
   int32_t *k_list;
   int32_t *topk_idx;
   float *topk_val;
-  uint32_t *sup_key;
-  float *sup_val;
-  int32_t *sup_off;
-  int32_t *sup_cnt;
+  uint16_t *sup_mask;
 } asa_state;
 
 /* Byte sizes of every state buffer and of the workspace the entry points
  * need for this problem.                                                   */
 typedef struct asa_sizes {
   size_t taus, norms, mask, q_ptr, q_list, k_ptr, k_list, topk_idx, topk_val;
-  size_t sup_key, sup_val, sup_off, sup_cnt;
+  size_t sup_mask;
   size_t workspace;
 } asa_sizes;
 
