@@ -39,7 +39,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kRowList = 64;   // keys listed per row before a dQ phase B
 constexpr int kKeyList = 128;  // rows listed per key before a dK/dV phase B
-constexpr int kBatch = 4;      // entries whose gathers are in flight together
+constexpr int kBatch = 2;      // entries whose gathers are in flight together
 constexpr int kChunk = 16;     // tiles whose masks are fetched together
 
 // 16 bytes of a row: raw (as loaded) and as floats.
@@ -55,6 +55,15 @@ template <> struct Chunk<u16> {
     }
   }
   static __device__ __forceinline__ void load(const u16* p, float (&x)[8]) { unpack(raw(p), x); }
+  // sum_i a_i b_i of two raw chunks: products exact, fp32 sums (v_dot2_f32_bf16)
+  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b) {
+    float s = 0.0f;
+    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.x), __builtin_bit_cast(bf16x2, b.x), s, false);
+    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.y), __builtin_bit_cast(bf16x2, b.y), s, false);
+    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.z), __builtin_bit_cast(bf16x2, b.z), s, false);
+    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.w), __builtin_bit_cast(bf16x2, b.w), s, false);
+    return s;
+  }
   static __device__ __forceinline__ void store(u16* p, const float (&x)[8]) {
     uint32_t w[4];
     for (int i = 0; i < 4; ++i)
@@ -72,6 +81,12 @@ template <> struct Chunk<float> {
     x[3] = __uint_as_float(v.w);
   }
   static __device__ __forceinline__ void load(const float* p, float (&x)[4]) { unpack(raw(p), x); }
+  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b) {
+    float s = __uint_as_float(a.x) * __uint_as_float(b.x);
+    s = fmaf(__uint_as_float(a.y), __uint_as_float(b.y), s);
+    s = fmaf(__uint_as_float(a.z), __uint_as_float(b.z), s);
+    return fmaf(__uint_as_float(a.w), __uint_as_float(b.w), s);
+  }
   static __device__ __forceinline__ void store(float* p, const float (&x)[4]) {
     *reinterpret_cast<float4*>(p) = float4{x[0], x[1], x[2], x[3]};
   }
@@ -92,13 +107,6 @@ __device__ __forceinline__ float group_lanes_sum(float v) {
   if constexpr (G >= 16) v += x(v, std::integral_constant<int, 8>{});
   if constexpr (G >= 32) v += x(v, std::integral_constant<int, 16>{});
   return v;
-}
-
-template <int E>
-__device__ __forceinline__ float dot(const float (&a)[E], const float (&b)[E]) {
-  float s = 0.0f;
-  for (int e = 0; e < E; ++e) s = fmaf(a[e], b[e], s);
-  return s;
 }
 
 // Maximum of a lane-group-uniform value over the wave's groups of G lanes.
@@ -129,7 +137,7 @@ __global__ __launch_bounds__(kThreads) void posmap_kernel(BackwardParams p) {
 // dQ
 // ---------------------------------------------------------------------------
 template <typename T, int D, int AC, bool REF>
-__global__ __launch_bounds__(kThreads, 3) void dq_sparse_kernel(BackwardParams p) {
+__global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p) {
   using C = Chunk<T>;
   constexpr int E = C::E;
   constexpr int LPR = D / E;          // lanes per row (16 bytes each)
@@ -166,12 +174,10 @@ __global__ __launch_bounds__(kThreads, 3) void dq_sparse_kernel(BackwardParams p
     const int qrow = qb * kBlock + 16 * w + rr;
     const bool ok = qrow < NQ;
     const size_t row = size_t(bh) * NQ + (ok ? qrow : 0);
-    float qv[E], dO[E];
+    uint4 qv{0u, 0u, 0u, 0u}, dO{0u, 0u, 0u, 0u};  // raw 16-byte chunks
     if (ok) {
-      C::load(static_cast<const T*>(p.q) + row * D + sub * E, qv);
-      C::load(static_cast<const T*>(p.dout) + row * D + sub * E, dO);
-    } else {
-      for (int x = 0; x < E; ++x) qv[x] = dO[x] = 0.0f;
+      qv = C::raw(static_cast<const T*>(p.q) + row * D + sub * E);
+      dO = C::raw(static_cast<const T*>(p.dout) + row * D + sub * E);
     }
     const ClippedU clip(am1, scale, ok ? p.taus[row] : 0.0f, ok);
 
@@ -195,12 +201,11 @@ __global__ __launch_bounds__(kThreads, 3) void dq_sparse_kernel(BackwardParams p
           vraw[u] = C::raw(Vb + size_t(key[u]) * D + sub * E);
         }
         for (int u = 0; u < kBatch; ++u) {
-          float kr[E], vr[E];
-          C::unpack(kraw[u], kr);
-          C::unpack(vraw[u], vr);
-          const float s = group_lanes_sum<LPR>(dot<E>(qv, kr));
-          const float dp = group_lanes_sum<LPR>(dot<E>(dO, vr));
+          const float s = group_lanes_sum<LPR>(C::dot(qv, kraw[u]));
+          const float dp = group_lanes_sum<LPR>(C::dot(dO, vraw[u]));
           if (val[u]) {
+            float kr[E];
+            C::unpack(kraw[u], kr);
             const float wv = weight(clip(s));
             sw += wv;
             const float wdp = wv * dp;
@@ -284,7 +289,7 @@ __global__ __launch_bounds__(kThreads, 3) void dq_sparse_kernel(BackwardParams p
 template <typename T, int D> constexpr int keys_per_block() { return 4 * (kWave / (D / Chunk<T>::E)); }
 
 template <typename T, int D, int AC, bool REF>
-__global__ __launch_bounds__(kThreads, 3) void dkdv_sparse_kernel(BackwardParams p) {
+__global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams p) {
   using C = Chunk<T>;
   constexpr int E = C::E;
   constexpr int LPR = D / E;          // lanes per key (16 bytes each)
@@ -317,12 +322,10 @@ __global__ __launch_bounds__(kThreads, 3) void dkdv_sparse_kernel(BackwardParams
   const int32_t* kl = p.k_list + size_t(bh) * nKB * nQB;
   const uint16_t* hmask = p.sup.mask + size_t(bh) * nQB * nKB * 256;
 
-  float kv[E], vv[E];
+  uint4 kv{0u, 0u, 0u, 0u}, vv{0u, 0u, 0u, 0u};  // raw 16-byte chunks of the key's rows
   if (jok) {
-    C::load(static_cast<const T*>(p.k) + krow * D + sub * E, kv);
-    C::load(static_cast<const T*>(p.v) + krow * D + sub * E, vv);
-  } else {
-    for (int x = 0; x < E; ++x) kv[x] = vv[x] = 0.0f;
+    kv = C::raw(static_cast<const T*>(p.k) + krow * D + sub * E);
+    vv = C::raw(static_cast<const T*>(p.v) + krow * D + sub * E);
   }
   float dk[E], dv[E];
   for (int x = 0; x < E; ++x) dk[x] = dv[x] = 0.0f;
@@ -347,12 +350,12 @@ __global__ __launch_bounds__(kThreads, 3) void dkdv_sparse_kernel(BackwardParams
         rc[u] = rec[r[u]];
       }
       for (int u = 0; u < kBatch; ++u) {
-        float qr[E], gr[E];
-        C::unpack(qraw[u], qr);
-        C::unpack(graw[u], gr);
-        const float s = group_lanes_sum<LPR>(dot<E>(qr, kv));
-        const float dp = group_lanes_sum<LPR>(dot<E>(gr, vv));
+        const float s = group_lanes_sum<LPR>(C::dot(qraw[u], kv));
+        const float dp = group_lanes_sum<LPR>(C::dot(graw[u], vv));
         if (val[u]) {
+          float qr[E], gr[E];
+          C::unpack(qraw[u], qr);
+          C::unpack(graw[u], gr);
           const float v = __builtin_amdgcn_fmed3f(fmaf(cu, s, rc[u].nt), rc[u].lo, rc[u].hi);
           const float pn = pow_clipped<PP>(v, a) * rc[u].invn;
           float wv = pow_clipped<PW>(v, ew);
@@ -370,9 +373,17 @@ __global__ __launch_bounds__(kThreads, 3) void dkdv_sparse_kernel(BackwardParams
 
   // phase A over the key block's query tiles (ascending query blocks),
   // kTileGroup tiles at a time with their loads in flight together:
-  // lane L <-> row L of a tile
+  // lane L <-> row L of a tile.  The list lengths are wave-uniform
+  // (scalar registers); drain() reads them from s_cnt.
   constexpr int kTileGroup = 8;
-  if (lane < KPW) s_cnt[w][lane] = 0;
+  int cnt[KPW];
+  for (int k = 0; k < KPW; ++k) cnt[k] = 0;
+  auto drain_lists = [&]() {
+    for (int k = 0; k < KPW; ++k)
+      if (lane == k) s_cnt[w][k] = cnt[k];
+    drain();
+    for (int k = 0; k < KPW; ++k) cnt[k] = 0;
+  };
   const int32_t* pm = p.posmap + size_t(bh) * nQB * nKB + kb;  // tile (qb, kb) at + qb * nKB
   const int x0 = kp[kb], x1 = kp[kb + 1];
   for (int c0 = x0; c0 < x1; c0 += kTileGroup) {
@@ -390,11 +401,8 @@ __global__ __launch_bounds__(kThreads, 3) void dkdv_sparse_kernel(BackwardParams
       if (u >= nt) break;
       // room for a whole tile in every list of the wave, else drain first
       bool room = true;
-      for (int k = 0; k < KPW; ++k) room = room && s_cnt[w][k] + kWave <= kKeyList;
-      if (!room) {
-        drain();
-        if (lane < KPW) s_cnt[w][lane] = 0;
-      }
+      for (int k = 0; k < KPW; ++k) room = room && cnt[k] + kWave <= kKeyList;
+      if (!room) drain_lists();
       // row L's four masks: bit 16 g + 4 f + r <-> key 16 f + 4 g + r
       const int row = __shfl(my_qb, u, kWave) * kBlock + lane;
       for (int k = 0; k < KPW; ++k) {
@@ -402,14 +410,12 @@ __global__ __launch_bounds__(kThreads, 3) void dkdv_sparse_kernel(BackwardParams
         const int bit = 16 * ((key >> 2) & 3) + 4 * (key >> 4) + (key & 3);
         const bool on = ((word[u] >> bit) & 1u) != 0;
         const uint64_t col = __ballot(on);
-        if (col == 0) continue;
-        const int cl = s_cnt[w][k];
-        if (on) s_list[w][k][cl + lane_rank(col)] = row;
-        if (lane == 0) s_cnt[w][k] = cl + __builtin_popcountll(col);
+        if (on) s_list[w][k][cnt[k] + lane_rank(col)] = row;
+        cnt[k] += __builtin_popcountll(col);
       }
     }
   }
-  drain();
+  drain_lists();
 
   if (jok) {
     for (int x = 0; x < E; ++x) {
