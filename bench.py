@@ -5,9 +5,9 @@ Workload: B=4, H=16, N=4096, d=64, bf16,
 alpha=1.5, k_keep=32, sm_scale=0.125, causal (Q_idx = K_idx = arange),
 64x64 blocks, Q/K/V and the upstream gradient ~ N(0,1) (synthetic, seeded).
 
-One step = forward (score pass, CSR compaction, block-sparse forward) plus
-backward (dQ, dK/dV, entmax-Jacobian gradient) through the autograd API,
-inputs resident in HBM.  value = effective TFLOP/s with the FlashAttention
+One step = forward (score pass, CSR compaction, block-sparse forward with
+the rows' support masks) plus backward (dQ, dK/dV over the support pairs,
+entmax-Jacobian gradient) through the autograd API, inputs resident in HBM.  value = effective TFLOP/s with the FlashAttention
 convention for dense causal fwd+bwd, 3.5 * 4 * BH * d * N^2 / 2 = 481.0 GFLOP
 per step.
 
@@ -42,16 +42,32 @@ ELEM = 2                 # bf16 bytes
 COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # HBM bytes per launch of each kernel at this workload, measured with
 # rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), the factors a plain
-# 256 MiB device copy gives (profiles/headline_hbm_traffic.md).
-HBM_TRAFFIC = {'bounds': 1107968, 'select': 104310512, 'tau': 34701568, 'compact': 2464256, 'forward': 139069984, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
+# 256 MiB device copy gives (profiles/headline_hbm_traffic.md).  The
+# bwd_dkdv_sparse launch includes its position-map kernel; bwd_dq and
+# bwd_dkdv are the dense passes (run when no support masks were recorded).
+HBM_TRAFFIC = {'bounds': 1107968, 'select': 102500352, 'tau': 34701568, 'compact': 2464256, 'forward': 207681536, 'bwd_dq_sparse': 522891264, 'bwd_dkdv_sparse': 284372992, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
 
 
 def effective_flops(B, H, N, d):
     return 3.5 * 4 * B * H * d * N * N / 2
 
 
-def kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep):
-    """Algorithmic FLOPs and HBM bytes per launch of every kernel."""
+def support_pairs(st) -> int:
+    """(row, key) pairs with u > 0 recorded in the state's support masks
+    (active tile slots only: slot e < q_ptr[bh, nQB])."""
+    import torch
+    lut = torch.tensor([bin(i).count("1") for i in range(256)], dtype=torch.int32,
+                       device=st.sup_mask.device)
+    total = 0
+    for bh in range(st.sup_mask.shape[0]):
+        n = int(st.q_ptr[bh, -1])
+        total += int(lut[st.sup_mask[bh, :n].contiguous().view(torch.uint8).long()].sum())
+    return total
+
+
+def kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep, nsup):
+    """Algorithmic FLOPs and HBM bytes per launch of every kernel (nsup: the
+    support pairs the sparse backward visits)."""
     BH = B * H
     rows = BH * N
     vis = BH * N * (N + 1) // 2          # visible (query, key) pairs, causal
@@ -72,6 +88,15 @@ def kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep):
                        bytes=nnzb * 2 * tile + 3 * rows * d * ELEM + 4 * rows * 4),
         "bwd_dkdv": dict(bound="hbm", flops=8.0 * 64 * 64 * d * nnzb,
                          bytes=nnzb * 2 * tile + 4 * rows * d * ELEM + nnzb * 64 * 4 * 5),
+        # support-mask backward: per listed pair, two gathered d-rows and
+        # 8 d FLOPs (two dot products, two accumulations); per active tile
+        # its 512 bytes of masks
+        "bwd_dq_sparse": dict(bound="hbm", flops=8.0 * d * nsup,
+                              bytes=nsup * 2 * d * ELEM + 3 * rows * d * ELEM + nnzb * 512
+                              + rows * (8 + 32)),
+        "bwd_dkdv_sparse": dict(bound="hbm", flops=8.0 * d * nsup,
+                                bytes=nsup * (2 * d * ELEM + 32) + 4 * rows * d * ELEM
+                                + nnzb * 512 + 4 * BH * nQB * nKB),
     }
 
 
@@ -222,8 +247,9 @@ def main():
     # Block-mask density of this workload (same for every step: same inputs).
     _, st = sa.ops.splash_forward(*sa.ops.check_inputs(Q, K, V, idx, idx), alpha, k_keep, scale)
     nnzb = int(st.mask.sum().item())
+    nsup = support_pairs(st)
     nQB = nKB = N // 64
-    models = kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep)
+    models = kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep, nsup)
     kernels = {}
     for name, (cnt, tot) in kern.items():
         if name in models:
@@ -254,6 +280,7 @@ def main():
                    "sm_scale": scale, "mask": "causal", "block": "64x64",
                    "grad_mode": args.grad_mode, "parallelism": "single GPU",
                    "active_block_pairs": nnzb,
+                   "support_pairs": nsup,
                    "active_block_density_of_causal": round(nnzb / (B * H * nQB * (nQB + 1) / 2), 4)},
         "roofline": roof,
         "kernels": kernels,
