@@ -61,28 +61,28 @@ __device__ __forceinline__ float group_max(float v) {
     return __float_as_uint(fmaxf(__uint_as_float(x), __uint_as_float(y)));
   }));
 }
-// v_max_f32 without the operand canonicalisation that fmaxf() carries (the
-// inputs are MFMA results or -inf, never signalling NaNs); NaN loses.
-__device__ __forceinline__ float vmax(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
+// max(m, x) for a running maximum m (never NaN) and an MFMA result x, in
+// one v_med3_f32: med3(x, m, +inf) is the larger of x and m, and m when x
+// is NaN (NaN loses).  `pinf` is +inf held in a register the compiler
+// cannot see into (with a constant +inf it rewrites the med3 as fmaxf(),
+// which canonicalises both operands first).  The MFMA results are only
+// ever read by compiler-visible instructions, never by inline asm, so the
+// compiler keeps the MFMA-to-VALU wait states it owes those reads.
+__device__ __forceinline__ float vmax(float m, float x, float pinf) {
+  return __builtin_amdgcn_fmed3f(x, m, pinf);
 }
-// m = 2 m + (x >= t || isnan(x)): one compare and one add-with-carry.
+__device__ __forceinline__ float opaque_inf() {
+  float v = __builtin_inff();
+  asm("" : "+v"(v));
+  return v;
+}
+// m = 2 m + (x >= t || isnan(x)).
 __device__ __forceinline__ uint32_t shift_in_nlt(uint32_t m, float x, float t) {
-  asm("v_cmp_nlt_f32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
-      : "+v"(m)
-      : "v"(x), "v"(t)
-      : "vcc");
-  return m;
+  return m + m + (x < t ? 0u : 1u);
 }
-// c + (x >= t): counts with the same two instructions.
+// c + (x >= t).
 __device__ __forceinline__ uint32_t count_ge(uint32_t c, float x, float t) {
-  asm("v_cmp_ge_f32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, 0, %0, vcc"
-      : "+v"(c)
-      : "v"(x), "v"(t)
-      : "vcc");
-  return c;
+  return c + (x >= t ? 1u : 0u);
 }
 template <int I, int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -447,12 +447,13 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
 
   // ---------------- sweep 1: class maxima ----------------
   float cm[16][R];
+  const float pinf = opaque_inf();
   for (int i = 0; i < 16; ++i)
     for (int j = 0; j < R; ++j) cm[i][j] = -__builtin_inff();
   sweep(std::integral_constant<int, R>{}, [&](auto uc, int, uint32_t, f32x4 (&acc)[4]) {
     constexpr int u = decltype(uc)::value;
     for (int f = 0; f < 4; ++f)
-      for (int r = 0; r < 4; ++r) cm[4 * f + r][u] = vmax(cm[4 * f + r][u], acc[f][r]);
+      for (int r = 0; r < 4; ++r) cm[4 * f + r][u] = vmax(cm[4 * f + r][u], acc[f][r], pinf);
   });
 
   // Per row: a value x with at least k class maxima >= x (bisection between

@@ -30,6 +30,9 @@ FLAGS = [
     "-Wall",
     # The packed-fp32 VALU forms are kept out of the generated code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results go to ordinary VGPRs (gfx950's unified register file)
+    # instead of AGPRs that every VALU consumer would first copy out of.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 
