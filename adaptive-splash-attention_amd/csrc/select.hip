@@ -144,6 +144,8 @@ template <int AC, int KMAX, typename S>
 __device__ float entmax_tau(S s, int k, float alpha_in) {
 #pragma clang fp contract(off)
   constexpr int PA = AlphaPow<AC>::P, P1 = AlphaPow<AC>::W, P2 = AlphaPow<AC>::V;
+  // register-resident values and closed-form powers: evaluate every slot
+  constexpr bool kFlat = KMAX > 0 && AC != kAGen;
   const float alpha = fmaxf(1.05f, fminf(alpha_in, 3.0f));
   const float am1 = alpha - 1.0f;
   const float a = 1.0f / am1;
@@ -172,7 +174,25 @@ __device__ float entmax_tau(S s, int k, float alpha_in) {
       if (finite(t2)) d2f = d2f + t2;
       return true;
     };
-    if constexpr (KMAX > 0) {
+    if constexpr (kFlat) {
+      // Branch-free over all KMAX slots: the values are sorted, so u is
+      // non-increasing in j and the terms the recurrence stops before are
+      // exactly the ones with u <= 0 (or j >= k).  Those add +0.0f, which
+      // leaves every sum unchanged (none of them can be -0.0f), so the
+      // result is bit-identical to the early-exit loop.
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) {
+        const float u = am1 * s(j) - tau;
+        const bool on = j < k && !(u <= 0.0f);
+        const float ue = fmaxf(u, kEps);
+        const float t = pow_exact_c<PA>(ue, a);
+        f = f + (on && finite(t) ? t : 0.0f);
+        const float t1 = -a * pow_exact_c<P1>(ue, e1);
+        df = df + (on && finite(t1) ? t1 : 0.0f);
+        const float t2 = c2 * pow_exact_c<P2>(ue, e2);
+        d2f = d2f + (on && finite(t2) ? t2 : 0.0f);
+      }
+    } else if constexpr (KMAX > 0) {
 #pragma unroll
       for (int j = 0; j < KMAX; ++j)
         if (!term(j)) break;
@@ -196,7 +216,14 @@ __device__ float entmax_tau(S s, int k, float alpha_in) {
       if (finite(t)) gsum = gsum + t;
       return true;
     };
-    if constexpr (KMAX > 0) {
+    if constexpr (kFlat) {
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) {
+        const float u = am1 * s(j) - next;
+        const float t = pow_exact_c<PA>(fmaxf(u, kEps), a);
+        gsum = gsum + (j < k && !(u <= 0.0f) && finite(t) ? t : 0.0f);
+      }
+    } else if constexpr (KMAX > 0) {
 #pragma unroll
       for (int j = 0; j < KMAX; ++j)
         if (!gterm(j)) break;
@@ -645,7 +672,7 @@ __global__ __launch_bounds__(kThreads) void tau_kernel(SelectParams p) {
   if constexpr (KMAX > 0) {
     float reg[KMAX];
 #pragma unroll
-    for (int j = 0; j < KMAX; ++j) reg[j] = j < k ? v[size_t(j) * rows] : 0.0f;
+    for (int j = 0; j < KMAX; ++j) reg[j] = v[size_t(min(j, k - 1)) * rows];  // k >= 1
     p.taus[r] = entmax_tau<AC, KMAX>([&](int j) { return reg[j]; }, k, p.d.alpha);
   } else {
     p.taus[r] = entmax_tau<AC, 0>([&](int j) { return v[size_t(j) * rows]; }, k, p.d.alpha);
