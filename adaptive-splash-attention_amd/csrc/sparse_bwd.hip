@@ -20,7 +20,14 @@
 //              lock-step batches: s = q.k_j, w, dp = dO.v_j, and the fp32
 //              sums A = sum w dp k_j, B = sum w k_j, sum w, sum w dp give
 //              dQ = scale c (A - shift B).  It also writes each row's
-//              constants for the dK/dV pass.
+//              constants for the dK/dV pass.  The lock step runs as long as
+//              the longest list among the lane groups, so when the wave's
+//              16 rows list at most kFlat keys in all, it counts them first,
+//              lists every row whole, and gives lane group g the rows of
+//              count ranks g, 15 - g, 16 + g, ... (a snake over the sorted
+//              counts): at the headline this cuts the lock-step iterations
+//              per wave from 35 to 23 (21 would be perfect balance).  Larger
+//              waves list their rows in rounds and chunks of tiles.
 //   dK/dV pass one block per slice of a key block, one lane group per key.
 //              Phase A walks the key block's query tiles (key-major CSR):
 //              the tile's masks give, by one ballot per key, the rows that
@@ -41,6 +48,7 @@ constexpr int kRowList = 64;   // keys listed per row before a dQ phase B
 constexpr int kKeyList = 128;  // rows listed per key before a dK/dV phase B
 constexpr int kBatch = 2;      // entries whose gathers are in flight together
 constexpr int kChunk = 16;     // tiles whose masks are fetched together
+constexpr int kFlat = 1024;    // keys a dQ wave lists at once on its balanced path
 
 // 16 bytes of a row: raw (as loaded) and as floats.
 template <typename T> struct Chunk;
@@ -141,11 +149,16 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
   using C = Chunk<T>;
   constexpr int E = C::E;
   constexpr int LPR = D / E;          // lanes per row (16 bytes each)
-  constexpr int RPR = kWave / LPR;    // rows per round of a wave
+  constexpr int RPR = kWave / LPR;    // rows per round of a wave (lane groups)
+  constexpr int NR = 16 / RPR;        // rows per lane group
   constexpr int PW = AlphaPow<AC>::W;
-  __shared__ int s_list[4][RPR][kRowList];
-  __shared__ uint64_t s_mw[4][kChunk][16];  // mask words of a chunk of tiles: [tile][row]
-  __shared__ int s_kb[4][kChunk];           // first key of each tile
+  __shared__ int s_flat[4][kFlat];           // balanced path: the wave's rows' lists
+  __shared__ int s_rn[4][16];                // listed keys per row of the wave
+  __shared__ int s_off[4][16];               // start of each row's list in s_flat
+  __shared__ int s_rank[4][16];              // rows in descending count order
+  __shared__ int s_list[4][RPR][kRowList];   // chunked path
+  __shared__ uint64_t s_mw[4][kChunk][16];   // mask words of a chunk of tiles: [tile][row]
+  __shared__ int s_kb[4][kChunk];            // first key of each tile
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
@@ -162,63 +175,179 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
   const int e0 = qp[qb], e1 = qp[qb + 1];
   // the wave's masks of tile e: row c's word at + e * 256 + 4 c
   const uint16_t* wmask = p.sup.mask + size_t(bh) * nQB * nKB * 256 + w * 64;
-  int* list = s_list[w][grp];
   auto weight = [&](float v) {
     float wv = pow_clipped<PW>(v, ew);
     if constexpr (REF) wv = v > kEps ? wv : 0.0f;  // the reference's u > EPS
     return wv;
   };
 
-  for (int r0 = 0; r0 < 16; r0 += RPR) {
-    const int rr = r0 + grp;  // row within the wave
+  // One row's state: its q and dO chunks, clipping, and the fp32 sums
+  // A = sum w dp k_j, B = sum w k_j, sum w, sum w dp.
+  int rr = 0;  // row within the wave
+  bool ok = false;
+  size_t row = 0;
+  uint4 qv{0u, 0u, 0u, 0u}, dO{0u, 0u, 0u, 0u};
+  ClippedU clip(am1, scale, 0.0f, false);
+  float a1[E], a2[E];
+  float sw = 0.0f, swdp = 0.0f;
+  auto start_row = [&](int r) {
+    rr = r;
     const int qrow = qb * kBlock + 16 * w + rr;
-    const bool ok = qrow < NQ;
-    const size_t row = size_t(bh) * NQ + (ok ? qrow : 0);
-    uint4 qv{0u, 0u, 0u, 0u}, dO{0u, 0u, 0u, 0u};  // raw 16-byte chunks
+    ok = qrow < NQ;
+    row = size_t(bh) * NQ + (ok ? qrow : 0);
+    qv = uint4{0u, 0u, 0u, 0u};
+    dO = uint4{0u, 0u, 0u, 0u};
     if (ok) {
       qv = C::raw(static_cast<const T*>(p.q) + row * D + sub * E);
       dO = C::raw(static_cast<const T*>(p.dout) + row * D + sub * E);
     }
-    const ClippedU clip(am1, scale, ok ? p.taus[row] : 0.0f, ok);
-
-    float a1[E], a2[E];
+    clip = ClippedU(am1, scale, ok ? p.taus[row] : 0.0f, ok);
     for (int x = 0; x < E; ++x) a1[x] = a2[x] = 0.0f;
-    float sw = 0.0f, swdp = 0.0f;
-
-    // phase B: the listed keys, kBatch at a time in every row group
-    auto drain = [&](int cnt) {
-      const int nmax = groups_max<LPR>(cnt);
-      for (int q = 0; q < nmax; q += kBatch) {
-        int key[kBatch];
-        bool val[kBatch];
-        uint4 kraw[kBatch], vraw[kBatch];
-        for (int u = 0; u < kBatch; ++u) {
-          val[u] = q + u < cnt;
-          key[u] = val[u] ? list[q + u] : 0;
-        }
-        for (int u = 0; u < kBatch; ++u) {
-          kraw[u] = C::raw(Kb + size_t(key[u]) * D + sub * E);
-          vraw[u] = C::raw(Vb + size_t(key[u]) * D + sub * E);
-        }
-        for (int u = 0; u < kBatch; ++u) {
-          const float s = group_lanes_sum<LPR>(C::dot(qv, kraw[u]));
-          const float dp = group_lanes_sum<LPR>(C::dot(dO, vraw[u]));
-          if (val[u]) {
-            float kr[E];
-            C::unpack(kraw[u], kr);
-            const float wv = weight(clip(s));
-            sw += wv;
-            const float wdp = wv * dp;
-            swdp += wdp;
-            for (int x = 0; x < E; ++x) {
-              a1[x] = fmaf(wdp, kr[x], a1[x]);
-              a2[x] = fmaf(wv, kr[x], a2[x]);
-            }
-          }
+    sw = swdp = 0.0f;
+  };
+  // entries q .. q + kBatch - 1 (those below n) of a key list, in lock step
+  // with the other lane groups: gathers first, then the sums
+  auto step = [&](const int* lst, int q, int n) {
+    int key[kBatch];
+    bool val[kBatch];
+    uint4 kraw[kBatch], vraw[kBatch];
+    for (int u = 0; u < kBatch; ++u) {
+      val[u] = q + u < n;
+      key[u] = val[u] ? lst[q + u] : 0;
+    }
+    for (int u = 0; u < kBatch; ++u) {
+      kraw[u] = C::raw(Kb + size_t(key[u]) * D + sub * E);
+      vraw[u] = C::raw(Vb + size_t(key[u]) * D + sub * E);
+    }
+    for (int u = 0; u < kBatch; ++u) {
+      const float s = group_lanes_sum<LPR>(C::dot(qv, kraw[u]));
+      const float dp = group_lanes_sum<LPR>(C::dot(dO, vraw[u]));
+      if (val[u]) {
+        float kr[E];
+        C::unpack(kraw[u], kr);
+        const float wv = weight(clip(s));
+        sw += wv;
+        const float wdp = wv * dp;
+        swdp += wdp;
+        for (int x = 0; x < E; ++x) {
+          a1[x] = fmaf(wdp, kr[x], a1[x]);
+          a2[x] = fmaf(wv, kr[x], a2[x]);
         }
       }
-    };
+    }
+  };
+  // dQ and the row's record for the dK/dV pass
+  auto finish_row = [&]() {
+    if (!ok) return;
+    const float norm = p.norms[row];
+    float cfac, shift;
+    if constexpr (REF) {
+      cfac = p.delta[rows + row];
+      shift = p.delta[row];
+    } else {
+      cfac = static_cast<float>(pow(static_cast<double>(norm + kEps), static_cast<double>(alpha) - 2.0));
+      shift = sw > 0.0f ? swdp / sw : 0.0f;
+      if (!finite(shift)) shift = 0.0f;
+    }
+    // dQ_i = scale c (A - shift B) = scale sum_j c w_j (dp_j - shift) k_j
+    const float cs = scale * cfac;
+    float o[E];
+    for (int x = 0; x < E; ++x) {
+      const float v = cs * fmaf(-shift, a2[x], a1[x]);
+      o[x] = finite(v) ? v : 0.0f;
+    }
+    C::store(static_cast<T*>(p.dq) + row * D + sub * E, o);
+    if (sub == 0)
+      p.rowrec[row] = RowRec{clip.nt, clip.lo, clip.hi, 1.0f / (norm + kEps), cfac, -cfac * shift,
+                             0.0f, 0.0f};
+  };
 
+  // ---- count the keys each row of the wave lists (lane: row c16, mask g4)
+  const int c16 = lane & 15, g4 = lane >> 4;
+  const uint16_t* lm = wmask + 4 * c16 + g4;  // this lane's mask of tile e at + e * 256
+  int nl = 0;
+  {
+    int e = e0;
+    for (; e + 4 <= e1; e += 4) {
+      const uint32_t m0 = lm[size_t(e) * 256], m1 = lm[size_t(e + 1) * 256];
+      const uint32_t m2 = lm[size_t(e + 2) * 256], m3 = lm[size_t(e + 3) * 256];
+      nl += __builtin_popcount(m0) + __builtin_popcount(m1) + __builtin_popcount(m2) +
+            __builtin_popcount(m3);
+    }
+    for (; e < e1; ++e) nl += __builtin_popcount(uint32_t(lm[size_t(e) * 256]));
+  }
+  const int rn = int(group_reduce_bits(uint32_t(nl), [](uint32_t x, uint32_t y) { return x + y; }));
+  if (lane < 16) s_rn[w][lane] = rn;
+  int cnt16[16];
+  for (int i = 0; i < 16; ++i) cnt16[i] = s_rn[w][i];
+  int total = 0, off = 0, rank = 0;
+  for (int i = 0; i < 16; ++i) {
+    total += cnt16[i];
+    off += i < c16 ? cnt16[i] : 0;
+    rank += (cnt16[i] > rn || (cnt16[i] == rn && i < c16)) ? 1 : 0;
+  }
+
+  if (total <= kFlat) {  // wave-uniform
+    // ---- balanced path.  Every row's whole list in s_flat (tile order,
+    // then bit 16 g + 4 f + r: the chunked path's order); the lane groups
+    // take the rows in a snake over the descending counts, so each group's
+    // total is close to the mean and the lock-step loop runs near its
+    // length.
+    if (lane < 16) {
+      s_off[w][lane] = off;
+      s_rank[w][rank] = lane;
+    }
+    int base = off;
+    for (int e = e0; e < e1; ++e) {
+      uint32_t m = lm[size_t(e) * 256];
+      const uint32_t n = uint32_t(__builtin_popcount(m));
+      // prefix of the counts over the row's lanes g4 = 0..3 (lanes c16 + 16 g4)
+      const auto pa = __builtin_amdgcn_permlane16_swap(n, n, false, false);
+      const uint32_t pair = pa[0] + pa[1];
+      const auto pb = __builtin_amdgcn_permlane32_swap(pair, pair, false, false);
+      const uint32_t tot = pb[0] + pb[1];
+      int pos = base + int(((g4 & 1) ? pair - n : 0u) + ((g4 & 2) ? tot - pair : 0u));
+      const int kb = ql[e] * kBlock + 4 * g4;
+      while (m) {
+        const int b = __builtin_ctz(m);
+        m &= m - 1;
+        // bit 4 f + r of mask g4 -> key 16 f + 4 g4 + r
+        s_flat[w][pos++] = kb + 16 * (b >> 2) + (b & 3);
+      }
+      base += int(tot);
+    }
+    auto rank_row = [&](int j) { return s_rank[w][j * RPR + ((j & 1) ? RPR - 1 - grp : grp)]; };
+    int j = 0;
+    start_row(rank_row(0));
+    int pos = s_off[w][rr], end = pos + s_rn[w][rr];
+    for (;;) {
+      while (j < NR && pos >= end) {  // group-uniform
+        finish_row();
+        if (++j < NR) {
+          start_row(rank_row(j));
+          pos = s_off[w][rr];
+          end = pos + s_rn[w][rr];
+        }
+      }
+      if (!__any(j < NR)) break;
+      if (j < NR) {
+        step(s_flat[w], pos, end);
+        pos += kBatch;
+      }
+    }
+    return;
+  }
+
+  // ---- chunked path (a wave with more than kFlat listed keys): rows in
+  // rounds of RPR, each row's keys listed kRowList at a time per chunk of
+  // tiles and drained in lock step
+  int* list = s_list[w][grp];
+  for (int r0 = 0; r0 < 16; r0 += RPR) {
+    start_row(r0 + grp);
+    auto drain = [&](int cnt) {
+      const int nmax = groups_max<LPR>(cnt);
+      for (int q = 0; q < nmax; q += kBatch) step(list, q, cnt);
+    };
     for (int c0 = e0; c0 < e1; c0 += kChunk) {
       const int nt = min(kChunk, e1 - c0);
       // the chunk's mask words: 4 tiles (16 rows each) per wave load
@@ -256,30 +385,7 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
         drain(cnt);
       }
     }
-
-    if (ok) {
-      const float norm = p.norms[row];
-      float cfac, shift;
-      if constexpr (REF) {
-        cfac = p.delta[rows + row];
-        shift = p.delta[row];
-      } else {
-        cfac = static_cast<float>(pow(static_cast<double>(norm + kEps), static_cast<double>(alpha) - 2.0));
-        shift = sw > 0.0f ? swdp / sw : 0.0f;
-        if (!finite(shift)) shift = 0.0f;
-      }
-      // dQ_i = scale c (A - shift B) = scale sum_j c w_j (dp_j - shift) k_j
-      const float cs = scale * cfac;
-      float o[E];
-      for (int x = 0; x < E; ++x) {
-        const float v = cs * fmaf(-shift, a2[x], a1[x]);
-        o[x] = finite(v) ? v : 0.0f;
-      }
-      C::store(static_cast<T*>(p.dq) + row * D + sub * E, o);
-      if (sub == 0)
-        p.rowrec[row] = RowRec{clip.nt, clip.lo, clip.hi, 1.0f / (norm + kEps), cfac, -cfac * shift,
-                               0.0f, 0.0f};
-    }
+    finish_row();
   }
 }
 

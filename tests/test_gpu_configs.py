@@ -180,3 +180,39 @@ def test_clustered_full_gradients(dev, d, alpha, k, causal):
     for nm, g, w in zip(("dQ", "dK", "dV"), grads, og):
         assert_close(f"clustered {nm}", np32(g), w, 2e-2)
     _identities("clustered", st.norms, grads, dO, 2e-2)
+
+
+def _wave_list_sizes(st, BH, nQB, nKB):
+    """Keys each dQ wave (16 rows of one query block) lists: the popcounts
+    of its support masks summed over the query block's active tiles."""
+    m = st.sup_mask.reshape(BH, nQB * nKB, 4, 64).to(torch.int32) & 0xFFFF
+    c = torch.zeros_like(m)
+    for b in range(16):
+        c += (m >> b) & 1
+    c = c.sum(-1).cpu()  # [BH, tile, wave]
+    qp = st.q_ptr.reshape(BH, nQB + 1).cpu().long()
+    return torch.stack([c[bh, qp[bh, qb]:qp[bh, qb + 1]].sum(0)
+                        for bh in range(BH) for qb in range(nQB)])
+
+
+@pytest.mark.parametrize("mode", ["entmax", "reference"])
+def test_dq_balanced_and_chunked_paths(dev, mode):
+    """The dQ pass lists a wave's keys whole when they fit in 1024 slots
+    (lane groups then take the rows in a balanced order) and in per-row
+    chunks otherwise.  Causal keys with sinks at alpha 1.25, k 128 give
+    waves of both kinds; every gradient against the oracle in fp32."""
+    print(f"[cfg] dQ paths 1x2x1536x64 fp32 sinks {mode}", flush=True)
+    B, H, N, d = 1, 2, 1536, 64
+    Q, K, V, dO = (_gauss((B, H, N, d), s, torch.float32) for s in (10, 11, 12, 13))
+    K[:, :, :16] *= 4
+    idx = causal_idx(B * H, N)
+    out, st, grads = _run(dev, Q, K, V, dO, idx, idx, 1.25, 128, 0.125, mode)
+    sizes = _wave_list_sizes(st, B * H, N // 64, N // 64)
+    assert (sizes > 1024).any() and (sizes <= 1024).any(), "need waves on both paths"
+    m = orc.GRAD_ENTMAX if mode == "entmax" else orc.GRAD_REFERENCE
+    own, fw, og = oracle_at_gpu_tau(np32(Q), np32(K), np32(V), np32(dO), idx.numpy(), idx.numpy(),
+                                    1.25, 0.125, 128, st.taus.cpu().numpy(), m)
+    np.testing.assert_array_equal(st.mask.cpu().numpy(), own.mask)
+    assert_close("dq paths out", np32(out), fw.out, 1e-5)
+    for nm, g, w in zip(("dQ", "dK", "dV"), grads, og):
+        assert_close(f"dq paths {nm}", np32(g), w, 1e-5)
