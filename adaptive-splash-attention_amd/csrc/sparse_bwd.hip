@@ -298,23 +298,27 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
       s_rank[w][rank] = lane;
     }
     int base = off;
-    for (int e = e0; e < e1; ++e) {
-      uint32_t m = lm[size_t(e) * 256];
-      const uint32_t n = uint32_t(__builtin_popcount(m));
-      // prefix of the counts over the row's lanes g4 = 0..3 (lanes c16 + 16 g4)
-      const auto pa = __builtin_amdgcn_permlane16_swap(n, n, false, false);
-      const uint32_t pair = pa[0] + pa[1];
-      const auto pb = __builtin_amdgcn_permlane32_swap(pair, pair, false, false);
-      const uint32_t tot = pb[0] + pb[1];
-      int pos = base + int(((g4 & 1) ? pair - n : 0u) + ((g4 & 2) ? tot - pair : 0u));
-      const int kb = ql[e] * kBlock + 4 * g4;
-      while (m) {
-        const int b = __builtin_ctz(m);
-        m &= m - 1;
-        // bit 4 f + r of mask g4 -> key 16 f + 4 g4 + r
-        s_flat[w][pos++] = kb + 16 * (b >> 2) + (b & 3);
+    for (int e8 = e0; e8 < e1; e8 += 8) {
+      uint32_t mm[8];  // 8 tiles' masks in flight together
+      for (int u = 0; u < 8; ++u) mm[u] = e8 + u < e1 ? uint32_t(lm[size_t(e8 + u) * 256]) : 0u;
+      for (int u = 0; u < 8 && e8 + u < e1; ++u) {
+        uint32_t m = mm[u];
+        const uint32_t n = uint32_t(__builtin_popcount(m));
+        // prefix of the counts over the row's lanes g4 = 0..3 (lanes c16 + 16 g4)
+        const auto pa = __builtin_amdgcn_permlane16_swap(n, n, false, false);
+        const uint32_t pair = pa[0] + pa[1];
+        const auto pb = __builtin_amdgcn_permlane32_swap(pair, pair, false, false);
+        const uint32_t tot = pb[0] + pb[1];
+        int pos = base + int(((g4 & 1) ? pair - n : 0u) + ((g4 & 2) ? tot - pair : 0u));
+        const int kb = ql[e8 + u] * kBlock + 4 * g4;
+        while (m) {
+          const int b = __builtin_ctz(m);
+          m &= m - 1;
+          // bit 4 f + r of mask g4 -> key 16 f + 4 g4 + r
+          s_flat[w][pos++] = kb + 16 * (b >> 2) + (b & 3);
+        }
+        base += int(tot);
       }
-      base += int(tot);
     }
     auto rank_row = [&](int j) { return s_rank[w][j * RPR + ((j & 1) ? RPR - 1 - grp : grp)]; };
     int j = 0;
@@ -403,7 +407,9 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   constexpr int KPB = 4 * KPW;        // keys per block
   constexpr int SLICES = kBlock / KPB;
   constexpr int PP = AlphaPow<AC>::P, PW = AlphaPow<AC>::W;
-  __shared__ int s_list[4][KPW][kKeyList];
+  // the waves' key lists, [wave][key][kKeyList], then one dump slot per
+  // lane for the phase A stores of lanes with nothing to list
+  __shared__ int s_lists[4 * KPW * kKeyList + 4 * kWave];
   __shared__ int s_cnt[4][KPW];
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
@@ -436,7 +442,7 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   float dk[E], dv[E];
   for (int x = 0; x < E; ++x) dk[x] = dv[x] = 0.0f;
 
-  const int* mylist = s_list[w][grp];
+  const int* mylist = s_lists + (w * KPW + grp) * kKeyList;
   // phase B: this group's listed rows, kBatch at a time in every group
   auto drain = [&]() {
     const int cnt = s_cnt[w][grp];
@@ -477,10 +483,12 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
     }
   };
 
-  // phase A over the key block's query tiles (ascending query blocks),
-  // kTileGroup tiles at a time with their loads in flight together:
-  // lane L <-> row L of a tile.  The list lengths are wave-uniform
-  // (scalar registers); drain() reads them from s_cnt.
+  // phase A over the key block's query tiles (ascending query blocks).
+  // Lane L <-> row L of a tile.  The tiles' query blocks and q_list
+  // positions are fetched for up to 64 tiles at once (one lane each); the
+  // mask words then come kTileGroup tiles at a time, the next group's
+  // loads in flight while the current group is listed.  The list lengths
+  // are wave-uniform (scalar registers); drain() reads them from s_cnt.
   constexpr int kTileGroup = 8;
   int cnt[KPW];
   for (int k = 0; k < KPW; ++k) cnt[k] = 0;
@@ -492,33 +500,50 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   };
   const int32_t* pm = p.posmap + size_t(bh) * nQB * nKB + kb;  // tile (qb, kb) at + qb * nKB
   const int x0 = kp[kb], x1 = kp[kb + 1];
-  for (int c0 = x0; c0 < x1; c0 += kTileGroup) {
-    const int nt = min(kTileGroup, x1 - c0);
-    const int my_qb = lane < nt ? kl[c0 + lane] : 0;
-    const int my_e = lane < nt ? pm[size_t(my_qb) * nKB] : 0;
-    uint64_t word[kTileGroup];
-    for (int u = 0; u < kTileGroup; ++u) {
-      const int e = __shfl(my_e, u, kWave);
-      word[u] = u < nt ? *reinterpret_cast<const uint64_t*>(hmask + size_t(e) * 256 +
-                                                             (lane >> 4) * 64 + 4 * (lane & 15))
-                       : 0ull;
-    }
-    for (int u = 0; u < kTileGroup; ++u) {
-      if (u >= nt) break;
-      // room for a whole tile in every list of the wave, else drain first
-      bool room = true;
-      for (int k = 0; k < KPW; ++k) room = room && cnt[k] + kWave <= kKeyList;
-      if (!room) drain_lists();
-      // row L's four masks: bit 16 g + 4 f + r <-> key 16 f + 4 g + r
-      const int row = __shfl(my_qb, u, kWave) * kBlock + lane;
-      for (int k = 0; k < KPW; ++k) {
-        const int key = jb + k;
-        const int bit = 16 * ((key >> 2) & 3) + 4 * (key >> 4) + (key & 3);
-        const bool on = ((word[u] >> bit) & 1u) != 0;
-        const uint64_t col = __ballot(on);
-        if (on) s_list[w][k][cnt[k] + lane_rank(col)] = row;
-        cnt[k] += __builtin_popcountll(col);
+  static_assert(KPW <= 8 && kBlock % KPW == 0, "a wave's keys must fit one mask pair");
+  const int gb = ((jb >> 2) & 3) & ~1;
+  const int dump = 4 * KPW * kKeyList + w * kWave + lane;
+  for (int m0 = x0; m0 < x1; m0 += kWave) {
+    const int nm = min(kWave, x1 - m0);
+    const int my_qb = lane < nm ? kl[m0 + lane] : 0;
+    const int my_e = lane < nm ? pm[size_t(my_qb) * nKB] : 0;
+    // Row L's masks g and g + 1 (g = gb, even) of a tile, which hold the
+    // bits of all this wave's keys (KPW <= 8 consecutive keys span at most
+    // two values of (key >> 2) & 3, and an aligned pair covers them).
+    const uint16_t* rowm = hmask + (lane >> 4) * 64 + 4 * (lane & 15) + gb;
+    // (slots past the last tile re-read the last tile and are not used)
+    auto fetch = [&](int g0, uint32_t (&wd)[kTileGroup]) {
+      for (int u = 0; u < kTileGroup; ++u) {
+        const int e = __builtin_amdgcn_readlane(my_e, min(g0 + u, nm - 1));
+        wd[u] = *reinterpret_cast<const uint32_t*>(rowm + size_t(e) * 256);
       }
+    };
+    uint32_t word[kTileGroup], next[kTileGroup];
+    fetch(0, word);
+    for (int g0 = 0; g0 < nm; g0 += kTileGroup) {
+      fetch(g0 + kTileGroup, next);  // unconditional: the waits stay exact
+#pragma unroll
+      for (int u = 0; u < kTileGroup; ++u) {
+        if (g0 + u >= nm) break;
+        // room for a whole tile in every list of the wave, else drain first
+        bool room = true;
+        for (int k = 0; k < KPW; ++k) room = room && cnt[k] + kWave <= kKeyList;
+        if (!room) drain_lists();
+        // bit 16 (g - gb) + 4 f + r of the pair <-> key 16 f + 4 g + r.
+        // Every lane stores: a lane whose row does not list the key writes
+        // its dump slot instead of branching around the store.
+        const int row = __builtin_amdgcn_readlane(my_qb, g0 + u) * kBlock + lane;
+        for (int k = 0; k < KPW; ++k) {
+          const int key = jb + k;
+          const int bit = 16 * (((key >> 2) & 3) - gb) + 4 * (key >> 4) + (key & 3);
+          const bool on = ((word[u] >> bit) & 1u) != 0;
+          const uint64_t col = __ballot(on);
+          const int at = (w * KPW + k) * kKeyList + cnt[k] + lane_rank(col);
+          s_lists[on ? at : dump] = row;
+          cnt[k] += __builtin_popcountll(col);
+        }
+      }
+      for (int u = 0; u < kTileGroup; ++u) word[u] = next[u];
     }
   }
   drain_lists();
