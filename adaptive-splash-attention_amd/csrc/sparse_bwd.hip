@@ -46,7 +46,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kRowList = 64;   // keys listed per row before a dQ phase B
 constexpr int kKeyList = 128;  // rows listed per key before a dK/dV phase B
-constexpr int kBatch = 2;      // entries whose gathers are in flight together
+constexpr int kBatch = 2;      // dK/dV entries whose gathers are in flight together
+constexpr int kBatchQ = 3;     // dQ entries whose gathers are in flight together
 constexpr int kChunk = 16;     // tiles whose masks are fetched together
 constexpr int kFlat = 1024;    // keys a dQ wave lists at once on its balanced path
 
@@ -205,21 +206,21 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
     for (int x = 0; x < E; ++x) a1[x] = a2[x] = 0.0f;
     sw = swdp = 0.0f;
   };
-  // entries q .. q + kBatch - 1 (those below n) of a key list, in lock step
+  // entries q .. q + kBatchQ - 1 (those below n) of a key list, in lock step
   // with the other lane groups: gathers first, then the sums
   auto step = [&](const int* lst, int q, int n) {
-    int key[kBatch];
-    bool val[kBatch];
-    uint4 kraw[kBatch], vraw[kBatch];
-    for (int u = 0; u < kBatch; ++u) {
+    int key[kBatchQ];
+    bool val[kBatchQ];
+    uint4 kraw[kBatchQ], vraw[kBatchQ];
+    for (int u = 0; u < kBatchQ; ++u) {
       val[u] = q + u < n;
       key[u] = val[u] ? lst[q + u] : 0;
     }
-    for (int u = 0; u < kBatch; ++u) {
+    for (int u = 0; u < kBatchQ; ++u) {
       kraw[u] = C::raw(Kb + size_t(key[u]) * D + sub * E);
       vraw[u] = C::raw(Vb + size_t(key[u]) * D + sub * E);
     }
-    for (int u = 0; u < kBatch; ++u) {
+    for (int u = 0; u < kBatchQ; ++u) {
       const float s = group_lanes_sum<LPR>(C::dot(qv, kraw[u]));
       const float dp = group_lanes_sum<LPR>(C::dot(dO, vraw[u]));
       if (val[u]) {
@@ -336,7 +337,7 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
       if (!__any(j < NR)) break;
       if (j < NR) {
         step(s_flat[w], pos, end);
-        pos += kBatch;
+        pos += kBatchQ;
       }
     }
     return;
@@ -350,7 +351,7 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
     start_row(r0 + grp);
     auto drain = [&](int cnt) {
       const int nmax = groups_max<LPR>(cnt);
-      for (int q = 0; q < nmax; q += kBatch) step(list, q, cnt);
+      for (int q = 0; q < nmax; q += kBatchQ) step(list, q, cnt);
     };
     for (int c0 = e0; c0 < e1; c0 += kChunk) {
       const int nt = min(kChunk, e1 - c0);
