@@ -591,6 +591,11 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
   }
 
   // ---------------- select: sort each row's candidates ----------------
+  // The top-k key blocks go into the block's mask bitmap: with at most 64
+  // key blocks as one register word per lane, OR-ed over the wave at the
+  // end (the per-entry LDS atomics would all hit the same two words).
+  const bool kb_word = nKB <= 64;
+  uint64_t kbm = 0;
   auto emit = [&](int r, int e, uint64_t key) {
     if (e >= k || q0 + r >= NQ) return;
     const bool real = key != 0ull;
@@ -604,7 +609,8 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
     }
     if (idx >= 0) {
       const int kb = idx / kBlock;
-      atomicOr(&s_bits[kb >> 5], 1u << (kb & 31));
+      if (kb_word) kbm |= uint64_t(1) << kb;
+      else atomicOr(&s_bits[kb >> 5], 1u << (kb & 31));
     }
   };
   auto ncand = [&](int r) -> int { return (q0 + r < NQ) ? min(int(s_cnt[r]), cap) : 0; };
@@ -631,6 +637,19 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
       sort_rows(std::integral_constant<int, 16>{}, base + 4);
     } else {
       for (int h = 0; h < 4; ++h) sort_rows(std::integral_constant<int, 32>{}, base + 2 * h);
+    }
+  }
+  if (kb_word) {  // block-uniform
+    kbm |= lane_xor64<1>(kbm);
+    kbm |= lane_xor64<2>(kbm);
+    kbm |= lane_xor64<4>(kbm);
+    kbm |= lane_xor64<8>(kbm);
+    auto bor = [](uint32_t x, uint32_t y) { return x | y; };
+    const uint32_t lo = group_reduce_bits(uint32_t(kbm), bor);
+    const uint32_t hi = group_reduce_bits(uint32_t(kbm >> 32), bor);
+    if (L == 0) {
+      if (lo) atomicOr(&s_bits[0], lo);
+      if (hi) atomicOr(&s_bits[1], hi);
     }
   }
   __syncthreads();
