@@ -2,7 +2,7 @@
 //
 // Reference: build_lookup_kernel (adasplashattention.cu:219-242), which
 // builds the query-major list (Qi_ptr / Qi_idx) with one serial thread per
-// (batch, head).  Here one 256-thread block per (batch, head) builds both
+// (batch, head).  Here two 256-thread blocks per (batch, head) build
 //   query-major:  q_ptr[nQB+1], q_list[nQB*nKB]  (same layout as Qi_ptr/Qi_idx)
 //   key-major:    k_ptr[nKB+1], k_list[nKB*nQB]  (feeds the atomic-free dK/dV)
 // with lists in ascending block order and zero-filled tails.  A wave takes
@@ -55,27 +55,45 @@ __device__ __forceinline__ int scan_line(const uint8_t* m, size_t rs, size_t es,
   return c;
 }
 
-__global__ __launch_bounds__(kThreads) void compact_kernel(CompactParams p) {
-  extern __shared__ int sm[];
-  const int nQB = p.nQB, nKB = p.nKB, bh = blockIdx.x, t = threadIdx.x;
+// Mask bytes of one head staged in LDS when they fit (the scans then read
+// LDS instead of making dependent global loads, 4 per line of the mask).
+constexpr int kStageMax = 32 * 1024;
+
+template <bool STAGED>
+__device__ __forceinline__ void compact_head(const CompactParams& p, int* sm) {
+  const int nQB = p.nQB, nKB = p.nKB, bh = blockIdx.x >> 1, t = threadIdx.x;
+  const bool key_major = (blockIdx.x & 1) != 0;  // the two lists in separate blocks
   const int w = t >> 6, L = t & 63;
-  const uint8_t* m = p.mask + size_t(bh) * nQB * nKB;
   int* cnt = sm;                  // max(nQB, nKB)
   int* ptr = sm + max(nQB, nKB);  // max(nQB, nKB) + 1
-
-  // ---- query-major: rows of the mask ----
-  for (int i = w; i < nQB; i += kWaves) {
-    const int c = scan_line(m, nKB, 1, i, nKB, nullptr, L);
-    if (L == 0) cnt[i] = c;
+  const uint8_t* m = p.mask + size_t(bh) * nQB * nKB;
+  if constexpr (STAGED) {
+    // 16-byte chunks, then the tail bytes; the staged copy starts 16-byte
+    // aligned after the scan arrays
+    uint8_t* sl = reinterpret_cast<uint8_t*>(sm + ((2 * max(nQB, nKB) + 1 + 3) & ~3));
+    const int nb = nQB * nKB, n16 = (size_t(m) % 16 == 0) ? nb / 16 : 0;
+    for (int i = t; i < n16; i += kThreads)
+      reinterpret_cast<uint4*>(sl)[i] = reinterpret_cast<const uint4*>(m)[i];
+    for (int i = n16 * 16 + t; i < nb; i += kThreads) sl[i] = m[i];
+    __syncthreads();
+    m = sl;
   }
-  __syncthreads();
-  block_scan(cnt, ptr, nQB);
-  int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
-  int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
-  for (int i = t; i <= nQB; i += kThreads) qp[i] = ptr[i];
-  for (int i = w; i < nQB; i += kWaves) scan_line(m, nKB, 1, i, nKB, ql + ptr[i], L);
-  for (int e = ptr[nQB] + t; e < nQB * nKB; e += kThreads) ql[e] = 0;
-  __syncthreads();
+
+  if (!key_major) {
+    // ---- query-major: rows of the mask ----
+    for (int i = w; i < nQB; i += kWaves) {
+      const int c = scan_line(m, nKB, 1, i, nKB, nullptr, L);
+      if (L == 0) cnt[i] = c;
+    }
+    __syncthreads();
+    block_scan(cnt, ptr, nQB);
+    int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
+    int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
+    for (int i = t; i <= nQB; i += kThreads) qp[i] = ptr[i];
+    for (int i = w; i < nQB; i += kWaves) scan_line(m, nKB, 1, i, nKB, ql + ptr[i], L);
+    for (int e = ptr[nQB] + t; e < nQB * nKB; e += kThreads) ql[e] = 0;
+    return;
+  }
 
   // ---- key-major: columns of the mask ----
   for (int j = w; j < nKB; j += kWaves) {
@@ -91,12 +109,19 @@ __global__ __launch_bounds__(kThreads) void compact_kernel(CompactParams p) {
   for (int e = ptr[nKB] + t; e < nQB * nKB; e += kThreads) kl[e] = 0;
 }
 
+__global__ __launch_bounds__(kThreads) void compact_kernel(CompactParams p) {
+  extern __shared__ int sm[];
+  if (p.nQB * p.nKB <= kStageMax) compact_head<true>(p, sm);  // block-uniform
+  else compact_head<false>(p, sm);
+}
+
 }  // namespace
 
 hipError_t launch_compact(const CompactParams& p, hipStream_t s) {
   const int n = p.nQB > p.nKB ? p.nQB : p.nKB;
-  const size_t lds = sizeof(int) * size_t(2 * n + 1);
-  hipLaunchKernelGGL(compact_kernel, dim3(p.BH), dim3(kThreads), lds, s, p);
+  size_t lds = sizeof(int) * size_t(2 * n + 1);
+  if (p.nQB * p.nKB <= kStageMax) lds = ((lds + 15) & ~size_t(15)) + size_t(p.nQB) * p.nKB;
+  hipLaunchKernelGGL(compact_kernel, dim3(2 * p.BH), dim3(kThreads), lds, s, p);
   return hipGetLastError();
 }
 
