@@ -113,6 +113,8 @@ hipError_t launch_forward(const ForwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_delta(const BackwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_dq(const BackwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BackwardParams& p, bool bf16, hipStream_t s);
+// The support-pair passes: dQ writes the row records and the position map
+// that dK/dV reads, so dK/dV must follow it on the stream.
 hipError_t launch_bwd_dq_sparse(const BackwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_dkdv_sparse(const BackwardParams& p, bool bf16, hipStream_t s);
 

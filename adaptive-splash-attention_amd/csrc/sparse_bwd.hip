@@ -20,8 +20,9 @@
 //              lock-step batches: s = q.k_j, w, dp = dO.v_j, and the fp32
 //              sums A = sum w dp k_j, B = sum w k_j, sum w, sum w dp give
 //              dQ = scale c (A - shift B).  It also writes each row's
-//              constants for the dK/dV pass.  The lock step runs as long as
-//              the longest list among the lane groups, so when the wave's
+//              constants and the tiles' position map (tile (qb, kb) -> its
+//              q_list position) for the dK/dV pass.  The lock step runs as
+//              long as the longest list among the lane groups, so when the wave's
 //              16 rows list at most kFlat keys in all, it counts them first,
 //              lists every row whole, and gives lane group g the rows of
 //              count ranks g, 15 - g, 16 + g, ... (a snake over the sorted
@@ -126,23 +127,6 @@ __device__ __forceinline__ int groups_max(int v) {
 }
 
 // ---------------------------------------------------------------------------
-// Position map: posmap[bh][qb * nKB + kb] = the head's q_list position of
-// the tile (qb, kb), for every active tile (the dK/dV pass finds the
-// tile's masks through it).  One wave per query block.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void posmap_kernel(BackwardParams p) {
-  const int nQB = p.d.nQB, nKB = p.d.nKB;
-  const int t = threadIdx.x, lane = t & 63;
-  const int task = blockIdx.x * (kThreads / kWave) + (t >> 6);
-  if (task >= nQB * p.d.BH) return;
-  const int qb = task % nQB, bh = task / nQB;
-  const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
-  const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
-  int32_t* pm = p.posmap + size_t(bh) * nQB * nKB + size_t(qb) * nKB;
-  for (int e = qp[qb] + lane; e < qp[qb + 1]; e += kWave) pm[ql[e]] = e;
-}
-
-// ---------------------------------------------------------------------------
 // dQ
 // ---------------------------------------------------------------------------
 template <typename T, int D, int AC, bool REF>
@@ -174,6 +158,12 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
   const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
   const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
   const int e0 = qp[qb], e1 = qp[qb + 1];
+  // Position map for the dK/dV pass (which runs after this one):
+  // posmap[bh][qb * nKB + kb] = the head's q_list position of tile (qb, kb).
+  {
+    int32_t* pm = p.posmap + size_t(bh) * nQB * nKB + size_t(qb) * nKB;
+    for (int e = e0 + t; e < e1; e += kThreads) pm[ql[e]] = e;
+  }
   // the wave's masks of tile e: row c's word at + e * 256 + 4 c
   const uint16_t* wmask = p.sup.mask + size_t(bh) * nQB * nKB * 256 + w * 64;
   auto weight = [&](float v) {
@@ -601,10 +591,7 @@ hipError_t launch_bwd_dq_sparse(const BackwardParams& p, bool bf16, hipStream_t 
   return launch_sparse<false>(p, bf16, s);
 }
 hipError_t launch_bwd_dkdv_sparse(const BackwardParams& p, bool bf16, hipStream_t s) {
-  const int waves = p.d.nQB * p.d.BH, per = kThreads / kWave;
-  hipLaunchKernelGGL(posmap_kernel, dim3((waves + per - 1) / per), dim3(kThreads), 0, s, p);
-  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-  return launch_sparse<true>(p, bf16, s);
+  return launch_sparse<true>(p, bf16, s);  // after the dQ pass, which writes the position map
 }
 
 }  // namespace asa

@@ -42,10 +42,11 @@ ELEM = 2                 # bf16 bytes
 COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # HBM bytes per launch of each kernel at this workload, measured with
 # rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), the factors a plain
-# 256 MiB device copy gives (profiles/headline_hbm_traffic.md).  The
-# bwd_dkdv_sparse launch includes its position-map kernel; bwd_dq and
-# bwd_dkdv are the dense passes (run when no support masks were recorded).
-HBM_TRAFFIC = {'bounds': 1107865, 'select': 104393800, 'tau': 34763867, 'compact': 2751429, 'forward': 207626949, 'bwd_dq_sparse': 262603365, 'bwd_dkdv_sparse': 283279699, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
+# 256 MiB device copy gives (profiles/headline_hbm_traffic.md).
+# bwd_dq_sparse includes the position map it writes for bwd_dkdv_sparse
+# (measured as a kernel of its own, 1.4 MB); bwd_dq and bwd_dkdv are the
+# dense passes (run when no support masks were recorded).
+HBM_TRAFFIC = {'bounds': 1107865, 'select': 104393800, 'tau': 34763867, 'compact': 2751429, 'forward': 207626949, 'bwd_dq_sparse': 264010263, 'bwd_dkdv_sparse': 281872801, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
 
 
 def effective_flops(B, H, N, d):
@@ -93,7 +94,7 @@ def kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep, nsup):
         # its 512 bytes of masks
         "bwd_dq_sparse": dict(bound="hbm", flops=8.0 * d * nsup,
                               bytes=nsup * 2 * d * ELEM + 3 * rows * d * ELEM + nnzb * 512
-                              + rows * (8 + 32)),
+                              + rows * (8 + 32) + 4 * nnzb),
         "bwd_dkdv_sparse": dict(bound="hbm", flops=8.0 * d * nsup,
                                 bytes=nsup * (2 * d * ELEM + 32) + 4 * rows * d * ELEM
                                 + nnzb * 512 + 4 * BH * nQB * nKB),
