@@ -61,6 +61,7 @@ struct ForwardParams {
   const int32_t* q_list;
   void* out;
   float* norms;
+  const int2* kbounds;  // (min, max) position per key block [BH * nKB], from the score pass
   // Support masks (optional: sup.mask == nullptr writes none).
   SupportMasks sup;
 };

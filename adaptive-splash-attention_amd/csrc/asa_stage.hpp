@@ -32,18 +32,21 @@ struct Stager {
   uint4 r[kPer][4];
 
   // Rows [row0, row0 + 64) of src0 / src1 ([*, D] row-major); rows >= nrows
-  // read as zero.
+  // read as zero.  A tile wholly inside loads its quad's four rows from one
+  // address (the row steps become immediate offsets), without tests.
   __device__ __forceinline__ void load(const T* src0, const T* src1, int row0, int nrows, int t) {
+    const bool whole = row0 + kBlock <= nrows;  // block-uniform
     for (int i = 0; i < kPer; ++i) {
       const int qi = t + i * NT;
       const int job = qi / kQuads, q = qi % kQuads;
       const int rq = q / kCpr, cc = q % kCpr;
-      const T* src = job == 0 ? src0 : src1;
-      for (int j = 0; j < 4; ++j) {
-        const int row = row0 + 4 * rq + j;
-        r[i][j] = row < nrows
-                      ? *reinterpret_cast<const uint4*>(src + size_t(row) * D + cc * kEpc)
-                      : uint4{0u, 0u, 0u, 0u};
+      const T* src = (job == 0 ? src0 : src1) + size_t(row0 + 4 * rq) * D + cc * kEpc;
+      if (whole) {
+        for (int j = 0; j < 4; ++j) r[i][j] = *reinterpret_cast<const uint4*>(src + j * D);
+      } else {
+        for (int j = 0; j < 4; ++j)
+          r[i][j] = row0 + 4 * rq + j < nrows ? *reinterpret_cast<const uint4*>(src + j * D)
+                                              : uint4{0u, 0u, 0u, 0u};
       }
     }
   }
@@ -70,6 +73,10 @@ struct PosStager {
   // entries past `n` read as `pad`
   __device__ __forceinline__ void load(const int32_t* pos, int base, int n, int pad, int t) {
     if (t < kWave) v = base + t < n ? pos[base + t] : pad;
+  }
+  // positions only (the caller knows the flag otherwise)
+  __device__ __forceinline__ void store(int* dst, int t) const {
+    if (t < kWave) dst[t] = v;
   }
   // kMax: flag = max over the tile <= bound; else flag = min over the tile >= bound
   template <bool kMax>

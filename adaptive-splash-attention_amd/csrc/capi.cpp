@@ -288,6 +288,7 @@ int asa_forward(const asa_problem* p, const void* q, const void* k, const void* 
   fp.q_list = st->q_list;
   fp.out = out;
   fp.norms = st->norms;
+  fp.kbounds = reinterpret_cast<const int2*>(static_cast<const char*>(workspace) + tkv_bytes(sh));
   fp.sup.mask = st->sup_mask;
   asa::profile_begin("forward", s);
   hipError_t e = asa::launch_forward(fp, sh.bf16, s);

@@ -28,7 +28,6 @@ template <typename T, int D> struct alignas(16) FwdSmem {
   T K[2][kBlock * Tile<T, D>::kRs];
   T V[2][kBlock * Tile<T, D>::kRs];
   int kid[2][kBlock];
-  int full[2];
 };
 
 template <typename T, int D, int PC, bool EMIT>
@@ -54,12 +53,15 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   const float am1 = p.d.alpha - 1.0f;
   const float a = 1.0f / am1;
   const ClippedU clip(am1, p.d.scale, qok ? p.taus[row] : 0.0f, qok);  // invalid rows: p = 0
-  // smallest position of the block's valid rows (wave 0 tests tiles with it)
-  int qmin = 0;
-  if (w == 0) {
+  // smallest position of the block's valid rows: a key block whose largest
+  // position (from the score pass's bounds) is at most this, and that lies
+  // wholly below NK, is visible to every row of the block
+  int qmin;
+  {
     const int qq = qb * kBlock + lane;
     qmin = wave_reduce_minmax<false>(qq < NQ ? p.q_idx[size_t(bh) * NQ + qq] : INT32_MAX);
   }
+  const int2* kbnd = p.kbounds + size_t(bh) * nKB;
 
   f32x4 o[D / 16];
   for (int db = 0; db < D / 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -81,7 +83,7 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   };
   auto put = [&](int b) {
     st.store(sm.K[b], sm.V[b], t);
-    ps.store<true>(sm.kid[b], &sm.full[b], qmin, t);
+    ps.store(sm.kid[b], t);
   };
   if (e0 < e1) {
     fetch(e0);
@@ -118,7 +120,8 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
           rowsum += pv;
         }
     };
-    if (sm.full[b] != 0) weights(std::false_type{});
+    const int kb = ql[e];
+    if (kb * kBlock + kBlock <= NK && kbnd[kb].y <= qmin) weights(std::false_type{});
     else weights(std::true_type{});
     tile_t_x_acc<D>(o, sm.V[b], acc, lane);
     if (e + 1 < e1) {
