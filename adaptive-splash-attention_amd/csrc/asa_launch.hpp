@@ -67,10 +67,11 @@ struct ForwardParams {
 };
 
 // Per-row constants of the support-mask backward, written by its dQ pass
-// for its dK/dV pass: ClippedU's nt, lo, hi; 1/(sum p + EPS); the gradient
-// factor c and cs = -c shift (ds = w (c dp + cs)).
+// for its dK/dV pass: ClippedU's nt (its lo and hi follow from nt and
+// alpha), 1/(sum p + EPS), the gradient factor c and cs = -c shift
+// (ds = w (c dp + cs)).  16 bytes: one load per listed row.
 struct alignas(16) RowRec {
-  float nt, lo, hi, invn, c, cs, pad0, pad1;
+  float nt, invn, c, cs;
 };
 
 struct BackwardParams {

@@ -249,8 +249,7 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
     }
     C::store(static_cast<T*>(p.dq) + row * D + sub * E, o);
     if (sub == 0)
-      p.rowrec[row] = RowRec{clip.nt, clip.lo, clip.hi, 1.0f / (norm + kEps), cfac, -cfac * shift,
-                             0.0f, 0.0f};
+      p.rowrec[row] = RowRec{clip.nt, 1.0f / (norm + kEps), cfac, -cfac * shift};
   };
 
   // ---- count the keys each row of the wave lists (lane: row c16, mask g4)
@@ -459,7 +458,10 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
           float qr[E], gr[E];
           C::unpack(qraw[u], qr);
           C::unpack(graw[u], gr);
-          const float v = __builtin_amdgcn_fmed3f(fmaf(cu, s, rc[u].nt), rc[u].lo, rc[u].hi);
+          // ClippedU of a valid row (the lists hold valid rows only)
+          const float lo = fmaxf(fmaf(-10.f, am1, rc[u].nt), 0.f);
+          const float hi = fmaxf(fmaf(10.f, am1, rc[u].nt), 0.f);
+          const float v = __builtin_amdgcn_fmed3f(fmaf(cu, s, rc[u].nt), lo, hi);
           const float pn = pow_clipped<PP>(v, a) * rc[u].invn;
           float wv = pow_clipped<PW>(v, ew);
           if constexpr (REF) wv = v > kEps ? wv : 0.0f;  // the reference's u > EPS
