@@ -126,7 +126,7 @@ void sizes_of(const Shape& s, asa_sizes* z) {
   z->topk_val = rows * s.k * sizeof(float);
   z->sup_mask = blocks * 256 * sizeof(uint16_t);
   // forward: the rows' sorted top-k values and the key blocks' position
-  // bounds; backward: two floats per row, a 32-byte record per row and an
+  // bounds; backward: two floats per row, a 16-byte record per row and an
   // int per tile
   const size_t fwd_ws = tkv_bytes(s) + size_t(s.BH) * s.nKB * 2 * sizeof(int32_t);
   const size_t bwd_ws = bwd_map_offset(s) + blocks * sizeof(int32_t);
