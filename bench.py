@@ -45,10 +45,10 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # HBM bytes per launch of each kernel at this workload, measured with
 # rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), the factors a plain
 # 256 MiB device copy gives (profiles/headline_hbm_traffic.md).
-# bwd_dq_sparse includes the position map it writes for bwd_dkdv_sparse
-# (measured as a kernel of its own, 1.4 MB); bwd_dq and bwd_dkdv are the
-# dense passes (run when no support masks were recorded).
-HBM_TRAFFIC = {'bounds': 1107865, 'select': 104393800, 'tau': 34763867, 'compact': 2751429, 'forward': 207626949, 'bwd_dq_sparse': 264010263, 'bwd_dkdv_sparse': 281872801, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
+# bwd_dq_sparse includes the position map it writes for bwd_dkdv_sparse;
+# bwd_dq and bwd_dkdv are the dense passes (run when no support masks were
+# recorded).
+HBM_TRAFFIC = {'bounds': 1107863, 'select': 103744695, 'tau': 34745314, 'compact': 2751257, 'forward': 207667377, 'bwd_dq_sparse': 257873289, 'bwd_dkdv_sparse': 276912586, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
 
 
 def effective_flops(B, H, N, d):
