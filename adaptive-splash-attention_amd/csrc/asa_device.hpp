@@ -197,6 +197,13 @@ __device__ __forceinline__ int key_index(uint64_t k) { return static_cast<int>(~
 // that the blocks of each XCD cover one contiguous range of tasks (a task
 // index is (batch*head) * blocks_per_head + block), which keeps the K/V (or
 // Q/dO) tiles of a head in the L2 of the XCD that reads them.
+//
+// Under the causal mask a block's work grows with its query block (and
+// shrinks with its key block), so the query-major kernels walk each head's
+// query blocks from the last to the first: the heaviest blocks of a head
+// start first and the short ones fill in behind them, which shortens the
+// tail of the launch.  The key-major kernels keep ascending key blocks,
+// which is already heaviest first.
 constexpr int kXcds = 8;
 __device__ __forceinline__ int xcd_task(int i, int total) {
   const int x = i % kXcds, j = i / kXcds;

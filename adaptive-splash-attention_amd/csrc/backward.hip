@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
   const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
-  const int qb = task % nQB, bh = task / nQB;
+  const int qb = nQB - 1 - task % nQB, bh = task / nQB;
   const int q = qb * kBlock + 16 * w + c16;
   const bool qok = q < NQ;
   const size_t rows = size_t(p.d.BH) * NQ;

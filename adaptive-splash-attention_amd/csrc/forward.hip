@@ -38,7 +38,7 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
   const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
-  const int qb = task % nQB, bh = task / nQB;
+  const int qb = nQB - 1 - task % nQB, bh = task / nQB;
   const int q = qb * kBlock + 16 * w + c16;  // this lane's query row
   const bool qok = q < NQ;
   const size_t row = size_t(bh) * NQ + (qok ? q : 0);

@@ -352,7 +352,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
 
   const int t = threadIdx.x, w = t >> 6, L = t & 63, g = L >> 4, c = L & 15;
   const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
-  const int qb = task % nQB, bh = task / nQB, q0 = qb * kBlock;
+  const int qb = nQB - 1 - task % nQB, bh = task / nQB, q0 = qb * kBlock;
   const int lq = 16 * w + c;  // this lane's row within the block
   const bool rowok = q0 + lq < NQ;
   const size_t grow = size_t(bh) * NQ + q0 + lq;  // global row (valid if rowok)

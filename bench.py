@@ -48,7 +48,7 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # bwd_dq_sparse includes the position map it writes for bwd_dkdv_sparse;
 # bwd_dq and bwd_dkdv are the dense passes (run when no support masks were
 # recorded).
-HBM_TRAFFIC = {'bounds': 1107863, 'select': 103744695, 'tau': 34745314, 'compact': 2751257, 'forward': 207667377, 'bwd_dq_sparse': 257873289, 'bwd_dkdv_sparse': 276912586, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
+HBM_TRAFFIC = {'bounds': 1108138, 'select': 103819594, 'tau': 34748757, 'compact': 2751317, 'forward': 207541610, 'bwd_dq_sparse': 248106329, 'bwd_dkdv_sparse': 277114956, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
 
 
 def effective_flops(B, H, N, d):
