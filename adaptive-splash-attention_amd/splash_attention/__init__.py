@@ -18,6 +18,8 @@ there is no CPU or PyTorch fallback.
 """
 from __future__ import annotations
 
+import torch
+
 from . import ops
 from ._lib import ASAError
 from .function import SplashAttentionFunction, splash_attention
@@ -38,19 +40,24 @@ __version__ = "0.1.0"
 
 def forward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, k_keep: int = 8):
     """Reference-compatible native forward (adasplashattention.cu:537-609)."""
+    d, dtype = Q.size(-1), Q.dtype
     Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     out, _ = ops.splash_forward(Q, K, V, qi, ki, ops.clamp_alpha(alpha), k_keep, sm_scale,
                                 with_support=False)
-    return out
+    return ops.from_kernel_layout(out, d, dtype)
 
 
 def backward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, dOut, k_keep: int = 8,
              grad_mode: str = "reference"):
     """Reference-compatible native backward (adasplashattention.cu:611-700):
     reruns the selection, then returns [dQ, dK, dV]."""
+    ops.check_shapes(Q, K, V)
+    if not isinstance(dOut, torch.Tensor) or dOut.shape != Q.shape:
+        raise ValueError(f"dOut shape {tuple(getattr(dOut, 'shape', ()))} must equal Q shape "
+                         f"{tuple(Q.shape)}")
+    d, dtype = Q.size(-1), Q.dtype
     Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     a = ops.clamp_alpha(alpha)
     out, st = ops.splash_forward(Q, K, V, qi, ki, a, k_keep, sm_scale)
-    dQ, dK, dV = ops.splash_backward(Q, K, V, qi, ki, out, dOut, st, a, k_keep, sm_scale,
-                                     grad_mode)
-    return [dQ, dK, dV]
+    grads = ops.splash_backward(Q, K, V, qi, ki, out, dOut, st, a, k_keep, sm_scale, grad_mode)
+    return [ops.from_kernel_layout(g, d, dtype) for g in grads]

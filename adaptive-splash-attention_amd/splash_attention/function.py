@@ -46,7 +46,8 @@ def splash_attention(Q, K, V, Q_idx=None, K_idx=None, alpha: float = 1.5, k_keep
                      sm_scale: float | None = None, grad_mode: str = "entmax") -> torch.Tensor:
     """Block-sparse alpha-entmax attention, differentiable in Q, K and V.
 
-    Q: [B, H, NQ, d]; K, V: [B, H, NK, d]; float32 or bfloat16 on one GPU.
+    Q: [B, H, NQ, d]; K, V: [B, H, NK, d], d <= 128; float32, bfloat16 or
+    float16 (computed in float32) on one GPU.
     Q_idx: [B*H, NQ] and K_idx: [B*H, NK] integer positions (None: arange);
     key j is visible to query i iff K_idx[j] <= Q_idx[i].
     grad_mode "entmax" (default) uses the alpha-entmax Jacobian; "reference"
@@ -56,9 +57,12 @@ def splash_attention(Q, K, V, Q_idx=None, K_idx=None, alpha: float = 1.5, k_keep
         raise ValueError(f"grad_mode must be one of {sorted(ops.GRAD_MODES)}")
     if torch.compiler.is_compiling():
         return library.attention(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode)
-    # eager: the autograd function, without the custom-operator dispatch
-    Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
+    # eager: the autograd function, without the custom-operator dispatch;
+    # check_inputs' padding and widening are differentiable torch ops
+    d, dtype = Q.size(-1), Q.dtype
     if sm_scale is None:
-        sm_scale = Q.size(-1) ** -0.5
-    return SplashAttentionFunction.apply(Q, K, V, qi, ki, float(alpha), int(k_keep),
-                                         float(sm_scale), grad_mode)
+        sm_scale = d ** -0.5
+    Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
+    out = SplashAttentionFunction.apply(Q, K, V, qi, ki, float(alpha), int(k_keep),
+                                        float(sm_scale), grad_mode)
+    return ops.from_kernel_layout(out, d, dtype)

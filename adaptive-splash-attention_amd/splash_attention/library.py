@@ -34,7 +34,9 @@ def forward_op(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx: 
                alpha: float, k_keep: int, sm_scale: float, grad_mode: str
                ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """out, taus, norms, mask, q_ptr, q_list, k_ptr, k_list and the support
-    masks sup_mask (grad_mode is recorded for the backward only)."""
+    masks sup_mask (grad_mode is recorded for the backward only).  out is in
+    the kernels' layout (ops.to_kernel_layout: head dimension 64 or 128,
+    float16 as float32), so that the backward sees the unrounded output."""
     q, k, v, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     out, st = ops.splash_forward(q, k, v, qi, ki, alpha, k_keep, sm_scale, with_support=True)
     return (out, *st.tensors())
@@ -48,7 +50,8 @@ def _forward_fake(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode):
     nQB, nKB = _nblocks(NQ, ops.BLOCK_M), _nblocks(NK, ops.BLOCK_N)
     f32 = dict(dtype=torch.float32, device=Q.device)
     i32 = dict(dtype=torch.int32, device=Q.device)
-    return (torch.empty_like(Q, memory_format=torch.contiguous_format),
+    odt = torch.float32 if Q.dtype == torch.float16 else Q.dtype
+    return (torch.empty((B, H, NQ, ops.kernel_head_dim(d)), dtype=odt, device=Q.device),
             torch.empty((BH, NQ), **f32), torch.empty((BH, NQ), **f32),
             torch.empty((BH, nQB, nKB), dtype=torch.uint8, device=Q.device),
             torch.empty((BH, nQB + 1), **i32), torch.empty((BH, nQB * nKB), **i32),
@@ -65,7 +68,8 @@ def backward_op(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx:
     """dQ, dK, dV from the state a matching forward_op returned."""
     q, k, v, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     st = ops.SplashState.from_tensors((taus, norms, mask, q_ptr, q_list, k_ptr, k_list, sup_mask))
-    return ops.splash_backward(q, k, v, qi, ki, out, dout, st, alpha, k_keep, sm_scale, grad_mode)
+    grads = ops.splash_backward(q, k, v, qi, ki, out, dout, st, alpha, k_keep, sm_scale, grad_mode)
+    return tuple(ops.from_kernel_layout(g, t.size(-1), t.dtype) for g, t in zip(grads, (Q, K, V)))
 
 
 @backward_op.register_fake
@@ -96,9 +100,11 @@ forward_op.register_autograd(_backward, setup_context=_setup_context)
 
 def attention(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx: Optional[Tensor],
               alpha: float, k_keep: int, sm_scale: Optional[float], grad_mode: str) -> Tensor:
-    """Shape-checked call of ``adasplash::forward``; returns the output."""
+    """Shape-checked call of ``adasplash::forward``; returns the output in
+    the caller's head dimension and dtype."""
     ops.check_shapes(Q, K, V, k_keep)
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(Q.size(-1))
-    return forward_op(Q, K, V, Q_idx, K_idx, float(alpha), int(k_keep), float(sm_scale),
-                      grad_mode)[0]
+    out = forward_op(Q, K, V, Q_idx, K_idx, float(alpha), int(k_keep), float(sm_scale),
+                     grad_mode)[0]
+    return ops.from_kernel_layout(out, Q.size(-1), Q.dtype)

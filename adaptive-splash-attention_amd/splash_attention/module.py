@@ -12,7 +12,8 @@ class AdaptiveSplashAttention(nn.Module):
     """Block-sparse alpha-entmax attention.
 
     Args follow README.md:105-111 of the reference:
-      head_dim: last dimension of Q, K, V (64 or 128).
+      head_dim: last dimension of Q, K, V (1..128, as the reference's
+        D_MAX; the kernels run at 64 or 128 with zero-padded columns).
       alpha: entmax parameter, clamped to [1.05, 3] as the reference does.
       k_keep: top-k kept per query row (1..128).
       adaptive_threshold: accepted for compatibility.  The reference
@@ -24,15 +25,16 @@ class AdaptiveSplashAttention(nn.Module):
 
     forward(Q, K, V, Q_idx=None, K_idx=None): Q [B, H, NQ, d], K and V
     [B, H, NK, d]; Q_idx [B*H, NQ], K_idx [B*H, NK] positions (default
-    arange, i.e. causal).  Returns [B, H, NQ, d] in the input dtype.
+    arange, i.e. causal).  float32, bfloat16 or float16 (computed in
+    float32).  Returns [B, H, NQ, d] in the input dtype.
     """
 
     def __init__(self, head_dim: int = 64, alpha: float = 1.5, k_keep: int = 8,
                  adaptive_threshold: bool = True, sm_scale: float | None = None,
                  grad_mode: str = "entmax"):
         super().__init__()
-        if head_dim not in (64, 128):
-            raise ValueError(f"head_dim {head_dim} not supported (64 or 128)")
+        if not 1 <= int(head_dim) <= 128:
+            raise ValueError(f"head_dim {head_dim} out of range [1, 128]")
         if not 1 <= int(k_keep) <= 128:
             raise ValueError(f"k_keep {k_keep} out of range [1, 128]")
         if grad_mode not in ("entmax", "reference"):

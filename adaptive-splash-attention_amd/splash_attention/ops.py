@@ -12,6 +12,7 @@ import math
 from dataclasses import dataclass
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib
 
@@ -19,8 +20,12 @@ BLOCK_M = 64
 BLOCK_N = 64
 MAX_HEAD_DIM = 128
 MAX_K_KEEP = 128
+KERNEL_HEAD_DIMS = (64, 128)
 
+# dtypes the kernels compute in
 _DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
+# dtypes the Python entry points accept (float16 runs on the float32 kernels)
+INPUT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 GRAD_MODES = {"entmax": _lib.GRAD_ENTMAX, "reference": _lib.GRAD_REFERENCE}
 
@@ -109,8 +114,9 @@ def check_shapes(Q, K, V, k_keep=None):
             raise ValueError(f"{name} must be 4-D [B, H, N, d], got shape {tuple(t.shape)}")
     if Q.size(3) > MAX_HEAD_DIM:
         raise ValueError("Head dimension too large; increase D_MAX")
-    if Q.dtype not in _DTYPES:
-        raise TypeError(f"unsupported dtype {Q.dtype}; use torch.float32 or torch.bfloat16")
+    if Q.dtype not in INPUT_DTYPES:
+        raise TypeError(f"unsupported dtype {Q.dtype}; use torch.float32, torch.bfloat16 "
+                        "or torch.float16")
     if K.dtype != Q.dtype or V.dtype != Q.dtype:
         raise TypeError("Q, K and V must have the same dtype")
     B, H, NQ, d = Q.shape
@@ -118,8 +124,8 @@ def check_shapes(Q, K, V, k_keep=None):
         raise ValueError(f"K shape {tuple(K.shape)} does not match Q shape {tuple(Q.shape)}")
     if V.shape != K.shape:
         raise ValueError(f"V shape {tuple(V.shape)} must equal K shape {tuple(K.shape)}")
-    if d not in (64, 128):
-        raise ValueError(f"head dimension {d} not supported (64 or 128)")
+    if d < 1:
+        raise ValueError("head dimension must be at least 1")
     NK = K.shape[2]
     if NQ < 1 or NK < 1 or B < 1 or H < 1:
         raise ValueError("empty attention problem")
@@ -132,14 +138,52 @@ def check_shapes(Q, K, V, k_keep=None):
 
 
 def check_inputs(Q, K, V, Q_idx=None, K_idx=None):
-    """Validate and normalise (Q, K, V, Q_idx, K_idx); returns contiguous tensors."""
+    """Validate and normalise (Q, K, V, Q_idx, K_idx); returns contiguous
+    tensors in the kernels' layout (see to_kernel_layout)."""
     check_shapes(Q, K, V)
     B, H, NQ, _ = Q.shape
     NK = K.shape[2]
     BH = B * H
     qi = _index(Q_idx, BH, NQ, B, H, Q.device, "Q_idx")
     ki = _index(K_idx, BH, NK, B, H, Q.device, "K_idx")
+    Q, K, V = to_kernel_layout(Q, K, V)
     return _aligned(Q), _aligned(K), _aligned(V), qi, ki
+
+
+def kernel_head_dim(d: int) -> int:
+    """The kernel head dimension a head dimension d <= 128 runs at."""
+    return KERNEL_HEAD_DIMS[0] if d <= KERNEL_HEAD_DIMS[0] else KERNEL_HEAD_DIMS[1]
+
+
+def to_kernel_layout(*ts):
+    """Tensors [..., d] as the kernels take them: the head dimension
+    zero-padded to 64 or 128, float16 widened to float32.
+
+    The reference accepts any d <= 128 (adasplashattention.cu:542); the
+    kernels are built for d = 64 and 128.  Zero columns add exact zeros to
+    every dot product, so scores, weights and tau are those of the unpadded
+    problem, and the padded columns of the outputs and of dQ, dK, dV are
+    zero.  float16 -> float32 is exact.  Both steps are differentiable
+    torch ops: gradients reach the caller's tensors through them.
+    """
+    dk = kernel_head_dim(ts[0].size(-1))
+    out = []
+    for t in ts:
+        if t.dtype == torch.float16:
+            t = t.float()
+        if t.size(-1) != dk:
+            t = F.pad(t, (0, dk - t.size(-1)))
+        out.append(t)
+    return out
+
+
+def from_kernel_layout(t: torch.Tensor, d: int, dtype: torch.dtype) -> torch.Tensor:
+    """Undo to_kernel_layout on an output: first d columns, caller's dtype."""
+    if t.size(-1) != d:
+        t = t[..., :d]
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    return t
 
 
 def _aligned(t: torch.Tensor) -> torch.Tensor:
@@ -209,6 +253,17 @@ def splash_forward(Q, K, V, Q_idx, K_idx, alpha: float, k_keep: int, sm_scale=No
     return out, st
 
 
+def _as_kernel_operand(t: torch.Tensor, Q: torch.Tensor, name: str) -> torch.Tensor:
+    """A [B, H, NQ, d'] operand of the backward (dOut, Out) in the layout of
+    the kernel-layout Q: padded to Q's head dimension, in Q's dtype."""
+    dq = Q.size(-1)
+    if (t.dim() != 4 or tuple(t.shape[:3]) != tuple(Q.shape[:3]) or t.size(-1) > dq
+            or kernel_head_dim(t.size(-1)) != dq):
+        raise ValueError(f"{name} shape {tuple(t.shape)} must equal Q shape {tuple(Q.shape)}")
+    (t,) = to_kernel_layout(t)
+    return _aligned(t.to(Q.dtype))
+
+
 def splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st: SplashState, alpha: float,
                     k_keep: int, sm_scale=None, grad_mode: str = "entmax"):
     """Gradients (dQ, dK, dV) from a forward's state."""
@@ -217,9 +272,9 @@ def splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st: SplashState, alpha: fl
         raise ValueError(f"grad_mode must be one of {sorted(GRAD_MODES)}")
     B, H, NQ, d = Q.shape
     p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale)
-    if dout.shape != Q.shape:
-        raise ValueError(f"dOut shape {tuple(dout.shape)} must equal Q shape {tuple(Q.shape)}")
-    dout = _aligned(dout.to(Q.dtype))
+    dout = _as_kernel_operand(dout, Q, "dOut")
+    if out is not None:
+        out = _as_kernel_operand(out, Q, "Out")
     ws = workspace(p, Q.device)
     dQ = torch.empty_like(Q)
     dK = torch.empty_like(K)

@@ -19,7 +19,8 @@ def test_module_mirrors_readme_signature():
     assert sa.AdaptiveSplashAttention(head_dim=128).sm_scale == pytest.approx(128 ** -0.5)
 
 
-@pytest.mark.parametrize("kw", [dict(head_dim=96), dict(k_keep=0), dict(k_keep=200),
+@pytest.mark.parametrize("kw", [dict(head_dim=0), dict(head_dim=129), dict(k_keep=0),
+                                dict(k_keep=200),
                                 dict(grad_mode="exact")])
 def test_module_rejects_bad_config(kw):
     with pytest.raises(ValueError):
@@ -42,9 +43,10 @@ def test_cpu_tensors_are_rejected_like_the_reference():
     (_t(1, 2, 8), _t(1, 2, 8, 64), _t(1, 2, 8, 64), ValueError),
     (_t(1, 2, 8, 64), _t(1, 3, 8, 64), _t(1, 3, 8, 64), ValueError),
     (_t(1, 2, 8, 64), _t(1, 2, 8, 64), _t(1, 2, 9, 64), ValueError),
-    (_t(1, 2, 8, 32), _t(1, 2, 8, 32), _t(1, 2, 8, 32), ValueError),
-    (_t(1, 2, 8, 64, dtype=torch.float16), _t(1, 2, 8, 64, dtype=torch.float16),
-     _t(1, 2, 8, 64, dtype=torch.float16), TypeError),
+    (_t(1, 2, 8, 0), _t(1, 2, 8, 0), _t(1, 2, 8, 0), ValueError),
+    (_t(1, 2, 8, 64, dtype=torch.float64), _t(1, 2, 8, 64, dtype=torch.float64),
+     _t(1, 2, 8, 64, dtype=torch.float64), TypeError),
+    (_t(1, 2, 8, 64, dtype=torch.float16), _t(1, 2, 8, 64), _t(1, 2, 8, 64), TypeError),
     (_t(1, 2, 8, 64), _t(1, 2, 8, 64, dtype=torch.bfloat16), _t(1, 2, 8, 64), TypeError),
 ])
 def test_shape_and_dtype_validation(Q, K, V, err):
@@ -87,3 +89,25 @@ def test_grad_mode_validation():
     with pytest.raises(ValueError):
         sa.splash_attention(_t(1, 1, 8, 64), _t(1, 1, 8, 64), _t(1, 1, 8, 64),
                             grad_mode="bogus")
+
+
+@pytest.mark.parametrize("d,dk", [(1, 64), (40, 64), (64, 64), (65, 128), (100, 128), (128, 128)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_kernel_layout_pads_and_widens(d, dk, dtype):
+    """Any head dimension <= 128 runs at 64 or 128 with zero columns (scores
+    unchanged), float16 as float32 (exact); gradients flow back through both."""
+    g = torch.Generator().manual_seed(3)
+    Q = torch.randn(1, 2, 5, d, generator=g).to(dtype).requires_grad_()
+    K = torch.randn(1, 2, 7, d, generator=g).to(dtype)
+    q, k = ops.to_kernel_layout(Q, K)
+    assert q.shape == (1, 2, 5, dk) and k.shape == (1, 2, 7, dk)
+    assert q.dtype == (torch.float32 if dtype == torch.float16 else dtype)
+    assert torch.count_nonzero(q[..., d:]) == 0
+    assert torch.equal(q[..., :d].to(dtype), Q.detach())
+    s_pad = q.double() @ k.double().transpose(-1, -2)
+    s = Q.detach().double() @ K.double().transpose(-1, -2)
+    assert torch.equal(s_pad, s)
+    back = ops.from_kernel_layout(q * 2, d, dtype)
+    assert back.shape == Q.shape and back.dtype == dtype
+    back.sum().backward()
+    assert torch.equal(Q.grad, torch.full_like(Q, 2))

@@ -11,21 +11,23 @@ from tests._util import causal_idx, make_inputs
 pytestmark = pytest.mark.gpu
 
 
-def test_opcheck_forward(dev):
-    print("[lib] opcheck forward fp32 1x2x128x64", flush=True)
-    Q, K, V, _ = make_inputs(1, 2, 128, 128, 64, seed=11)
+@pytest.mark.parametrize("d,dtype", [(64, torch.float32), (40, torch.float16)])
+def test_opcheck_forward(dev, d, dtype):
+    print(f"[lib] opcheck forward {dtype} 1x2x128x{d}", flush=True)
+    Q, K, V, _ = make_inputs(1, 2, 128, 128, d, seed=11, dtype=dtype)
     args = (Q.to(dev), K.to(dev), V.to(dev), None, None, 1.5, 8, 0.125, "entmax")
     torch.library.opcheck(library.forward_op, args,
                           test_utils=("test_schema", "test_faketensor"))
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_compile_matches_eager(dev, dtype):
-    print(f"[lib] torch.compile aot_eager {dtype}", flush=True)
-    B, H, N, d = 1, 2, 192, 64
+@pytest.mark.parametrize("dtype,d", [(torch.float32, 64), (torch.bfloat16, 64),
+                                     (torch.float16, 40)])
+def test_compile_matches_eager(dev, dtype, d):
+    print(f"[lib] torch.compile aot_eager {dtype} d={d}", flush=True)
+    B, H, N = 1, 2, 192
     Q, K, V, dO = make_inputs(B, H, N, N, d, seed=12, dtype=dtype)
     idx = causal_idx(B * H, N).to(dev)
-    attn = sa.AdaptiveSplashAttention(head_dim=64, alpha=1.5, k_keep=16, sm_scale=0.125)
+    attn = sa.AdaptiveSplashAttention(head_dim=d, alpha=1.5, k_keep=16, sm_scale=0.125)
 
     def run(fn):
         q, k, v = (t.to(dev).requires_grad_(True) for t in (Q, K, V))
