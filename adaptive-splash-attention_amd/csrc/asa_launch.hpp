@@ -110,6 +110,11 @@ size_t select_lds_bytes(const Dims& d, bool bf16, bool from_scores, int cap);
 int select_capacity(const Dims& d, bool bf16, bool from_scores, size_t max_lds);
 hipError_t launch_bounds(const SelectParams& p, hipStream_t s);
 hipError_t launch_tau(const SelectParams& p, hipStream_t s);
+// Exact-threshold pass (tau mode "exact"): after launch_tau, before
+// compaction; reads tkv and kbounds, rewrites taus and ORs blocks into mask.
+hipError_t launch_refine(const SelectParams& p, bool bf16, hipStream_t s);
+// LDS bytes of one refine block.
+size_t refine_lds_bytes(const Dims& d, bool bf16);
 hipError_t launch_compact(const CompactParams& p, hipStream_t s);
 hipError_t launch_forward(const ForwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_delta(const BackwardParams& p, bool bf16, hipStream_t s);

@@ -65,6 +65,37 @@ struct Stager {
   }
 };
 
+// K tile of 64 keys in LDS, in the attention passes' tile layout (padded
+// row stride, swizzled 16-byte chunks: Tile<T, D>), filled by all NT
+// threads in 16-byte chunks (consecutive threads, consecutive chunks of a
+// row: coalesced global reads).  The scores are formed by rows_x_frag, the
+// attention passes' score product with the same operands and accumulation
+// order, so every pass sees bit-identical scores.
+template <typename T, int D, int NT = 256> struct KStage {
+  static constexpr int kRs = Tile<T, D>::kRs;                   // elements per LDS row
+  static constexpr int kRowChunks = D * int(sizeof(T)) / 16;    // 16-byte chunks per row
+  static constexpr int kPerThread = kBlock * kRowChunks / NT;
+  static_assert(kBlock * kRowChunks % NT == 0, "tile chunks must divide the block");
+  uint4 r[kPerThread];
+  // rows >= NK read as zero (such keys are never visible)
+  __device__ __forceinline__ void load(const T* Kb, int kbase, int NK, int t) {
+    for (int j = 0; j < kPerThread; ++j) {
+      const int ch = t + j * NT, row = ch / kRowChunks;
+      const int col = (ch % kRowChunks) * (16 / int(sizeof(T)));
+      r[j] = kbase + row < NK
+                 ? *reinterpret_cast<const uint4*>(Kb + size_t(kbase + row) * D + col)
+                 : uint4{0u, 0u, 0u, 0u};
+    }
+  }
+  __device__ __forceinline__ void store(T* buf, int t) const {
+    for (int j = 0; j < kPerThread; ++j) {
+      const int ch = t + j * NT, row = ch / kRowChunks;
+      const int col = (ch % kRowChunks) * (16 / int(sizeof(T)));
+      *reinterpret_cast<uint4*>(buf + row * kRs + (col ^ Tile<T, D>::sw(row))) = r[j];
+    }
+  }
+};
+
 // Positions of the 64 keys (or queries) of a tile, staged beside it by the
 // first wave, with a flag telling whether the whole tile passes a block-wide
 // visibility test (then the per-element checks can be skipped).

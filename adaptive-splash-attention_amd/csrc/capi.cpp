@@ -46,6 +46,7 @@ int check_hip(hipError_t e, const char* what) {
 struct Shape {
   int BH, NQ, NK, D, k, nQB, nKB;
   bool bf16;
+  bool exact;  // ASA_TAU_EXACT
   float alpha, scale;
 };
 
@@ -69,6 +70,8 @@ int validate(const asa_problem* p, Shape* sh) {
                 p->block_m, p->block_n);
   if (p->dtype != ASA_DTYPE_F32 && p->dtype != ASA_DTYPE_BF16)
     return fail(ASA_ERR_INVALID_ARGUMENT, "unknown dtype %d", p->dtype);
+  if (p->tau_mode != ASA_TAU_REFERENCE && p->tau_mode != ASA_TAU_EXACT)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "unknown tau_mode %d", p->tau_mode);
   if (!std::isfinite(p->alpha)) return fail(ASA_ERR_INVALID_ARGUMENT, "alpha is not finite");
   if (!std::isfinite(p->sm_scale)) return fail(ASA_ERR_INVALID_ARGUMENT, "sm_scale is not finite");
   const long long bh = (long long)p->batch * p->heads;
@@ -84,6 +87,7 @@ int validate(const asa_problem* p, Shape* sh) {
   sh->nQB = int(nqb);
   sh->nKB = int(nkb);
   sh->bf16 = p->dtype == ASA_DTYPE_BF16;
+  sh->exact = p->tau_mode == ASA_TAU_EXACT;
   // alpha is clamped to [1.05, 3] as the reference does (adasplashattention.cu:547).
   sh->alpha = std::fmax(1.05f, std::fmin(p->alpha, 3.0f));
   sh->scale = p->sm_scale;
@@ -204,6 +208,23 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
   e = asa::launch_tau(sp, s);
   asa::profile_end(s);
   if (int rc = check_hip(e, "tau kernel launch")) return rc;
+  if (sh.exact) {
+    // exact threshold over the whole row; adds the support's key blocks
+    int dev = 0, max_lds = 0;
+    if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (int rc = check_hip(hipDeviceGetAttribute(&max_lds,
+                                                 hipDeviceAttributeMaxSharedMemoryPerBlock, dev),
+                           "hipDeviceGetAttribute"))
+      return rc;
+    const size_t need = asa::refine_lds_bytes(sp.d, sh.bf16);
+    if (need > size_t(max_lds))
+      return fail(ASA_ERR_UNSUPPORTED, "exact tau mode needs %zu bytes of LDS per block, device has %d",
+                  need, max_lds);
+    asa::profile_begin("refine", s);
+    e = asa::launch_refine(sp, sh.bf16, s);
+    asa::profile_end(s);
+    if (int rc = check_hip(e, "refine kernel launch")) return rc;
+  }
 
   asa::CompactParams cp{sh.BH, sh.nQB, sh.nKB, st->mask, st->q_ptr, st->q_list, st->k_ptr,
                         st->k_list};
@@ -373,6 +394,8 @@ int asa_select_from_scores(const asa_problem* p, const float* scores, const int3
                            void* stream) {
   Shape sh;
   if (int rc = validate(p, &sh)) return rc;
+  if (sh.exact)
+    return fail(ASA_ERR_UNSUPPORTED, "exact tau mode needs Q and K (asa_forward)");
   if (!scores || !q_idx || !k_idx)
     return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
   if (int rc = check_state(st, false)) return rc;

@@ -38,6 +38,7 @@
 
 #include "asa_device.hpp"
 #include "asa_launch.hpp"
+#include "asa_stage.hpp"
 #include "asa_tiles.hpp"
 
 namespace asa {
@@ -253,37 +254,6 @@ __device__ __forceinline__ float sweep_floor(float th, bool exact, float scale) 
   return f;
 }
 
-
-// K tile of 64 keys in LDS, in the attention passes' tile layout (padded
-// row stride, swizzled 16-byte chunks: Tile<T, D>), filled by all 256
-// threads in 16-byte chunks (consecutive threads, consecutive chunks of a
-// row: coalesced global reads).  The scores are formed by rows_x_frag, the
-// attention passes' score product with the same operands and accumulation
-// order, so every pass sees bit-identical scores.
-template <typename T, int D> struct KStage {
-  static constexpr int kRs = Tile<T, D>::kRs;                   // elements per LDS row
-  static constexpr int kRowChunks = D * int(sizeof(T)) / 16;    // 16-byte chunks per row
-  static constexpr int kPerThread = kBlock * kRowChunks / kThreads;
-  static_assert(kBlock * kRowChunks % kThreads == 0, "tile chunks must divide the block");
-  uint4 r[kPerThread];
-  // rows >= NK read as zero (such keys are never visible)
-  __device__ __forceinline__ void load(const T* Kb, int kbase, int NK, int t) {
-    for (int j = 0; j < kPerThread; ++j) {
-      const int ch = t + j * kThreads, row = ch / kRowChunks;
-      const int col = (ch % kRowChunks) * (16 / int(sizeof(T)));
-      r[j] = kbase + row < NK
-                 ? *reinterpret_cast<const uint4*>(Kb + size_t(kbase + row) * D + col)
-                 : uint4{0u, 0u, 0u, 0u};
-    }
-  }
-  __device__ __forceinline__ void store(T* buf, int t) const {
-    for (int j = 0; j < kPerThread; ++j) {
-      const int ch = t + j * kThreads, row = ch / kRowChunks;
-      const int col = (ch % kRowChunks) * (16 / int(sizeof(T)));
-      *reinterpret_cast<uint4*>(buf + row * kRs + (col ^ Tile<T, D>::sw(row))) = r[j];
-    }
-  }
-};
 
 // acc[b >> 2][b & 3] for a per-lane index b in [0, 16): a select tree on
 // the index bits instead of a dynamically indexed register array.

@@ -20,7 +20,8 @@ BUILD = os.path.join(ROOT, "_build")
 LIBDIR = os.path.join(PKG_DIR, "lib")
 LIB = os.path.join(LIBDIR, "libadasplash.so")
 
-SOURCES = ["select.hip", "compact.hip", "forward.hip", "backward.hip", "sparse_bwd.hip", "capi.cpp"]
+SOURCES = ["select.hip", "exact.hip", "compact.hip", "forward.hip", "backward.hip", "sparse_bwd.hip",
+           "capi.cpp"]
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}",

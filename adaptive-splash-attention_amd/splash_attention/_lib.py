@@ -12,7 +12,7 @@ import threading
 
 from . import _build
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 ASA_OK = 0
 ASA_ERR_INVALID_ARGUMENT = 1
@@ -22,6 +22,8 @@ ASA_ERR_DEVICE = 3
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
+TAU_REFERENCE = 0
+TAU_EXACT = 1
 GRAD_ENTMAX = 0
 GRAD_REFERENCE = 1
 
@@ -51,6 +53,7 @@ class Problem(ctypes.Structure):
         ("alpha", ctypes.c_float),
         ("sm_scale", ctypes.c_float),
         ("dtype", ctypes.c_int32),
+        ("tau_mode", ctypes.c_int32),
     ]
 
 

@@ -31,19 +31,22 @@ def _nblocks(n: int, b: int) -> int:
 
 @torch.library.custom_op(f"{_NS}::forward", mutates_args=(), device_types="cuda")
 def forward_op(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx: Optional[Tensor],
-               alpha: float, k_keep: int, sm_scale: float, grad_mode: str
+               alpha: float, k_keep: int, sm_scale: float, grad_mode: str,
+               tau_mode: str = "reference"
                ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """out, taus, norms, mask, q_ptr, q_list, k_ptr, k_list and the support
     masks sup_mask (grad_mode is recorded for the backward only).  out is in
     the kernels' layout (ops.to_kernel_layout: head dimension 64 or 128,
     float16 as float32), so that the backward sees the unrounded output."""
     q, k, v, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
-    out, st = ops.splash_forward(q, k, v, qi, ki, alpha, k_keep, sm_scale, with_support=True)
+    out, st = ops.splash_forward(q, k, v, qi, ki, alpha, k_keep, sm_scale, with_support=True,
+                                 tau_mode=tau_mode)
     return (out, *st.tensors())
 
 
 @forward_op.register_fake
-def _forward_fake(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode):
+def _forward_fake(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode,
+                  tau_mode="reference"):
     B, H, NQ, d = Q.shape
     NK = K.shape[2]
     BH = B * H
@@ -81,7 +84,7 @@ def _backward_fake(Q, K, V, Q_idx, K_idx, out, dout, taus, norms, mask, q_ptr, q
 
 
 def _setup_context(ctx, inputs, output):
-    Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode = inputs
+    Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode, tau_mode = inputs
     out, *state = output
     ctx.params = (alpha, k_keep, sm_scale, grad_mode)
     ctx.save_for_backward(Q, K, V, Q_idx, K_idx, out, *state)
@@ -92,19 +95,20 @@ def _backward(ctx, dout, *unused_state_grads):
     alpha, k_keep, sm_scale, grad_mode = ctx.params
     dQ, dK, dV = backward_op(Q, K, V, Q_idx, K_idx, out, dout.contiguous(), *state, alpha, k_keep,
                              sm_scale, grad_mode)
-    return dQ, dK, dV, None, None, None, None, None, None
+    return dQ, dK, dV, None, None, None, None, None, None, None
 
 
 forward_op.register_autograd(_backward, setup_context=_setup_context)
 
 
 def attention(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx: Optional[Tensor],
-              alpha: float, k_keep: int, sm_scale: Optional[float], grad_mode: str) -> Tensor:
+              alpha: float, k_keep: int, sm_scale: Optional[float], grad_mode: str,
+              tau_mode: str = "reference") -> Tensor:
     """Shape-checked call of ``adasplash::forward``; returns the output in
     the caller's head dimension and dtype."""
     ops.check_shapes(Q, K, V, k_keep)
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(Q.size(-1))
     out = forward_op(Q, K, V, Q_idx, K_idx, float(alpha), int(k_keep), float(sm_scale),
-                     grad_mode)[0]
+                     grad_mode, tau_mode)[0]
     return ops.from_kernel_layout(out, Q.size(-1), Q.dtype)

@@ -28,6 +28,9 @@ _DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
 INPUT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 GRAD_MODES = {"entmax": _lib.GRAD_ENTMAX, "reference": _lib.GRAD_REFERENCE}
+# "reference": the reference's top-k threshold; "exact": the alpha-entmax
+# threshold over the whole visible row (asa_tau_mode in adasplash.h)
+TAU_MODES = {"reference": _lib.TAU_REFERENCE, "exact": _lib.TAU_EXACT}
 
 
 @dataclass
@@ -194,13 +197,21 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
-def make_problem(B, H, NQ, NK, d, dtype, alpha, k_keep, sm_scale) -> _lib.Problem:
+def check_tau_mode(tau_mode: str) -> int:
+    if tau_mode not in TAU_MODES:
+        raise ValueError(f"tau_mode must be one of {sorted(TAU_MODES)}")
+    return TAU_MODES[tau_mode]
+
+
+def make_problem(B, H, NQ, NK, d, dtype, alpha, k_keep, sm_scale,
+                 tau_mode: str = "reference") -> _lib.Problem:
     if not (1 <= int(k_keep) <= MAX_K_KEEP):
         raise ValueError(f"k_keep {k_keep} out of range [1, {MAX_K_KEEP}]")
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(d)
     return _lib.Problem(B, H, NQ, NK, d, int(k_keep), BLOCK_M, BLOCK_N, float(alpha),
-                        float(sm_scale), _DTYPES[dtype] if isinstance(dtype, torch.dtype) else dtype)
+                        float(sm_scale), _DTYPES[dtype] if isinstance(dtype, torch.dtype) else dtype,
+                        check_tau_mode(tau_mode))
 
 
 def alloc_state(p: _lib.Problem, device, with_topk: bool = False,
@@ -234,13 +245,15 @@ def workspace(p: _lib.Problem, device) -> torch.Tensor:
 
 
 def splash_forward(Q, K, V, Q_idx, K_idx, alpha: float, k_keep: int, sm_scale=None,
-                   with_topk: bool = False, with_support: bool = True):
+                   with_topk: bool = False, with_support: bool = True,
+                   tau_mode: str = "reference"):
     """Forward pass; returns (out, SplashState).  Inputs as check_inputs() returns them.
     with_support records the rows' support masks for the sparse backward
-    (skip it for inference)."""
+    (skip it for inference).  tau_mode "exact" solves tau over the whole
+    visible row instead of the top-k (see TAU_MODES)."""
     lib = _lib.load()
     B, H, NQ, d = Q.shape
-    p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale)
+    p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale, tau_mode)
     st = alloc_state(p, Q.device, with_topk, with_support)
     out = torch.empty_like(Q)
     ws = workspace(p, Q.device)

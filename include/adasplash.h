@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define ASA_ABI_VERSION 2
+#define ASA_ABI_VERSION 3
 
 typedef enum asa_status {
   ASA_OK = 0,
@@ -56,6 +56,20 @@ typedef enum asa_status {
 } asa_status;
 
 typedef enum asa_dtype { ASA_DTYPE_F32 = 0, ASA_DTYPE_BF16 = 1 } asa_dtype;
+
+typedef enum asa_tau_mode {
+  /* The reference's threshold: its 5-step recurrence on the row's top-k
+   * scores (adasplashattention.cu:51-125); block mask = union of the rows'
+   * top-k key blocks (:210-216).                                          */
+  ASA_TAU_REFERENCE = 0,
+  /* The alpha-entmax threshold over every visible key of the row (dense
+   * alpha-entmax), found by safeguarded Newton steps started from the
+   * top-k root; key blocks holding a key with u > 0 at that threshold are
+   * added to the mask, so the forward weights the exact alpha-entmax
+   * support.  No reference counterpart (the reference has only the top-k
+   * threshold); asa_forward only.                                         */
+  ASA_TAU_EXACT = 1
+} asa_tau_mode;
 
 typedef enum asa_grad_mode {
   /* ds = g (dp - sum(g dp)/sum(g)), g = P^(2-alpha): the alpha-entmax
@@ -83,6 +97,7 @@ typedef struct asa_problem {
   float alpha;      /* clamped to [1.05, 3]                               */
   float sm_scale;
   int32_t dtype;    /* asa_dtype of Q, K, V, Out, dOut, dQ, dK, dV        */
+  int32_t tau_mode; /* asa_tau_mode (asa_forward; ignored by asa_backward) */
 } asa_problem;
 
 /* Per-call selection state written by asa_forward (and by

@@ -99,7 +99,8 @@ def attention_backward(Q, K, V, P, dO, alpha: float, sm_scale: float):
     V = np.asarray(V, np.float64)
     dO = np.asarray(dO, np.float64)
     dP = np.einsum("bid,bjd->bij", dO, V)
-    g = np.where(P > 0, P, 0.0) ** (2.0 - alpha) * (P > 0)
+    # P^(2-alpha) on the support only (for alpha > 2, 0^(2-alpha) is inf)
+    g = np.where(P > 0, np.where(P > 0, P, 1.0) ** (2.0 - alpha), 0.0)
     sg = g.sum(-1, keepdims=True)
     shift = np.where(sg > 0, (g * dP).sum(-1, keepdims=True) / np.where(sg > 0, sg, 1.0), 0.0)
     dS = g * (dP - shift)

@@ -73,6 +73,7 @@ def test_query_sizes_headline():
     (dict(dtype=7), 1, "dtype"),
     (dict(alpha=float("nan")), 1, "alpha"),
     (dict(sm_scale=float("inf")), 1, "sm_scale"),
+    (dict(tau_mode=5), 1, "tau_mode"),
 ])
 def test_invalid_problems_are_rejected_on_the_host(lib, bad, code, msg):
     from splash_attention import _lib
@@ -112,3 +113,16 @@ def test_error_string_is_cleared_on_success(lib):
     good = _problem()
     assert lib.asa_query_sizes(ctypes.byref(good), ctypes.byref(z)) == 0
     assert lib.asa_last_error().decode() == ""
+
+
+def test_exact_tau_mode_is_forward_only(lib):
+    from splash_attention import _lib
+
+    p = _problem(tau_mode=_lib.TAU_EXACT)
+    z = _lib.Sizes()
+    assert lib.asa_query_sizes(ctypes.byref(p), ctypes.byref(z)) == 0
+    st = _lib.State()
+    rc = lib.asa_select_from_scores(ctypes.byref(p), None, None, None, ctypes.byref(st), None,
+                                    None)
+    assert rc == _lib.ASA_ERR_UNSUPPORTED
+    assert "exact tau mode" in lib.asa_last_error().decode()
