@@ -38,6 +38,7 @@ struct SelectParams {
   float* tkv;             // workspace: sorted top-k values, [k][BH * NQ]
   int2* kbounds;          // workspace: (min, max) position per key block, [BH * nKB]
   int cap;                // candidate keys per row in LDS (select_capacity)
+  int lcap;               // refine pass: listed keys per row in LDS (refine_list_capacity)
 };
 
 struct CompactParams {
@@ -113,8 +114,11 @@ hipError_t launch_tau(const SelectParams& p, hipStream_t s);
 // Exact-threshold pass (tau mode "exact"): after launch_tau, before
 // compaction; reads tkv and kbounds, rewrites taus and ORs blocks into mask.
 hipError_t launch_refine(const SelectParams& p, bool bf16, hipStream_t s);
-// LDS bytes of one refine block.
-size_t refine_lds_bytes(const Dims& d, bool bf16);
+// LDS bytes of one refine block holding `lcap` listed keys per row.
+size_t refine_lds_bytes(const Dims& d, bool bf16, int lcap);
+// Listed keys per row that fit `max_lds` bytes (max(64, k + 32) at most;
+// 0: none fit, every row sweeps; -1: not even the sweep stage fits).
+int refine_list_capacity(const Dims& d, bool bf16, size_t max_lds);
 hipError_t launch_compact(const CompactParams& p, hipStream_t s);
 hipError_t launch_forward(const ForwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_delta(const BackwardParams& p, bool bf16, hipStream_t s);

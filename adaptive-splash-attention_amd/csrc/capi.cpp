@@ -216,10 +216,10 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
                                                  hipDeviceAttributeMaxSharedMemoryPerBlock, dev),
                            "hipDeviceGetAttribute"))
       return rc;
-    const size_t need = asa::refine_lds_bytes(sp.d, sh.bf16);
-    if (need > size_t(max_lds))
+    sp.lcap = asa::refine_list_capacity(sp.d, sh.bf16, size_t(max_lds));
+    if (sp.lcap < 0)
       return fail(ASA_ERR_UNSUPPORTED, "exact tau mode needs %zu bytes of LDS per block, device has %d",
-                  need, max_lds);
+                  asa::refine_lds_bytes(sp.d, sh.bf16, 0), max_lds);
     asa::profile_begin("refine", s);
     e = asa::launch_refine(sp, sh.bf16, s);
     asa::profile_end(s);

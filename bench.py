@@ -82,6 +82,10 @@ def kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep, nsup):
                        bytes=rows * d * ELEM + vis_blocks * tile + rows * k_keep * 4
                        + BH * nQB * nKB),
         "tau": dict(bound="hbm", flops=0.0, bytes=rows * k_keep * 4 + rows * 4),
+        # exact tau mode: FLOPs of ONE full-row sweep (the kernel sweeps a
+        # query block until its rows converge, a data-dependent count)
+        "refine": dict(bound="mfma", flops=2.0 * d * vis,
+                       bytes=rows * d * ELEM + vis_blocks * tile + rows * k_keep * 4),
         "bounds": dict(bound="hbm", flops=0.0, bytes=BH * N * 4 + BH * nKB * 8),
         "compact": dict(bound="hbm", flops=0.0, bytes=2 * BH * nQB * nKB + csr),
         "forward": dict(bound="hbm", flops=4.0 * 64 * 64 * d * nnzb,
@@ -195,6 +199,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--grad-mode", default="entmax", choices=["entmax", "reference"])
+    ap.add_argument("--tau-mode", default="reference", choices=["reference", "exact"],
+                    help="reference: the reference's top-k threshold (the headline); exact: "
+                         "the alpha-entmax threshold over the whole visible row")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -229,7 +236,8 @@ def main():
 
     def step():
         q.grad = k.grad = v.grad = None
-        out = sa.splash_attention(q, k, v, idx, idx, alpha, k_keep, scale, args.grad_mode)
+        out = sa.splash_attention(q, k, v, idx, idx, alpha, k_keep, scale, args.grad_mode,
+                                  args.tau_mode)
         out.backward(dO)
 
     for _ in range(args.warmup):
@@ -253,7 +261,8 @@ def main():
     kern = _lib.profile_read()
 
     # Block-mask density of this workload (same for every step: same inputs).
-    _, st = sa.ops.splash_forward(*sa.ops.check_inputs(Q, K, V, idx, idx), alpha, k_keep, scale)
+    _, st = sa.ops.splash_forward(*sa.ops.check_inputs(Q, K, V, idx, idx), alpha, k_keep, scale,
+                                  tau_mode=args.tau_mode)
     nnzb = int(st.mask.sum().item())
     nsup = support_pairs(st)
     nQB = nKB = N // 64
@@ -292,7 +301,8 @@ def main():
         "config": {"workload": "adaptive splash attention fwd+bwd (BASELINE configs[2])",
                    "B": B, "H": H, "N": N, "d": d, "alpha": alpha, "k_keep": k_keep,
                    "sm_scale": scale, "mask": "causal", "block": "64x64",
-                   "grad_mode": args.grad_mode, "parallelism": "single GPU",
+                   "grad_mode": args.grad_mode, "tau_mode": args.tau_mode,
+                   "parallelism": "single GPU",
                    "active_block_pairs": nnzb,
                    "support_pairs": nsup,
                    "active_block_density_of_causal": round(nnzb / (B * H * nQB * (nQB + 1) / 2), 4)},

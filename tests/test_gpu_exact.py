@@ -144,14 +144,28 @@ def test_exact_mode_clustered_noncausal():
 
 
 def test_exact_mode_adds_support_blocks():
-    """A few rows over a long non-causal key range with flat scores: the
-    supports span every key block while the rows' top-1 keys cover at most
-    8 of 32, so the refine pass must add the support's blocks to the mask."""
+    """A few rows over a long non-causal key range.  Rows 0-3 have flat
+    scores: their supports (hundreds of keys) span every key block and
+    overflow the per-row key lists of the refine pass's first sweep, so they
+    take further sweeps; rows 4-7 have sharp scores and finish on their
+    lists, in the same query block.  The rows' top-1 keys cover at most 8 of
+    32 key blocks, so the support's blocks must be added to the mask."""
     B, H, NQ, NK, d = 1, 2, 8, 2048, 64
     BH = B * H
+    Q, K, V, dO = make_inputs(B, H, NQ, NK, d, seed=11)
+    Q[:, :, 4:] *= 20.0
     qidx = torch.full((BH, NQ), NK - 1, dtype=torch.int32)
-    *_, extra = _run("few_rows_wide", B, H, NQ, NK, d, 1.25, 1, 0.02, torch.float32,
-                     qidx=qidx, kidx=causal_idx(BH, NK))
+    _, _, _, P, extra = _run("few_rows_wide", B, H, NQ, NK, d, 1.25, 1, 0.02, torch.float32,
+                             Q, K, V, dO, qidx=qidx, kidx=causal_idx(BH, NK))
+    sup = (P > 0).sum(-1)
+    assert (sup[:, :4] > 256).all() and (sup[:, 4:] > 1).all()
+    # keys listed by the first sweep (u > -1e-3 at the top-k root, which is
+    # z_max - 1 at k = 1), against the 64-key lists used at k = 1: head 0
+    # mixes overflowing rows (0-3) and listed rows (4-7) in one block
+    z = 0.25 * np.clip(np.einsum("bid,bjd->bij", np32(Q).astype(np.float64),
+                                 np32(K).astype(np.float64)) * 0.02, -10, 10)
+    listed = (z > z.max(-1, keepdims=True) - 1.0 - 1e-3).sum(-1)
+    assert (listed[0, :4] > 64).all() and (listed[0, 4:] <= 64).all()
     assert extra >= BH * 16
 
 
