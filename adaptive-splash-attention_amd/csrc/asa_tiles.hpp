@@ -92,6 +92,41 @@ __device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const float* rm,
     }
 }
 
+// rows_x_frag with the tile read straight from global memory: `rows` points
+// at the tile's first row of a [*, D] row-major tensor, rows >= nrows read as
+// zero.  The same operands in the same MFMA order as the LDS versions above
+// (the LDS tile holds the same values; its swizzle only moves them), so the
+// results are bit-identical.
+template <int D>
+__device__ __forceinline__ void rows_x_frag_global(f32x4 (&acc)[4], const u16* rows, int nrows,
+                                                   const RowFrag<u16, D>& b, int lane) {
+  const int g = lane >> 4, c = lane & 15;
+  bf16x8 a[D / 32][4];
+  for (int s = 0; s < D / 32; ++s)
+    for (int f = 0; f < 4; ++f)
+      a[s][f] = 16 * f + c < nrows
+                    ? *reinterpret_cast<const bf16x8*>(rows + (16 * f + c) * D + 32 * s + 8 * g)
+                    : bf16x8{};
+  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < D / 32; ++s)
+    for (int f = 0; f < 4; ++f) acc[f] = mfma(a[s][f], b.v[s], acc[f]);
+}
+template <int D>
+__device__ __forceinline__ void rows_x_frag_global(f32x4 (&acc)[4], const float* rows, int nrows,
+                                                   const RowFrag<float, D>& b, int lane) {
+  const int g = lane >> 4, c = lane & 15;
+  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < D / 16; ++j) {
+    f32x4 a[4];
+    for (int f = 0; f < 4; ++f)
+      a[f] = 16 * f + c < nrows
+                 ? *reinterpret_cast<const f32x4*>(rows + (16 * f + c) * D + 16 * j + 4 * g)
+                 : f32x4{};
+    for (int f = 0; f < 4; ++f)
+      for (int r = 0; r < 4; ++r) acc[f] = mfma(a[f][r], b.v[j][r], acc[f]);
+  }
+}
+
 // bf16: `rm` is the row-major tile.  The A operand (4 consecutive tile rows
 // at one column per lane and half) is read with ds_read_b64_tr_b16: in each
 // 16-lane group, lane l reads the 8 bytes at row key0 + l/4, columns

@@ -24,32 +24,36 @@
 //      so tau_k is already the exact threshold (every row with fewer than k
 //      visible keys, and every row whose support is smaller than k).
 //   2. Otherwise the row needs the whole row.  A sweep recomputes the row's
-//      scores (S^T = K Q^T on MFMA from K tiles staged through LDS, as in
-//      the forward) and sums v^a and v^(a-1) over v = max(u, 0).  The
+//      scores (S^T = K Q^T on MFMA, the forward's operands and order, so
+//      the same bits) and sums v^a and v^(a-1) over v = max(u, 0).  The
 //      first sweep, at tau_k, also lists in LDS every key with u > 0 (its
 //      raw dot product and key block): the exact support lies inside that
-//      list, since tau_exact >= tau_k (lists for up to kListRows rows per
-//      block).  A row whose list fits (lcap entries) finishes there: safeguarded Newton steps over
-//      the listed keys, then its support's key blocks are marked from the
-//      list.  A row whose list overflowed takes one safeguarded Newton
-//      step per further sweep instead (bracket: left end from step 1,
-//      right end z1), until |f| <= 1e-6, a step leaves tau unchanged, or
-//      kMaxSweeps sweeps.  The block sweeps until all its rows have
-//      stopped; in that last sweep every row uses its final tau, and the
-//      key blocks where some row had u > 0 in it join the mask.
+//      list, since tau_exact >= tau_k.  A row whose lists fit finishes
+//      there: safeguarded Newton steps over the listed keys, then its
+//      support's key blocks are marked from them.  A row whose lists
+//      overflowed (or beyond the first kListRows of a block) takes one
+//      safeguarded Newton step per further sweep instead (bracket: left
+//      end from step 1, right end z1), until |f| <= 1e-6, a step leaves tau
+//      unchanged, or kMaxSweeps sweeps.  The block sweeps until all its rows
+//      have stopped; in that last sweep every row uses its final tau, and
+//      the key blocks where some row had u > 0 in it join the mask.
 //
 // One 256-thread block per (batch*head, 64-query block).  In step 1 wave w
-// owns rows 16w..16w+15; for step 2 the rows that need sweeps are packed
-// into the first waves (about 5 of 64 rows at the headline shape, so
-// usually one wave computes while the others only stage K tiles).  Lane L
-// holds keys 16f + 4g + r (g = L / 16) of its row L % 16: the four lanes of
-// a row hold identical per-row state, and their partial sums are combined
-// with sum_groups (bit-identical in all four).
+// owns rows 16w..16w+15.  The rows that need sweeps (about 5 of 64 at the
+// headline shape) are packed into groups of 16; in a sweep every wave
+// holds the packed rows group by group and takes every fourth visible key
+// tile, reading the tile's K fragments straight from global memory (a
+// head's K stays in L2), so no barrier separates the tiles and all four
+// waves compute.  The waves' partial sums and key lists (one per wave and
+// row) meet in LDS and are combined in a fixed order, so results do not
+// depend on timing.  Lane L holds keys 16f + 4g + r (g = L / 16) of its
+// row L % 16: the four lanes of a row hold identical per-row state, and
+// their partial sums are combined with sum_groups (bit-identical in all
+// four).
 #include <climits>
 
 #include "asa_device.hpp"
 #include "asa_launch.hpp"
-#include "asa_stage.hpp"
 #include "asa_tiles.hpp"
 
 namespace asa {
@@ -59,10 +63,9 @@ constexpr int kThreads = 256;
 constexpr int kMaxTopkSteps = 64;  // Newton / bisection steps on the top-k values
 constexpr int kMaxSweeps = 32;     // full-row sweeps per query block
 constexpr float kTol = 1e-6f;      // |sum p - 1| at which a row's tau is final
-// Packed rows with a key list (the first 16: one wave's rows).  More rows
-// than this per block are rare (about 5 of 64 need sweeps at the headline
-// shape); the others sweep.  Fewer lists keep the LDS per block small, so
-// that more blocks share a compute unit.
+// Packed rows with key lists (the first 16 of a block).  More rows than
+// this per block are rare (about 5 of 64 need sweeps at the headline
+// shape); the others sweep.
 constexpr int kListRows = 16;
 
 // v^a and v^(a-1) for v = max(u, 0); both zero at v = 0.
@@ -99,20 +102,19 @@ __device__ __forceinline__ float newton_step(float tau, float f, float F1, float
 }
 
 struct ExactLayout {
-  int kid, busy, cnt, rowst, ldot, lkb, vlist, bits, total;
+  int busy, cnt, rowst, part, ldot, lkb, vlist, bits, total;
 };
 __host__ __device__ inline int align16(int x) { return (x + 15) & ~15; }
-// lcap: listed keys per row (0: no lists)
-__host__ __device__ inline ExactLayout exact_layout(int D, int tbytes, int nKB, int lcap) {
-  const int rs = tbytes == 2 ? D + 8 : D + 4;  // Tile<T, D>::kRs
+// lcap: listed keys per packed row and wave (0: no lists)
+__host__ __device__ inline ExactLayout exact_layout(int nKB, int lcap) {
   ExactLayout l;
-  l.kid = align16(2 * kBlock * rs * tbytes);
-  l.busy = l.kid + 2 * kBlock * 4;
-  l.cnt = l.busy + 16 * 4;
-  l.rowst = l.cnt + kBlock * 4;  // tau, lo, z1 and packed row of each row
-  l.ldot = l.rowst + 4 * kBlock * 4;
-  l.lkb = l.ldot + kListRows * lcap * 4;
-  l.vlist = l.lkb + kListRows * lcap * 4;
+  l.busy = 0;
+  l.cnt = l.busy + 16 * 4;          // list lengths [wave][packed row < kListRows]
+  l.rowst = l.cnt + kBlock * 4;     // per row: tau, lo, z1, packed row; per slot: tau
+  l.part = l.rowst + 5 * kBlock * 4;  // per wave and slot: partial F and F1
+  l.ldot = l.part + 2 * 4 * kBlock * 4;
+  l.lkb = l.ldot + 4 * kListRows * lcap * 4;
+  l.vlist = l.lkb + 4 * kListRows * lcap * 4;
   l.bits = l.vlist + align16(nKB * 4);
   l.total = l.bits + align16((nKB + 31) / 32 * 4);
   return l;
@@ -121,24 +123,22 @@ __host__ __device__ inline ExactLayout exact_layout(int D, int tbytes, int nKB, 
 template <typename T, int D, int PC>
 __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  using Ks = KStage<T, D, kThreads>;
-  static_assert(Tile<T, D>::kRs == (sizeof(T) == 2 ? D + 8 : D + 4), "layout row stride");
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB, k = p.d.k;
   const int lcap = p.lcap;
-  const ExactLayout lay = exact_layout(D, int(sizeof(T)), nKB, lcap);
-  T* s_k = reinterpret_cast<T*>(smem);
-  int* s_kid = reinterpret_cast<int*>(smem + lay.kid);
+  const ExactLayout lay = exact_layout(nKB, lcap);
   int* s_busy = reinterpret_cast<int*>(smem + lay.busy);
   uint32_t* s_cnt = reinterpret_cast<uint32_t*>(smem + lay.cnt);
   float* s_tau = reinterpret_cast<float*>(smem + lay.rowst);
   float* s_lo = s_tau + kBlock;
   float* s_z1 = s_lo + kBlock;
   int* s_rows = reinterpret_cast<int*>(s_z1 + kBlock);
+  float* s_ptau = reinterpret_cast<float*>(s_rows + kBlock);
+  float* s_pF = reinterpret_cast<float*>(smem + lay.part);
+  float* s_pF1 = s_pF + 4 * kBlock;
   float* s_ldot = reinterpret_cast<float*>(smem + lay.ldot);
   int* s_lkb = reinterpret_cast<int*>(smem + lay.lkb);
   int* s_vlist = reinterpret_cast<int*>(smem + lay.vlist);
   uint32_t* s_bits = reinterpret_cast<uint32_t*>(smem + lay.bits);
-  constexpr int kTileElems = kBlock * Tile<T, D>::kRs;
 
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
@@ -233,67 +233,62 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
   __syncthreads();
 
   if (nneed > 0) {  // block-uniform
-    // this lane's packed row
+    // Update-phase identity: wave w, column c16 owns packed slot 16w + c16
+    // (its per-row state lives in registers of the row's four lanes).
     const int slot = 16 * w + c16;
     const bool pk = slot < nneed;
     const int prow = pk ? s_rows[slot] : 0;
-    const int pq = qb * kBlock + prow;
-    const size_t pgrow = size_t(bh) * NQ + pq;
+    const size_t pgrow = size_t(bh) * NQ + qb * kBlock + prow;
     tau = pk ? s_tau[prow] : 0.0f;
     lo = pk ? s_lo[prow] : 0.0f;
     const float pz1 = pk ? s_z1[prow] : 0.0f;
     hi = pz1;  // f over the whole row is -1 there; lo keeps f >= 0
+    if (pk && g == 0) s_ptau[slot] = tau;
 
+    // Sweep-phase identity: every wave holds the packed rows group by group
+    // and takes every fourth visible key tile, reading its K fragments
+    // straight from global memory (a head's K stays in L2), so no barrier
+    // separates the tiles.  Partial sums meet in LDS in a fixed order.
+    const int ngroups = (nneed + 15) >> 4;
     const T* Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
     const int32_t* kidx = p.k_idx + size_t(bh) * NK;
-    RowFrag<T, D> qf;
-    qf.load(static_cast<const T*>(p.q) + pgrow * D, pk, lane);
-    const int qpos = pk ? p.q_idx[pgrow] : 0;
-    const bool wsweep = 16 * w < nneed;  // wave-uniform
     const int nbw = (nKB + 31) >> 5;
-    const bool lslot = slot < kListRows;  // this row has a key list
-    float* ldot = s_ldot + (lslot ? slot : 0) * lcap;
-    int* lkb = s_lkb + (lslot ? slot : 0) * lcap;
     bool done = !pk;
-    bool listed = false;  // the row finished on its list
-    Ks ks;
-    PosStager ps;
+    bool listed = false;  // the row finished on its key lists
     for (int sw = 0;; ++sw) {
       for (int i = t; i < nbw; i += kThreads) s_bits[i] = 0u;
-      // rows that stopped keep their final tau and still mark their blocks
-      const ClippedU clip(am1, p.d.scale, tau, pk);
-      // first sweep (at tau_k): the keys with u > 0 go to the row's list
+      // first sweep (at tau_k): every key with u > 0 goes to a list of its
+      // (wave, row), for the first kListRows packed rows
       const bool collect = sw == 0 && lcap > 0;  // block-uniform
-      double F = 0.0, F1 = 0.0;
-      auto fetch = [&](int e) {
-        const int kbase = (s_vlist[e] & 0xffffff) * kBlock;
-        ks.load(Kb, kbase, NK, t);
-        ps.load(kidx, kbase, NK, INT32_MAX, t);
-      };
-      auto put = [&](int b) {
-        ks.store(s_k + b * kTileElems, t);
-        ps.store(s_kid + b * kBlock, t);
-      };
-      __syncthreads();  // bitmap cleared; the previous sweep's tiles consumed
-      if (nvis > 0) {
-        fetch(0);
-        put(0);
-        if (nvis > 1) fetch(1);
-      }
-      __syncthreads();
-      for (int e = 0; e < nvis; ++e) {
-        const int b = e & 1;
-        const int ent = s_vlist[e];
-        if (wsweep) {
-          f32x4 acc[4];
-          rows_x_frag<D>(acc, s_k + b * kTileElems, qf, lane);
+      __syncthreads();  // bitmap cleared; s_ptau published
+      for (int rg = 0; rg < ngroups; ++rg) {
+        const int sl = 16 * rg + c16;
+        const bool spk = sl < nneed;
+        const size_t sgrow = size_t(bh) * NQ + qb * kBlock + (spk ? s_rows[sl] : 0);
+        RowFrag<T, D> qf;
+        qf.load(static_cast<const T*>(p.q) + sgrow * D, spk, lane);
+        const int sqpos = spk ? p.q_idx[sgrow] : 0;
+        // rows that stopped keep their final tau and still mark their blocks
+        const ClippedU clip(am1, p.d.scale, spk ? s_ptau[sl] : 0.0f, spk);
+        const bool scol = collect && spk && sl < kListRows;
+        float* ldot = s_ldot + (w * kListRows + (scol ? sl : 0)) * lcap;
+        int* lkb = s_lkb + (w * kListRows + (scol ? sl : 0)) * lcap;
+        double F = 0.0, F1 = 0.0;
+        for (int e = w; e < nvis; e += 4) {
+          const int ent = s_vlist[e];
+          const int kb = ent & 0xffffff, kbase = kb * kBlock;
           const bool full = (ent >> 24) == 2;
+          f32x4 acc[4];
+          rows_x_frag_global<D>(acc, Kb + size_t(kbase) * D, NK - kbase, qf, lane);
           float tF = 0.0f, tF1 = 0.0f, vmax = 0.0f;
           uint32_t m = 0;  // bit 4f + r: key 16f + 4g + r has u > 0
           for (int f = 3; f >= 0; --f)
             for (int r = 3; r >= 0; --r) {
               float v = clip(acc[f][r]);
-              if (!full) v = s_kid[b * kBlock + 16 * f + 4 * g + r] <= qpos ? v : 0.0f;
+              if (!full) {
+                const int key = kbase + 16 * f + 4 * g + r;
+                v = key < NK && kidx[key] <= sqpos ? v : 0.0f;
+              }
               float pa, pa1;
               pow_pair<PC>(v, a, pa, pa1);
               tF += pa;
@@ -303,11 +298,10 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
             }
           F += double(tF);
           F1 += double(tF1);
-          const int kb = ent & 0xffffff;
           if (__ballot(collect ? m != 0u : vmax > 0.0f) != 0 && lane == 0)
             atomicOr(&s_bits[kb >> 5], 1u << (kb & 31));
-          if (collect && lslot && m) {
-            int j = int(atomicAdd(&s_cnt[slot], uint32_t(__builtin_popcount(m))));
+          if (scol && m) {
+            int j = int(atomicAdd(&s_cnt[w * kListRows + sl], uint32_t(__builtin_popcount(m))));
             for (int f = 0; f < 4; ++f)
               for (int r = 0; r < 4; ++r)
                 if ((m >> (4 * f + r)) & 1u) {
@@ -319,33 +313,45 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
                 }
           }
         }
-        if (e + 1 < nvis) {
-          put(b ^ 1);
-          if (e + 2 < nvis) fetch(e + 2);
+        const float Fs = sum_groups(float(F));
+        const float F1s = sum_groups(float(F1));
+        if (spk && g == 0) {
+          s_pF[w * kBlock + sl] = Fs;
+          s_pF1[w * kBlock + sl] = F1s;
         }
-        __syncthreads();
       }
-      const float Fs = sum_groups(float(F));
-      const float F1s = sum_groups(float(F1));
-      const float f = Fs - 1.0f;
+      __syncthreads();  // partial sums and lists complete
+
+      // ---- update phase ----
+      float f = 0.0f, F1s = 0.0f;
+      if (pk) {
+        f = ((s_pF[slot] + s_pF[kBlock + slot]) + (s_pF[2 * kBlock + slot] + s_pF[3 * kBlock + slot])) - 1.0f;
+        F1s = (s_pF1[slot] + s_pF1[kBlock + slot]) + (s_pF1[2 * kBlock + slot] + s_pF1[3 * kBlock + slot]);
+      }
       if (collect) {
-        // a row whose list holds every key with u > 0 at tau_k finishes on
-        // it: f over the list is exact for tau >= tau_k (the fused u is
+        // a row whose lists hold every key with u > 0 at tau_k finishes on
+        // them: f over the lists is exact for tau >= tau_k (the fused u is
         // monotone in tau), and tau_exact >= tau_k
-        listed = lslot && !done && s_cnt[slot] <= uint32_t(lcap);
-        const int n = listed ? int(s_cnt[slot]) : 0;
+        listed = pk && !done && slot < kListRows;
+        for (int ww = 0; ww < 4; ++ww)
+          listed = listed && s_cnt[ww * kListRows + (slot < kListRows ? slot : 0)] <= uint32_t(lcap);
         float llo = tau, lhi = pz1;
         bool lbusy = listed;
         for (int it = 0; it < kMaxTopkSteps; ++it) {
           if (__ballot(lbusy) == 0) break;  // wave-uniform
           const ClippedU cl(am1, p.d.scale, tau, true);
           float LF = 0.0f, LF1 = 0.0f;
-          for (int j = g; j < n; j += 4) {
-            float pa, pa1;
-            pow_pair<PC>(cl(ldot[j]), a, pa, pa1);
-            LF += pa;
-            LF1 += pa1;
-          }
+          if (listed)
+            for (int ww = 0; ww < 4; ++ww) {
+              const float* ld = s_ldot + (ww * kListRows + slot) * lcap;
+              const int n = int(s_cnt[ww * kListRows + slot]);
+              for (int j = g; j < n; j += 4) {
+                float pa, pa1;
+                pow_pair<PC>(cl(ld[j]), a, pa, pa1);
+                LF += pa;
+                LF1 += pa1;
+              }
+            }
           LF = sum_groups(LF);
           LF1 = sum_groups(LF1);
           if (lbusy) {
@@ -370,24 +376,29 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
           tau = nt;
         }
       }
-      // After the first sweep a block with an overflowed list sweeps again
-      // even if every row stopped: its marks must come from a sweep at the
-      // rows' final tau.
+      if (pk && g == 0) s_ptau[slot] = tau;
+      // After the first sweep a block with a row that did not finish on its
+      // lists sweeps again even if every row stopped: its marks must come
+      // from a sweep at the rows' final tau.
       const uint64_t wbusy = __ballot(!done || (collect && pk && !listed));
       if (lane == 0) s_busy[4 * (sw & 1) + w] = wbusy != 0;
       __syncthreads();
       const int* bz = s_busy + 4 * (sw & 1);
       if ((bz[0] | bz[1] | bz[2] | bz[3]) == 0) {  // block-uniform
         if (collect) {
-          // every row that swept finished on its list, but the sweep ran at
-          // tau_k: mark the blocks of the listed keys with u > 0 at the
-          // final tau instead
+          // every row finished on its lists, but the sweep ran at tau_k:
+          // mark the blocks of the listed keys with u > 0 at the final tau
           for (int i = t; i < nbw; i += kThreads) s_bits[i] = 0u;
           __syncthreads();
           const ClippedU cl(am1, p.d.scale, tau, listed);
-          const int n = listed ? int(s_cnt[slot]) : 0;
-          for (int j = g; j < n; j += 4)
-            if (cl(ldot[j]) > 0.0f) atomicOr(&s_bits[lkb[j] >> 5], 1u << (lkb[j] & 31));
+          if (listed)
+            for (int ww = 0; ww < 4; ++ww) {
+              const float* ld = s_ldot + (ww * kListRows + slot) * lcap;
+              const int* lk = s_lkb + (ww * kListRows + slot) * lcap;
+              const int n = int(s_cnt[ww * kListRows + slot]);
+              for (int j = g; j < n; j += 4)
+                if (cl(ld[j]) > 0.0f) atomicOr(&s_bits[lk[j] >> 5], 1u << (lk[j] & 31));
+            }
           __syncthreads();
         }
         break;
@@ -426,13 +437,15 @@ hipError_t launch_td(const SelectParams& p, size_t lds, hipStream_t s) {
 }  // namespace
 
 size_t refine_lds_bytes(const Dims& d, bool bf16, int lcap) {
-  return size_t(exact_layout(d.D, bf16 ? 2 : 4, d.nKB, lcap).total);
+  (void)bf16;  // K is read from global memory: the LDS does not depend on the type
+  return size_t(exact_layout(d.nKB, lcap).total);
 }
 
 int refine_list_capacity(const Dims& d, bool bf16, size_t max_lds) {
-  // k + 32 listed keys hold the u > 0 keys of random rows at tau_k with
-  // room to spare (at most ~1.7 k at k = 32); rows that overflow sweep on
-  int lcap = d.k + 32 > 64 ? d.k + 32 : 64;
+  // Per wave and row: the u > 0 keys of random rows at tau_k number at
+  // most ~1.7 k at k = 32, a quarter of them per wave on average; (k + 32)
+  // / 2 per wave leaves room for uneven splits.  Rows that overflow sweep.
+  int lcap = (d.k + 32) / 2 > 32 ? (d.k + 32) / 2 : 32;
   while (lcap > 0 && refine_lds_bytes(d, bf16, lcap) > max_lds) lcap -= 16;
   if (lcap < 0) lcap = 0;
   return refine_lds_bytes(d, bf16, lcap) <= max_lds ? lcap : -1;

@@ -160,8 +160,9 @@ def test_exact_mode_adds_support_blocks():
     sup = (P > 0).sum(-1)
     assert (sup[:, :4] > 256).all() and (sup[:, 4:] > 1).all()
     # keys listed by the first sweep (u > -1e-3 at the top-k root, which is
-    # z_max - 1 at k = 1), against the 64-key lists used at k = 1: head 0
-    # mixes overflowing rows (0-3) and listed rows (4-7) in one block
+    # z_max - 1 at k = 1), against the lists used at k = 1 (32 keys per wave
+    # and row, the row's key tiles dealt to the four waves): head 0 mixes
+    # overflowing rows (0-3) and listed rows (4-7) in one block
     z = 0.25 * np.clip(np.einsum("bid,bjd->bij", np32(Q).astype(np.float64),
                                  np32(K).astype(np.float64)) * 0.02, -10, 10)
     listed = (z > z.max(-1, keepdims=True) - 1.0 - 1e-3).sum(-1)
