@@ -208,3 +208,91 @@ def test_exact_mode_through_module_and_custom_op():
     assert torch.equal(op[1], st.taus)
     ref = sa.splash_attention(Q, K, V, None, None, alpha, k, 0.125)  # reference tau
     assert not torch.equal(ref, out_ops)  # c1-like rows: supports exceed k
+
+
+def _exact_full(name, Q, K, V, dO, qi, ki, alpha, k, scale, sample):
+    """Exact mode at a full BASELINE shape (bf16), checked through
+    size-independent properties and sampled rows:
+      - every row has sum_j p_j = 1 (the exact threshold's defining
+        equation), read from the forward's own row sums: to 1e-3, since each
+        lane adds up to N/4 float32 terms in sequence (about 2.4e-4 at
+        N = 16384), while a top-k threshold misses by far more wherever the
+        support exceeds k (c4: about 216 keys tie at the +10 clamp against
+        k = 64, so the reference threshold gives sum p ~ 3.4);
+      - the full-gradient identities of the entmax Jacobian (sum_j dK_j = 0,
+        sum_j dV_j = sum_i dO_i N_i / (N_i + EPS));
+      - for the sampled (head, 64-row block) pairs, tau and the output rows
+        against dense alpha-entmax in float64 over the same bf16 inputs
+        (tau to 1e-4, output 2e-2)."""
+    import time
+
+    import splash_attention as sa
+    from tests.test_gpu_configs import _identities
+
+    dev = torch.device("cuda:0")
+    B, H, N, d = Q.shape
+    q, kk, v, qi_, ki_ = sa.ops.check_inputs(Q.to(dev), K.to(dev), V.to(dev), qi.to(dev), ki.to(dev))
+    do = dO.to(dev)
+
+    def step():
+        out, st = sa.ops.splash_forward(q, kk, v, qi_, ki_, alpha, k, scale, tau_mode="exact")
+        grads = sa.ops.splash_backward(q, kk, v, qi_, ki_, out, do, st, alpha, k, scale, "entmax")
+        return out, st, grads
+
+    out, st, grads = step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3
+    assert torch.isfinite(out).all()
+    norms = st.norms  # every row of these configs sees at least key 0
+    e_norm = float((norms - 1.0).abs().max())
+    assert e_norm <= 1e-3, f"{name}: max |sum p - 1| = {e_norm:.2e}"
+    _identities(name, norms, grads, dO, 2e-2)
+    e_tau = e_out = 0.0
+    for bh, q0 in sample:
+        b, h = divmod(bh, H)
+        qs = slice(q0, q0 + 64)
+        qr = Q[b, h, qs].double().numpy()
+        kr = K[b, h].double().numpy()
+        vr = V[b, h].double().numpy()
+        vis = ki[bh].numpy()[None, :] <= qi[bh, qs].numpy()[:, None]
+        ref_out, _, taus = dense.attention_forward(qr[None], kr[None], vr[None], vis[None], alpha,
+                                                   scale)
+        gt = st.taus[bh, qs].cpu().double().numpy()
+        e_tau = max(e_tau, float(np.abs(gt - taus[0]).max()))
+        e_out = max(e_out, assert_close(f"{name} out[{bh},{q0}]", np32(out[b:b + 1, h:h + 1, qs]),
+                                        ref_out, 2e-2))
+    assert e_tau <= 1e-4, f"{name}: tau differs by {e_tau:.2e}"
+    print(f"  {name}: fwd+bwd {ms:.1f} ms, max |sum p - 1| {e_norm:.1e}, sampled tau {e_tau:.1e}, "
+          f"out {e_out:.1e}", flush=True)
+
+
+def test_exact_mode_c4_full():
+    """configs[3] at full size in exact mode: B=1, H=32, N=16384, d=128 bf16,
+    sparsemax, k 64, non-causal, clustered keys (most supports exceed k)."""
+    from tests.test_gpu_configs import _clustered
+
+    print("[exact] c4 bf16 1x32x16384x128 clustered", flush=True)
+    B, H, N, d = 1, 32, 16384, 128
+    Q, K, V, dO = _clustered(B, H, N, d, seed=0)
+    qi = torch.full((B * H, N), N - 1, dtype=torch.int32)
+    _exact_full("c4", Q, K, V, dO, qi, causal_idx(B * H, N), 2.0, 64, 128 ** -0.5,
+                ((0, 0), (21, 8192)))
+
+
+def test_exact_mode_c5_full():
+    """configs[4] at full size in exact mode: B=1, H=8, N=32768, d=128 bf16,
+    alpha 1.25, k 128, causal, keys 0..15 scaled x4 (sinks)."""
+    from tests.test_gpu_configs import _gauss
+
+    print("[exact] c5 bf16 1x8x32768x128 sinks", flush=True)
+    B, H, N, d = 1, 8, 32768, 128
+    Q, K, V = (_gauss((B, H, N, d), s, torch.float32) for s in (0, 1, 2))
+    K[:, :, :16] *= 4
+    Q, K, V = (t.to(torch.bfloat16) for t in (Q, K, V))
+    dO = _gauss((B, H, N, d), 3, torch.bfloat16)
+    idx = causal_idx(B * H, N)
+    _exact_full("c5", Q, K, V, dO, idx, idx, 1.25, 128, 128 ** -0.5,
+                ((3, 0), (3, 16384), (5, 32704)))
