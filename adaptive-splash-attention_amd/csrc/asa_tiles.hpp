@@ -127,6 +127,39 @@ __device__ __forceinline__ void rows_x_frag_global(f32x4 (&acc)[4], const float*
   }
 }
 
+// A key tile's A operands of rows_x_frag_global, loaded once and multiplied
+// by several B fragments (bf16: held in registers; fp32: re-read per
+// product, since D = 128 would take 128 registers).
+template <typename T, int D> struct KFrags;
+template <int D> struct KFrags<u16, D> {
+  bf16x8 a[D / 32][4];
+  __device__ __forceinline__ void load(const u16* rows, int nrows, int lane) {
+    const int g = lane >> 4, c = lane & 15;
+    for (int s = 0; s < D / 32; ++s)
+      for (int f = 0; f < 4; ++f)
+        a[s][f] = 16 * f + c < nrows
+                      ? *reinterpret_cast<const bf16x8*>(rows + (16 * f + c) * D + 32 * s + 8 * g)
+                      : bf16x8{};
+  }
+  __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<u16, D>& b) const {
+    for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < D / 32; ++s)
+      for (int f = 0; f < 4; ++f) acc[f] = mfma(a[s][f], b.v[s], acc[f]);
+  }
+};
+template <int D> struct KFrags<float, D> {
+  const float* rows;
+  int nrows, lane;
+  __device__ __forceinline__ void load(const float* r, int n, int l) {
+    rows = r;
+    nrows = n;
+    lane = l;
+  }
+  __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<float, D>& b) const {
+    rows_x_frag_global<D>(acc, rows, nrows, b, lane);
+  }
+};
+
 // bf16: `rm` is the row-major tile.  The A operand (4 consecutive tile rows
 // at one column per lane and half) is read with ds_read_b64_tr_b16: in each
 // 16-lane group, lane l reads the 8 bytes at row key0 + l/4, columns

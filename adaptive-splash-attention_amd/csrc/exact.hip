@@ -102,17 +102,19 @@ __device__ __forceinline__ float newton_step(float tau, float f, float F1, float
 }
 
 struct ExactLayout {
-  int busy, cnt, rowst, part, ldot, lkb, vlist, bits, total;
+  int busy, cnt, rowst, part, qrows, ldot, lkb, vlist, bits, total;
 };
 __host__ __device__ inline int align16(int x) { return (x + 15) & ~15; }
-// lcap: listed keys per packed row and wave (0: no lists)
-__host__ __device__ inline ExactLayout exact_layout(int nKB, int lcap) {
+// lcap: listed keys per packed row and wave (0: no lists); qbytes: one
+// query row (D elements)
+__host__ __device__ inline ExactLayout exact_layout(int nKB, int lcap, int qbytes) {
   ExactLayout l;
   l.busy = 0;
   l.cnt = l.busy + 16 * 4;          // list lengths [wave][packed row < kListRows]
   l.rowst = l.cnt + kBlock * 4;     // per row: tau, lo, z1, packed row; per slot: tau
   l.part = l.rowst + 5 * kBlock * 4;  // per wave and slot: partial F and F1
-  l.ldot = l.part + 2 * 4 * kBlock * 4;
+  l.qrows = l.part + 2 * 4 * kBlock * 4;  // the packed rows' Q, [slot][D]
+  l.ldot = l.qrows + kBlock * qbytes;
   l.lkb = l.ldot + 4 * kListRows * lcap * 4;
   l.vlist = l.lkb + 4 * kListRows * lcap * 4;
   l.bits = l.vlist + align16(nKB * 4);
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB, k = p.d.k;
   const int lcap = p.lcap;
-  const ExactLayout lay = exact_layout(nKB, lcap);
+  const ExactLayout lay = exact_layout(nKB, lcap, D * int(sizeof(T)));
   int* s_busy = reinterpret_cast<int*>(smem + lay.busy);
   uint32_t* s_cnt = reinterpret_cast<uint32_t*>(smem + lay.cnt);
   float* s_tau = reinterpret_cast<float*>(smem + lay.rowst);
@@ -135,6 +137,7 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
   float* s_ptau = reinterpret_cast<float*>(s_rows + kBlock);
   float* s_pF = reinterpret_cast<float*>(smem + lay.part);
   float* s_pF1 = s_pF + 4 * kBlock;
+  T* s_q = reinterpret_cast<T*>(smem + lay.qrows);
   float* s_ldot = reinterpret_cast<float*>(smem + lay.ldot);
   int* s_lkb = reinterpret_cast<int*>(smem + lay.lkb);
   int* s_vlist = reinterpret_cast<int*>(smem + lay.vlist);
@@ -244,6 +247,15 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
     const float pz1 = pk ? s_z1[prow] : 0.0f;
     hi = pz1;  // f over the whole row is -1 there; lo keeps f >= 0
     if (pk && g == 0) s_ptau[slot] = tau;
+    {  // the packed rows' Q, 16 bytes per thread and step
+      constexpr int kEpc = 16 / int(sizeof(T)), kCpr = D / kEpc;
+      const T* Qh = static_cast<const T*>(p.q) + (size_t(bh) * NQ + qb * kBlock) * D;
+      for (int i = t; i < nneed * kCpr; i += kThreads) {
+        const int sl = i / kCpr, cc = i % kCpr;
+        *reinterpret_cast<uint4*>(s_q + sl * D + cc * kEpc) =
+            *reinterpret_cast<const uint4*>(Qh + size_t(s_rows[sl]) * D + cc * kEpc);
+      }
+    }
 
     // Sweep-phase identity: every wave holds the packed rows group by group
     // and takes every fourth visible key tile, reading its K fragments
@@ -261,63 +273,83 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
       // (wave, row), for the first kListRows packed rows
       const bool collect = sw == 0 && lcap > 0;  // block-uniform
       __syncthreads();  // bitmap cleared; s_ptau published
-      for (int rg = 0; rg < ngroups; ++rg) {
+      // per packed row group (at most 4), the lane's row state
+      int sqpos[4];
+      ClippedU clips[4] = {ClippedU(am1, p.d.scale, 0.0f, false), ClippedU(am1, p.d.scale, 0.0f, false),
+                           ClippedU(am1, p.d.scale, 0.0f, false), ClippedU(am1, p.d.scale, 0.0f, false)};
+      double F[4] = {0.0, 0.0, 0.0, 0.0}, F1[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
         const int sl = 16 * rg + c16;
         const bool spk = sl < nneed;
-        const size_t sgrow = size_t(bh) * NQ + qb * kBlock + (spk ? s_rows[sl] : 0);
-        RowFrag<T, D> qf;
-        qf.load(static_cast<const T*>(p.q) + sgrow * D, spk, lane);
-        const int sqpos = spk ? p.q_idx[sgrow] : 0;
+        sqpos[rg] = spk ? p.q_idx[size_t(bh) * NQ + qb * kBlock + s_rows[sl]] : 0;
         // rows that stopped keep their final tau and still mark their blocks
-        const ClippedU clip(am1, p.d.scale, spk ? s_ptau[sl] : 0.0f, spk);
-        const bool scol = collect && spk && sl < kListRows;
-        float* ldot = s_ldot + (w * kListRows + (scol ? sl : 0)) * lcap;
-        int* lkb = s_lkb + (w * kListRows + (scol ? sl : 0)) * lcap;
-        double F = 0.0, F1 = 0.0;
-        for (int e = w; e < nvis; e += 4) {
-          const int ent = s_vlist[e];
-          const int kb = ent & 0xffffff, kbase = kb * kBlock;
-          const bool full = (ent >> 24) == 2;
-          f32x4 acc[4];
-          rows_x_frag_global<D>(acc, Kb + size_t(kbase) * D, NK - kbase, qf, lane);
-          float tF = 0.0f, tF1 = 0.0f, vmax = 0.0f;
-          uint32_t m = 0;  // bit 4f + r: key 16f + 4g + r has u > 0
-          for (int f = 3; f >= 0; --f)
-            for (int r = 3; r >= 0; --r) {
-              float v = clip(acc[f][r]);
-              if (!full) {
-                const int key = kbase + 16 * f + 4 * g + r;
-                v = key < NK && kidx[key] <= sqpos ? v : 0.0f;
-              }
-              float pa, pa1;
-              pow_pair<PC>(v, a, pa, pa1);
-              tF += pa;
-              tF1 += pa1;
-              if (collect) m = 2u * m + (v > 0.0f ? 1u : 0u);
-              else vmax = fmaxf(vmax, v);
-            }
-          F += double(tF);
-          F1 += double(tF1);
-          if (__ballot(collect ? m != 0u : vmax > 0.0f) != 0 && lane == 0)
-            atomicOr(&s_bits[kb >> 5], 1u << (kb & 31));
-          if (scol && m) {
-            int j = int(atomicAdd(&s_cnt[w * kListRows + sl], uint32_t(__builtin_popcount(m))));
-            for (int f = 0; f < 4; ++f)
-              for (int r = 0; r < 4; ++r)
-                if ((m >> (4 * f + r)) & 1u) {
-                  if (j < lcap) {
-                    ldot[j] = acc[f][r];
-                    lkb[j] = kb;
-                  }
-                  ++j;
+        clips[rg] = ClippedU(am1, p.d.scale, spk ? s_ptau[sl] : 0.0f, spk);
+      }
+      const bool scol = collect && c16 < nneed;  // group 0 rows have lists
+      float* ldot = s_ldot + (w * kListRows + c16) * lcap;
+      int* lkb = s_lkb + (w * kListRows + c16) * lcap;
+      // Tiles outermost: a tile's K fragments are loaded once and multiplied
+      // by every group's Q rows (staged in LDS), so K is read once per sweep
+      // whatever the number of groups.
+      for (int e = w; e < nvis; e += 4) {
+        const int ent = s_vlist[e];
+        const int kb = ent & 0xffffff, kbase = kb * kBlock;
+        const bool full = (ent >> 24) == 2;
+        KFrags<T, D> kf;
+        kf.load(Kb + size_t(kbase) * D, NK - kbase, lane);
+        float vany = 0.0f;  // > 0: some row of the wave has u > 0 in the tile
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          if (rg < ngroups) {  // block-uniform
+            RowFrag<T, D> qf;
+            qf.load(s_q + (16 * rg + c16) * D, 16 * rg + c16 < nneed, lane);
+            f32x4 acc[4];
+            kf.product(acc, qf);
+            float tF = 0.0f, tF1 = 0.0f;
+            uint32_t m = 0;  // bit 4f + r: key 16f + 4g + r has u > 0 (group 0)
+            for (int f = 3; f >= 0; --f)
+              for (int r = 3; r >= 0; --r) {
+                float v = clips[rg](acc[f][r]);
+                if (!full) {
+                  const int key = kbase + 16 * f + 4 * g + r;
+                  v = key < NK && kidx[key] <= sqpos[rg] ? v : 0.0f;
                 }
+                float pa, pa1;
+                pow_pair<PC>(v, a, pa, pa1);
+                tF += pa;
+                tF1 += pa1;
+                vany = fmaxf(vany, v);
+                if (rg == 0 && collect) m = 2u * m + (v > 0.0f ? 1u : 0u);
+              }
+            F[rg] += double(tF);
+            F1[rg] += double(tF1);
+            if (rg == 0 && scol && m) {
+              int j = int(atomicAdd(&s_cnt[w * kListRows + c16], uint32_t(__builtin_popcount(m))));
+              for (int f = 0; f < 4; ++f)
+                for (int r = 0; r < 4; ++r)
+                  if ((m >> (4 * f + r)) & 1u) {
+                    if (j < lcap) {
+                      ldot[j] = acc[f][r];
+                      lkb[j] = kb;
+                    }
+                    ++j;
+                  }
+            }
           }
         }
-        const float Fs = sum_groups(float(F));
-        const float F1s = sum_groups(float(F1));
-        if (spk && g == 0) {
-          s_pF[w * kBlock + sl] = Fs;
-          s_pF1[w * kBlock + sl] = F1s;
+        if (__ballot(vany > 0.0f) != 0 && lane == 0) atomicOr(&s_bits[kb >> 5], 1u << (kb & 31));
+      }
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        if (rg < ngroups) {
+          const int sl = 16 * rg + c16;
+          const float Fs = sum_groups(float(F[rg]));
+          const float F1s = sum_groups(float(F1[rg]));
+          if (sl < nneed && g == 0) {
+            s_pF[w * kBlock + sl] = Fs;
+            s_pF1[w * kBlock + sl] = F1s;
+          }
         }
       }
       __syncthreads();  // partial sums and lists complete
@@ -437,8 +469,7 @@ hipError_t launch_td(const SelectParams& p, size_t lds, hipStream_t s) {
 }  // namespace
 
 size_t refine_lds_bytes(const Dims& d, bool bf16, int lcap) {
-  (void)bf16;  // K is read from global memory: the LDS does not depend on the type
-  return size_t(exact_layout(d.nKB, lcap).total);
+  return size_t(exact_layout(d.nKB, lcap, d.D * (bf16 ? 2 : 4)).total);
 }
 
 int refine_list_capacity(const Dims& d, bool bf16, size_t max_lds) {
