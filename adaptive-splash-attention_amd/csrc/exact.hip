@@ -93,11 +93,18 @@ __device__ __forceinline__ void pow_pair(float v, float a, float& pa, float& pa1
 // One safeguarded Newton step from tau, where f(tau) = f and
 // f'(tau) = -a F1: the bracket end on tau's side of the root moves to tau;
 // a step that leaves the open bracket (or F1 = 0) is replaced by bisection.
+// For a >= 1 (alpha <= 2) the terms of F1 are bounded, so a step below
+// half an ulp of tau means tau is the root to float precision: it is
+// returned unchanged (the caller stops) instead of being taken for a step
+// out of the bracket, which would restart a bisection from the bracket's
+// width.  For a < 1 a key with u -> 0+ makes F1 unbounded while f may
+// still be far from 0, so the bisection safeguard stays.
 __device__ __forceinline__ float newton_step(float tau, float f, float F1, float a, float& lo,
                                              float& hi) {
   if (f >= 0.0f) lo = tau;
   else hi = tau;
   const float nt = tau + f / (a * F1);
+  if (nt == tau && a >= 1.0f) return tau;
   return (nt > lo && nt < hi) ? nt : 0.5f * (lo + hi);
 }
 
