@@ -98,8 +98,10 @@ def _time(fn, warmup: int, trials: int) -> tuple[float, float]:
 def run_config(B: int, H: int, N: int, d: int, alpha: float = 1.5, k_keep: int = 8,
                dtype: torch.dtype = torch.float32, baseline: str = "entmax",
                backward: bool = False, input_scale: float = 0.1, warmup: int = 3,
-               trials: int = 10, seed: int = 42) -> dict:
-    """Benchmark one [B, H, N, d] configuration; returns the notebook's fields."""
+               trials: int = 10, seed: int = 42, tau_mode: str = "reference") -> dict:
+    """Benchmark one [B, H, N, d] configuration; returns the notebook's fields.
+    tau_mode="exact" makes splash attention compute dense alpha-entmax, so
+    against the "entmax" baseline the error fields measure parity."""
     dev = torch.device("cuda")
     g = torch.Generator().manual_seed(seed)
     Q, K, V, dO = (torch.randn(B, H, N, d, generator=g).mul_(input_scale).to(dtype).to(dev)
@@ -118,7 +120,8 @@ def run_config(B: int, H: int, N: int, d: int, alpha: float = 1.5, k_keep: int =
                     fn(Q, K, V)
         return step
 
-    sp = lambda q, k, v: splash_attention(q, k, v, idx, idx, alpha, k_keep, sm_scale)
+    sp = lambda q, k, v: splash_attention(q, k, v, idx, idx, alpha, k_keep, sm_scale,
+                                          tau_mode=tau_mode)
     dn = lambda q, k, v: dense(q, k, v, alpha, sm_scale)
     t_dense, m_dense = _time(make(dn), warmup, trials)
     t_splash, m_splash = _time(make(sp), warmup, trials)
@@ -131,7 +134,7 @@ def run_config(B: int, H: int, N: int, d: int, alpha: float = 1.5, k_keep: int =
     return {
         "config_name": f"{B}x{H}x{N}x{d}", "B": B, "H": H, "NQ": N, "NK": N, "d": d,
         "alpha": alpha, "k_keep": k_keep, "dtype": str(dtype).replace("torch.", ""),
-        "baseline": baseline, "pass": "fwd+bwd" if backward else "fwd",
+        "baseline": baseline, "tau_mode": tau_mode, "pass": "fwd+bwd" if backward else "fwd",
         "vanilla_time": round(t_dense, 4), "splash_time": round(t_splash, 4),
         "speedup": round(t_dense / t_splash, 3),
         "mse_error": mse, "max_error": max_err, "cosine_similarity": cos,
@@ -161,6 +164,8 @@ def build_parser() -> argparse.ArgumentParser:
     ap.add_argument("--dtype", choices=["fp32", "bf16"], default="fp32")
     ap.add_argument("--baseline", choices=sorted(BASELINES), default="entmax")
     ap.add_argument("--backward", action="store_true", help="time forward + backward")
+    ap.add_argument("--tau-mode", choices=["reference", "exact"], default="reference",
+                    help="exact: the alpha-entmax threshold over the whole row")
     ap.add_argument("--input-scale", type=float, default=0.1)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--trials", type=int, default=10)
@@ -175,7 +180,7 @@ def main(argv=None) -> list[dict]:
     results = []
     for B, H, N, d in configs:
         r = run_config(B, H, N, d, args.alpha, args.k_keep, dtype, args.baseline, args.backward,
-                       args.input_scale, args.warmup, args.trials)
+                       args.input_scale, args.warmup, args.trials, tau_mode=args.tau_mode)
         results.append(r)
         if args.json:
             print(json.dumps(r), flush=True)

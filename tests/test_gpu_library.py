@@ -59,3 +59,16 @@ def test_benchmark_cli_fields(dev, baseline, backward):
     assert r["splash_time"] > 0 and r["vanilla_time"] > 0
     assert -1.0 <= r["cosine_similarity"] <= 1.0 + 1e-6
     assert r["mse_error"] >= 0 and r["max_error"] >= 0
+
+
+def test_benchmark_cli_exact_mode_matches_dense_entmax(dev):
+    """With tau_mode="exact" splash attention computes dense alpha-entmax,
+    so against the CLI's dense "entmax" baseline (float32, 40 bisection
+    steps) the notebook's error fields become a parity readout."""
+    from splash_attention import benchmark
+
+    print("[lib] benchmark cli exact mode", flush=True)
+    r = benchmark.run_config(1, 2, 256, 64, 1.5, 8, torch.float32, "entmax", False,
+                             input_scale=1.0, warmup=1, trials=2, tau_mode="exact")
+    assert r["tau_mode"] == "exact"
+    assert r["max_error"] <= 1e-5 and r["cosine_similarity"] > 1 - 1e-9, r

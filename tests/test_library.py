@@ -49,3 +49,5 @@ def test_benchmark_cli_parsing():
     args = benchmark.build_parser().parse_args(["--config", "2x2x256x64", "--baseline", "vanilla",
                                                 "--backward", "--dtype", "bf16"])
     assert args.config == [(2, 2, 256, 64)] and args.baseline == "vanilla" and args.backward
+    assert args.tau_mode == "reference"
+    assert benchmark.build_parser().parse_args(["--tau-mode", "exact"]).tau_mode == "exact"
