@@ -296,3 +296,35 @@ def test_exact_mode_c5_full():
     idx = causal_idx(B * H, N)
     _exact_full("c5", Q, K, V, dO, idx, idx, 1.25, 128, 128 ** -0.5,
                 ((3, 0), (3, 16384), (5, 32704)))
+
+
+@pytest.mark.parametrize("grad_mode", ["reference", "entmax"])
+def test_exact_mode_backward_vs_oracle_at_gpu_state(grad_mode):
+    """Both gradient modes after an exact-mode forward against the C oracle's
+    backward evaluated at the GPU's taus and CSR (the exact mode's mask,
+    top-k union plus support blocks): 1e-5 (fp32).  Few rows over a long
+    key range, so the mask holds blocks outside the top-k union."""
+    import splash_attention as sa
+
+    dev = torch.device("cuda:0")
+    B, H, NQ, NK, d, k, alpha, scale = 1, 2, 72, 1024, 64, 2, 1.5, 0.05
+    Q, K, V, dO = make_inputs(B, H, NQ, NK, d, seed=13)
+    BH = B * H
+    qidx = torch.full((BH, NQ), NK - 1, dtype=torch.int32)
+    qidx[:, 40:] = torch.arange(600, 632, dtype=torch.int32)  # partly causal rows
+    kidx = causal_idx(BH, NK)
+    print(f"[exact] backward {grad_mode} vs oracle at GPU state", flush=True)
+    q, kk, v, qi, ki = sa.ops.check_inputs(*(t.to(dev) for t in (Q, K, V, qidx, kidx)))
+    out, st = sa.ops.splash_forward(q, kk, v, qi, ki, alpha, k, scale, tau_mode="exact")
+    grads = sa.ops.splash_backward(q, kk, v, qi, ki, out, dO.to(dev), st, alpha, k, scale,
+                                   grad_mode)
+    torch.cuda.synchronize()
+    topk = orc.forward(np32(Q), np32(K), np32(V), qidx.numpy(), kidx.numpy(), alpha, scale,
+                       k).mask.astype(bool)
+    assert (st.mask.cpu().numpy().astype(bool) & ~topk).sum() > 0  # support blocks were added
+    want = orc.backward(np32(Q), np32(K), np32(V), qidx.numpy(), kidx.numpy(), np32(dO), alpha,
+                        scale, st.taus.cpu().numpy(), st.q_ptr.cpu().numpy(),
+                        st.q_list.cpu().numpy(), 1 if grad_mode == "reference" else 0)
+    for gname, g, w in zip(("dQ", "dK", "dV"), grads, want):
+        e = assert_close(f"{grad_mode}: {gname}", np32(g), w, 1e-5)
+        print(f"  {gname} {e:.2e}", flush=True)
