@@ -39,14 +39,15 @@
 //      the key blocks where some row had u > 0 in it join the mask.
 //
 // One 256-thread block per (batch*head, 64-query block).  In step 1 wave w
-// owns rows 16w..16w+15.  The rows that need sweeps (about 5 of 64 at the
-// headline shape) are packed into groups of 16; in a sweep every wave
-// holds the packed rows group by group and takes every fourth visible key
-// tile, reading the tile's K fragments straight from global memory (a
-// head's K stays in L2), so no barrier separates the tiles and all four
-// waves compute.  The waves' partial sums and key lists (one per wave and
-// row) meet in LDS and are combined in a fixed order, so results do not
-// depend on timing.  Lane L holds keys 16f + 4g + r (g = L / 16) of its
+// owns rows 16w..16w+15, starting from the reference recurrence's tau when
+// it lies in the bracket.  The rows that need sweeps (about 5 of 64 at the
+// headline shape) are packed into groups of 16, their Q rows staged in LDS.
+// In a sweep every wave takes every fourth visible key tile, loads the
+// tile's K fragments once straight from global memory (a head's K stays in
+// L2) and multiplies them by every group's Q rows, so no barrier separates
+// the tiles, all four waves compute and K is read once per sweep.  The
+// waves' partial sums and key lists (one per wave and row) meet in LDS and
+// are combined in a fixed order, so results do not depend on timing.  Lane L holds keys 16f + 4g + r (g = L / 16) of its
 // row L % 16: the four lanes of a row hold identical per-row state, and
 // their partial sums are combined with sum_groups (bit-identical in all
 // four).
@@ -198,9 +199,9 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
 
   // ---- 2. full-row sweeps, for the rows that need them ----
   if (seen && !need && g == 0) p.taus[grow] = tau;  // final
-  // The rows that need sweeps are packed into the first waves (slot j of
-  // the packed list goes to wave j / 16, column j % 16), so that waves with
-  // no such row only help stage the K tiles.
+  // The rows that need sweeps are packed in row order: slot j of the
+  // packed list is row s_rows[j]; its state is read by wave j / 16, column
+  // j % 16 in the update phase, and by every wave in the sweeps.
   const int lrow = 16 * w + c16;  // the lane's row within the block
   const uint32_t wneed = uint32_t(__ballot(need)) & 0xffffu;  // lanes 0-15: one per row
   if (lane == 0) s_busy[8 + w] = __builtin_popcount(wneed);
@@ -264,10 +265,9 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
       }
     }
 
-    // Sweep-phase identity: every wave holds the packed rows group by group
-    // and takes every fourth visible key tile, reading its K fragments
-    // straight from global memory (a head's K stays in L2), so no barrier
-    // separates the tiles.  Partial sums meet in LDS in a fixed order.
+    // Sweep phase: every wave takes every fourth visible key tile and
+    // multiplies its K fragments by all packed row groups (below).  Partial
+    // sums meet in LDS in a fixed order.
     const int ngroups = (nneed + 15) >> 4;
     const T* Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
     const int32_t* kidx = p.k_idx + size_t(bh) * NK;
