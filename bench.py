@@ -17,7 +17,12 @@ second pass of K steps in which the library records HIP events around each
 launch on the launch stream (asa_profile_*); the roofline of each kernel
 uses its algorithmic FLOPs / bytes per launch.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+The line also carries the same step with the other tau mode
+(`exact_tau_mode`: the alpha-entmax threshold over the whole visible row,
+i.e. dense alpha-entmax attention computed block-sparsely), timed the same
+way; --tau-mode exact swaps the two.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--tau-mode reference|exact]
 """
 from __future__ import annotations
 
@@ -204,6 +209,8 @@ def main():
                          "the alpha-entmax threshold over the whole visible row")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense-baseline", action="store_true")
+    ap.add_argument("--no-exact-line", action="store_true",
+                    help="skip the exact_tau_mode entry (the other tau mode, same workload)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 plain device copies of 256 MiB (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -309,6 +316,29 @@ def main():
         "roofline": roof,
         "kernels": kernels,
     }
+    if not args.no_exact_line:
+        # the other tau mode on the same workload, timed the same way (the
+        # headline fields above are the --tau-mode run's)
+        other = "exact" if args.tau_mode == "reference" else "reference"
+
+        def step_other():
+            q.grad = k.grad = v.grad = None
+            out = sa.splash_attention(q, k, v, idx, idx, alpha, k_keep, scale, args.grad_mode,
+                                      other)
+            out.backward(dO)
+
+        for _ in range(args.warmup):
+            step_other()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step_other()
+        torch.cuda.synchronize()
+        oms = (time.perf_counter() - t0) * 1e3 / args.steps
+        line[f"{other}_tau_mode"] = {"ms_per_step": round(oms, 4),
+                                     "value": round(eff / (oms / 1e3) / 1e12, 3),
+                                     "unit": "TFLOP/s",
+                                     "what": "same workload and step with tau_mode=" + repr(other)}
     if not args.no_dense_baseline:
         try:
             dms = dense_gpu_baseline(Q, K, V, dO, alpha, scale)
