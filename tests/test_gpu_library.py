@@ -18,16 +18,21 @@ def test_opcheck_forward(dev, d, dtype):
     args = (Q.to(dev), K.to(dev), V.to(dev), None, None, 1.5, 8, 0.125, "entmax")
     torch.library.opcheck(library.forward_op, args,
                           test_utils=("test_schema", "test_faketensor"))
+    torch.library.opcheck(library.forward_op, args + ("exact",),
+                          test_utils=("test_schema", "test_faketensor"))
 
 
-@pytest.mark.parametrize("dtype,d", [(torch.float32, 64), (torch.bfloat16, 64),
-                                     (torch.float16, 40)])
-def test_compile_matches_eager(dev, dtype, d):
-    print(f"[lib] torch.compile aot_eager {dtype} d={d}", flush=True)
+@pytest.mark.parametrize("dtype,d,tau_mode", [(torch.float32, 64, "reference"),
+                                              (torch.bfloat16, 64, "reference"),
+                                              (torch.float16, 40, "reference"),
+                                              (torch.float32, 64, "exact")])
+def test_compile_matches_eager(dev, dtype, d, tau_mode):
+    print(f"[lib] torch.compile aot_eager {dtype} d={d} tau_mode={tau_mode}", flush=True)
     B, H, N = 1, 2, 192
     Q, K, V, dO = make_inputs(B, H, N, N, d, seed=12, dtype=dtype)
     idx = causal_idx(B * H, N).to(dev)
-    attn = sa.AdaptiveSplashAttention(head_dim=d, alpha=1.5, k_keep=16, sm_scale=0.125)
+    attn = sa.AdaptiveSplashAttention(head_dim=d, alpha=1.5, k_keep=16, sm_scale=0.125,
+                                      tau_mode=tau_mode)
 
     def run(fn):
         q, k, v = (t.to(dev).requires_grad_(True) for t in (Q, K, V))
