@@ -187,6 +187,20 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
   sp.kbounds = reinterpret_cast<int2*>(static_cast<char*>(workspace) + tkv_bytes(sh));
   if (int rc = select_cap(sh, scores != nullptr, &sp.cap)) return rc;
   sp.d = dims_of(sh);
+  if (sh.exact) {
+    // the refine pass's key lists: checked before anything is launched
+    int dev = 0, max_lds = 0;
+    if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (int rc = check_hip(hipDeviceGetAttribute(&max_lds,
+                                                 hipDeviceAttributeMaxSharedMemoryPerBlock, dev),
+                           "hipDeviceGetAttribute"))
+      return rc;
+    sp.lcap = asa::refine_list_capacity(sp.d, sh.bf16, size_t(max_lds));
+    if (sp.lcap < 0)
+      return fail(ASA_ERR_UNSUPPORTED,
+                  "exact tau mode needs %zu bytes of LDS per block, device has %d",
+                  asa::refine_lds_bytes(sp.d, sh.bf16, 0), max_lds);
+  }
   sp.q = q;
   sp.k = k;
   sp.scores = scores;
@@ -210,16 +224,6 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
   if (int rc = check_hip(e, "tau kernel launch")) return rc;
   if (sh.exact) {
     // exact threshold over the whole row; adds the support's key blocks
-    int dev = 0, max_lds = 0;
-    if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
-    if (int rc = check_hip(hipDeviceGetAttribute(&max_lds,
-                                                 hipDeviceAttributeMaxSharedMemoryPerBlock, dev),
-                           "hipDeviceGetAttribute"))
-      return rc;
-    sp.lcap = asa::refine_list_capacity(sp.d, sh.bf16, size_t(max_lds));
-    if (sp.lcap < 0)
-      return fail(ASA_ERR_UNSUPPORTED, "exact tau mode needs %zu bytes of LDS per block, device has %d",
-                  asa::refine_lds_bytes(sp.d, sh.bf16, 0), max_lds);
     asa::profile_begin("refine", s);
     e = asa::launch_refine(sp, sh.bf16, s);
     asa::profile_end(s);

@@ -159,8 +159,10 @@ const char *asa_last_error(void);
 int asa_query_sizes(const asa_problem *p, asa_sizes *out);
 
 /* Forward pass (reference: forward_splash, adasplashattention.cu:537-609):
- * score pass (QK^T on MFMA, top-k, tau, block mask), CSR compaction and the
- * block-sparse weighted sum.  Writes `out` and every non-NULL field of *st.
+ * score pass (QK^T on MFMA, top-k, tau, block mask), with p->tau_mode ==
+ * ASA_TAU_EXACT the exact-threshold pass (tau over the whole row, support
+ * blocks added to the mask), CSR compaction and the block-sparse weighted
+ * sum.  Writes `out` and every non-NULL field of *st.
  * `workspace` must hold asa_sizes.workspace bytes.  `stream` is a
  * hipStream_t (NULL: the null stream).                                     */
 int asa_forward(const asa_problem *p, const void *q, const void *k, const void *v,
