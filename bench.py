@@ -50,10 +50,12 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # HBM bytes per launch of each kernel at this workload, measured with
 # rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), the factors a plain
 # 256 MiB device copy gives (profiles/headline_hbm_traffic.md).
+# refine (exact tau mode only) from the same two passes over
+# `bench.py --tau-mode exact` (profiles/exact_mode_kernel_stats.md).
 # bwd_dq_sparse includes the position map it writes for bwd_dkdv_sparse;
 # bwd_dq and bwd_dkdv are the dense passes (run when no support masks were
 # recorded).
-HBM_TRAFFIC = {'bounds': 1108138, 'select': 103819594, 'tau': 34748757, 'compact': 2751317, 'forward': 207541610, 'bwd_dq_sparse': 248106329, 'bwd_dkdv_sparse': 277114956, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
+HBM_TRAFFIC = {'refine': 74134323, 'bounds': 1108138, 'select': 103819594, 'tau': 34748757, 'compact': 2751317, 'forward': 207541610, 'bwd_dq_sparse': 248106329, 'bwd_dkdv_sparse': 277114956, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
 
 
 def effective_flops(B, H, N, d):
