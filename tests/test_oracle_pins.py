@@ -293,10 +293,12 @@ def test_reference_gradient_is_fixed_tau_gradient(alpha):
                                    rtol=2e-5, atol=2e-7)
 
 
-@pytest.mark.parametrize("alpha", [1.5, 2.0, 1.25])
+@pytest.mark.parametrize("alpha", [1.5, 2.0, 1.25, 2.5])
 def test_entmax_gradient_is_dense_entmax_gradient(alpha):
     """Mode 0 with the exact tau and k >= N is the gradient of dense exact
-    alpha-entmax attention (tau re-solved at every perturbed point)."""
+    alpha-entmax attention (tau re-solved at every perturbed point).  At
+    alpha = 2.5 the Jacobian weight P^(2-alpha) has a negative exponent:
+    dense.attention_backward must keep it on the support only."""
     Q, K, V, dO, idx = _rand_problem(3, BH=1, N=72)
     scale = 0.125
     vis = (idx[:, None, :] <= idx[:, :, None])
