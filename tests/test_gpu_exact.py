@@ -105,6 +105,7 @@ CASES = [
     ("fp32_alpha_general", 1, 1, 128, 128, 64, 1.7, 8, 0.125, torch.float32),
     ("fp32_alpha_above_2", 1, 1, 128, 128, 64, 2.5, 8, 0.125, torch.float32),
     ("fp32_ragged_k1", 2, 1, 100, 150, 64, 1.5, 1, 0.125, torch.float32),
+    ("fp32_negative_scale", 1, 1, 128, 128, 64, 1.5, 8, -0.125, torch.float32),
     ("bf16_k32", 1, 2, 512, 512, 64, 1.5, 32, 0.125, torch.bfloat16),
     ("bf16_d128_a125", 1, 2, 256, 256, 128, 1.25, 64, 128 ** -0.5, torch.bfloat16),
 ]
