@@ -238,8 +238,11 @@ template <int M>
 __device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
   if constexpr (M == 1) return dpp_mov<0xB1>(v);
   else if constexpr (M == 2) return dpp_mov<0x4E>(v);
+  else if constexpr (M == 3) return dpp_mov<0x1B>(v);
   else if constexpr (M == 4) return dpp_mov<0x1B>(dpp_mov<0x141>(v));  // (i^7)^3
+  else if constexpr (M == 7) return dpp_mov<0x141>(v);
   else if constexpr (M == 8) return dpp_mov<0x141>(dpp_mov<0x140>(v)); // (i^15)^7
+  else if constexpr (M == 15) return dpp_mov<0x140>(v);
   else return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), M, 64));
 }
 template <int M>

@@ -39,7 +39,14 @@ struct SelectParams {
   int2* kbounds;          // workspace: (min, max) position per key block, [BH * nKB]
   int cap;                // candidate keys per row in LDS (select_capacity)
   int lcap;               // refine pass: listed keys per row in LDS (refine_list_capacity)
+  uint32_t* status;       // optional per-call status word (kStatus* bits), zeroed by bounds_kernel
 };
+
+// Bits of the per-call status word.  Bits 8-15 hold the largest number of
+// overflow rounds a select block ran (saturating at 255): information only.
+// Values as ASA_STATUS_* in adasplash.h.
+constexpr uint32_t kStatusSelectRounds = 1u;  // select stopped at its proven round bound
+constexpr uint32_t kStatusRefineSweeps = 2u;  // exact-mode refine stopped at its sweep cap
 
 struct CompactParams {
   int BH, nQB, nKB;

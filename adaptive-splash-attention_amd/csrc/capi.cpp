@@ -210,6 +210,7 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
   sp.mask = st->mask;
   sp.topk_idx = st->topk_idx;
   sp.topk_val = st->topk_val;
+  sp.status = st->status;
   asa::profile_begin("bounds", s);
   hipError_t eb = asa::launch_bounds(sp, s);
   asa::profile_end(s);

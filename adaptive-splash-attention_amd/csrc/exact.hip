@@ -194,6 +194,9 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
       }
     }
   }
+  // a row still stepping after kMaxTopkSteps keeps its last iterate; the
+  // caller can see that in the status word
+  if (__ballot(busy) != 0 && lane == 0 && p.status) atomicOr(p.status, kStatusRefineSweeps);
   // rows whose k-th value is inside the support need the full row
   const bool need = seen && am1 * tk[size_t(k - 1) * rows] > tau;
 
@@ -404,10 +407,12 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
             }
           }
         }
+        if (__ballot(lbusy) != 0 && lane == 0 && p.status) atomicOr(p.status, kStatusRefineSweeps);
         if (listed) done = true;
       }
       if (!done) {
         if (fabsf(f) <= kTol || sw + 1 == kMaxSweeps) {
+          if (!(fabsf(f) <= kTol) && p.status) atomicOr(p.status, kStatusRefineSweeps);
           done = true;
         } else {
           const float nt = newton_step(tau, f, F1s, a, lo, hi);

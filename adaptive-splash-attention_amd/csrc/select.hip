@@ -77,10 +77,6 @@ __device__ __forceinline__ float opaque_inf() {
   asm("" : "+v"(v));
   return v;
 }
-// m = 2 m + (x >= t || isnan(x)).
-__device__ __forceinline__ uint32_t shift_in_nlt(uint32_t m, float x, float t) {
-  return m + m + (x < t ? 0u : 1u);
-}
 // c + (x >= t).
 __device__ __forceinline__ uint32_t count_ge(uint32_t c, float x, float t) {
   return c + (x >= t ? 1u : 0u);
@@ -124,6 +120,42 @@ __device__ __forceinline__ void segment_sort_desc(uint64_t (&v)[8], int lane) {
             const bool sw = desc ? (a < b) : (a > b);
             v[p] = sw ? b : a;
             v[pp] = sw ? a : b;
+          }
+        }
+      }
+    });
+  });
+}
+
+// Descending sort of independent segments of 8*LS 32-bit values, no
+// payload: lanes [s*LS, (s+1)*LS) hold segment s, element e = (lane % LS) * 8
+// + p in v[p].  Bitonic network in the form where every comparator puts the
+// larger value first: the first step of each merge compares e with its
+// mirror e ^ (size - 1), the later steps e with e ^ j.  One max and one min
+// per in-lane pair; a lane move, max or min and a select per element across
+// lanes.
+template <int LS>
+__device__ __forceinline__ void segment_sort_desc32(uint32_t (&v)[8], int lane) {
+  const int i = lane & (LS - 1);
+  static_for<1, ilog2(8 * LS) + 1>([&](auto sc) {
+    constexpr int size = 1 << decltype(sc)::value;
+    static_for<0, decltype(sc)::value>([&](auto jc) {
+      constexpr int j = (size >> 1) >> decltype(jc)::value;
+      constexpr bool mirror = j == (size >> 1);
+      if constexpr (j >= 8) {
+        // partner lane i ^ M, element 7 - p (mirror) or p
+        constexpr int M = mirror ? (size - 1) >> 3 : j >> 3;
+        const bool lower = (i & (mirror ? (size >> 4) : (j >> 3))) == 0;
+        uint32_t o[8];
+        for (int p = 0; p < 8; ++p) o[p] = lane_xor<M>(v[mirror ? 7 - p : p]);
+        for (int p = 0; p < 8; ++p) v[p] = lower ? max(v[p], o[p]) : min(v[p], o[p]);
+      } else {
+        for (int p = 0; p < 8; ++p) {
+          const int pp = mirror ? (p ^ (size - 1)) : (p ^ j);
+          if (pp > p) {
+            const uint32_t a = v[p], b = v[pp];
+            v[p] = max(a, b);
+            v[pp] = min(a, b);
           }
         }
       }
@@ -255,45 +287,78 @@ __device__ __forceinline__ float sweep_floor(float th, bool exact, float scale) 
 }
 
 
-// acc[b >> 2][b & 3] for a per-lane index b in [0, 16): a select tree on
-// the index bits instead of a dynamically indexed register array.
-__device__ __forceinline__ float pick16(const f32x4 (&acc)[4], int b) {
-  const bool b2 = (b & 4) != 0, b3 = (b & 8) != 0;
-  f32x4 x;
-  for (int r = 0; r < 4; ++r) {
-    const float lo = b2 ? acc[1][r] : acc[0][r];
-    const float hi = b2 ? acc[3][r] : acc[2][r];
-    x[r] = b3 ? hi : lo;
-  }
-  const float y0 = (b & 1) ? x[1] : x[0];
-  const float y1 = (b & 1) ? x[3] : x[2];
-  return (b & 2) ? y1 : y0;
-}
-
 enum SweepMode : int {
   kRawDots = 0,     // MFMA dot products, scale > 0: filters on raw dots
   kExactScores = 1, // MFMA dot products converted to exact scores (scale <= 0)
   kGivenScores = 2  // caller-given scores
 };
 
-// LDS layout, shared by the kernel and the host-side size query.
+// One wave's quarter of a 64-key tile (keys 16 w .. 16 w + 15) as MFMA A
+// operands, loaded straight from global memory (L2) into registers: lane
+// (c, g) holds key 16 w + c at the head-dimension slots that rows_x_frag
+// gives lane group g.  product() forms, for each of the four 16-row groups
+// cb of the query block, the scores of the quarter's keys against rows
+// 16 cb + c with the same operands in the same accumulation order as the
+// attention passes' rows_x_frag, so every score is bit-identical to theirs.
+// acc[cb][r] is the score of key 16 w + 4 g + r and row 16 cb + c.
+template <typename T, int D> struct KQuarter;
+template <int D> struct KQuarter<u16, D> {
+  bf16x8 a[D / 32];
+  // Keys >= NK read key 0 instead: they lie in partially visible tiles,
+  // where the visibility test discards their scores, so no zeroing (and no
+  // wait for the load where it is issued) is needed.
+  __device__ __forceinline__ void load(const u16* Kb, int key, int NK, int g) {
+    const u16* src = Kb + size_t(key < NK ? key : 0) * D + 8 * g;
+    for (int s = 0; s < D / 32; ++s) a[s] = *reinterpret_cast<const bf16x8*>(src + 32 * s);
+  }
+  __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<u16, D> (&qf)[4]) const {
+    for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < D / 32; ++s)
+      for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma(a[s], qf[cb].v[s], acc[cb]);
+  }
+};
+template <int D> struct KQuarter<float, D> {
+  f32x4 a[D / 16];
+  __device__ __forceinline__ void load(const float* Kb, int key, int NK, int g) {
+    const float* src = Kb + size_t(key < NK ? key : 0) * D + 4 * g;
+    for (int j = 0; j < D / 16; ++j) a[j] = *reinterpret_cast<const f32x4*>(src + 16 * j);
+  }
+  __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<float, D> (&qf)[4]) const {
+    for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < D / 16; ++j)
+      for (int cb = 0; cb < 4; ++cb)
+        for (int r = 0; r < 4; ++r) acc[cb] = mfma(a[j][r], qf[cb].v[j][r], acc[cb]);
+  }
+};
+
+// LDS layout, shared by the kernel and the host-side size query.  The class
+// maxima exchanged between the sweeps share their bytes with the candidate
+// lists (they are read before the first candidate is written).
 struct SelLayout {
-  int tiles, tk, cand, tkey, cnt, ctl, bits, vlist, total;
+  int cand, cm, scm, scr, tk, tkey, fl, cnt, ctl, bits, vlist, total;
 };
 __host__ __device__ inline int align_up(int x, int a) { return (x + a - 1) / a * a; }
-__host__ __device__ inline SelLayout sel_layout(int k, int cap, int nKB, int D, int tbytes,
-                                                bool given_scores) {
+__host__ __device__ inline int classes_per_lane(int k) { return k <= 32 ? 2 : 4; }
+// Sweep-2 value scratch: 16 floats per lane, the lane's 16-byte chunk j
+// stored at chunk j ^ ((lane >> 1) & 3), so that the 8 lanes a 16-byte
+// store serves per cycle hit distinct banks.
+constexpr int kScrStride = 16;
+__host__ __device__ inline SelLayout sel_layout(int k, int cap, int nKB) {
   SelLayout l;
-  const int rs = tbytes == 2 ? D + 8 : D + 4;
-  const int tiles = given_scores ? 0 : 2 * kBlock * rs * tbytes;
-  const int tk = k * kWave * 4;
-  // the sorted top-k values reuse the tile buffers once the sweeps are over
-  const int a = align_up(tiles > tk ? tiles : tk, 16);
-  l.tiles = 0;
-  l.tk = 0;
-  l.cand = a;
-  l.tkey = l.cand + kBlock * cap * 8;
-  l.cnt = l.tkey + kBlock * 8;
+  const int R = classes_per_lane(k);
+  l.scm = 64 * R;  // floats per row of the class-maxima exchange
+  const int cand_bytes = kBlock * cap * 8;
+  const int cm_bytes = kBlock * l.scm * 4;
+  const int scr_bytes = kThreads * kScrStride * 4;
+  const int tk_bytes = k * kBlock * 4;
+  l.cand = 0;
+  l.cm = 0;
+  // the value scratch (sweeps) and the sorted top-k values (emission) share bytes
+  l.scr = align_up(cand_bytes > cm_bytes ? cand_bytes : cm_bytes, 16);
+  l.tk = l.scr;
+  l.tkey = l.scr + align_up(scr_bytes > tk_bytes ? scr_bytes : tk_bytes, 16);
+  l.fl = l.tkey + kBlock * 8;
+  l.cnt = l.fl + kBlock * 4;
   l.ctl = l.cnt + kBlock * 4;
   l.bits = l.ctl + 16;
   l.vlist = l.bits + align_up((nKB + 31) / 32 * 4, 16);
@@ -301,37 +366,58 @@ __host__ __device__ inline SelLayout sel_layout(int k, int cap, int nKB, int D, 
   return l;
 }
 
+// Overflow rounds a row can need.  Round 0 stores the first `cap` of its c_0
+// candidates; the k-th best stored key T_1 then excludes at least the cap - k
+// stored keys below it, so round 1 finds c_1 <= c_0 - (cap - k) keys >= T_1,
+// and so on: with c_0 <= NK, at most 2 + (NK - cap) / (cap - k) rounds end
+// with every candidate stored.
+__host__ __device__ inline int select_round_bound(int NK, int k, int cap) {
+  return 2 + (NK > cap ? (NK - cap) / (cap - k) + 1 : 0);
+}
+
+// Score pass of one (batch, head) and 64-row query block; 4 waves.  Wave w
+// multiplies its quarter of every visible key tile with all 64 rows (no LDS
+// staging, no barrier inside a sweep); lane (c, g) sees rows 16 cb + c and
+// keys 16 w + 4 g + r of each tile.  R class maxima per (lane, row, r)
+// give 64 R classes per row.
 template <typename T, int D, int MODE, int R>
 __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
   constexpr bool kExact = MODE != kRawDots;
   constexpr bool kTiles = MODE != kGivenScores;
+  constexpr int UR = R > 2 ? R : 2;  // sweep-1 unroll: class of a tile = ordinal % R
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int k = p.d.k, NQ = p.d.NQ, NK = p.d.NK, nKB = p.d.nKB, nQB = p.d.nQB;
   const int cap = p.cap;
   const int nbw = (nKB + 31) >> 5;
-  const SelLayout lay = sel_layout(k, cap, nKB, D, int(sizeof(T)), !kTiles);
-  T* s_tiles = reinterpret_cast<T*>(smem + lay.tiles);
-  float* s_tk = reinterpret_cast<float*>(smem + lay.tk);
+  const SelLayout lay = sel_layout(k, cap, nKB);
   uint64_t* s_cand = reinterpret_cast<uint64_t*>(smem + lay.cand);
+  float* s_cm = reinterpret_cast<float*>(smem + lay.cm);
+  float* s_tk = reinterpret_cast<float*>(smem + lay.tk);
   uint64_t* s_tkey = reinterpret_cast<uint64_t*>(smem + lay.tkey);
+  float* s_fl = reinterpret_cast<float*>(smem + lay.fl);
   uint32_t* s_cnt = reinterpret_cast<uint32_t*>(smem + lay.cnt);
   uint32_t* s_ctl = reinterpret_cast<uint32_t*>(smem + lay.ctl);
   uint32_t* s_bits = reinterpret_cast<uint32_t*>(smem + lay.bits);
   int32_t* s_vlist = reinterpret_cast<int32_t*>(smem + lay.vlist);
-  constexpr int kTileElems = kBlock * KStage<T, D>::kRs;
 
   const int t = threadIdx.x, w = t >> 6, L = t & 63, g = L >> 4, c = L & 15;
+  float* s_scr = reinterpret_cast<float*>(smem + lay.scr) + t * kScrStride;  // this lane's
+  const int scr_sw = ((L >> 1) & 3) << 2;  // chunk swizzle, in floats
   const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
   const int qb = nQB - 1 - task % nQB, bh = task / nQB, q0 = qb * kBlock;
-  const int lq = 16 * w + c;  // this lane's row within the block
-  const bool rowok = q0 + lq < NQ;
-  const size_t grow = size_t(bh) * NQ + q0 + lq;  // global row (valid if rowok)
-  const int qpos = rowok ? p.q_idx[grow] : 0;
+  const size_t grow0 = size_t(bh) * NQ + q0;  // global index of the block's row 0
   const float scale = p.d.scale;
 
+  // The lane's rows 16 cb + c.
+  bool rowok[4];
+  int qpos[4];
+  for (int cb = 0; cb < 4; ++cb) {
+    rowok[cb] = q0 + 16 * cb + c < NQ;
+    qpos[cb] = rowok[cb] ? p.q_idx[grow0 + 16 * cb + c] : 0;
+  }
   // Position range of the valid rows of the whole block (lane L <-> row L).
   const bool lv = q0 + L < NQ;
-  const int lpos = lv ? p.q_idx[size_t(bh) * NQ + q0 + L] : 0;
+  const int lpos = lv ? p.q_idx[grow0 + L] : 0;
   const int qmax_blk = wave_max(lv ? lpos : INT_MIN);
   const int qmin_blk = wave_min(lv ? lpos : INT_MAX);
 
@@ -363,110 +449,129 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
   __syncthreads();
   const int nvis = int(s_ctl[1]);
 
-  RowFrag<T, D> qf;  // Q^T operand: the lane's query row (column c of the products)
+  RowFrag<T, D> qf[4];  // Q^T operands: row 16 cb + c in column c of the products
   const T* Kb = nullptr;
   if constexpr (kTiles) {
-    qf.load(static_cast<const T*>(p.q) + grow * D, rowok, L);
+    for (int cb = 0; cb < 4; ++cb)
+      qf[cb].load(static_cast<const T*>(p.q) + (grow0 + 16 * cb + c) * D, rowok[cb], L);
     Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
   }
-  KStage<T, D> ks;
+  const int kq0 = 16 * w + c;  // the lane's A-operand key within a tile
 
-  // Sweep values of one key block for the lane's row: acc[f][r] is the value
-  // of key 16f + 4g + r.  Bit 4f + r of the returned mask is set where that
-  // key is visible to a valid row; invisible values are set to -inf.
-  auto sweep_values = [&](const T* buf, int kt, int vis, f32x4 (&acc)[4]) -> uint32_t {
-    const int kbase = kt * kBlock;
-    if constexpr (MODE == kGivenScores) {
-      for (int f = 0; f < 4; ++f)
-        for (int r = 0; r < 4; ++r) {
-          const int key = kbase + 16 * f + 4 * g + r;
-          acc[f][r] = rowok && key < NK ? clamp_score(p.scores[grow * NK + key]) : 0.0f;
-        }
-    } else {
-      rows_x_frag<D>(acc, buf, qf, L);
-      if constexpr (MODE == kExactScores)
-        for (int f = 0; f < 4; ++f)
-          for (int r = 0; r < 4; ++r) acc[f][r] = clamp_score(acc[f][r] * scale);
-    }
-    uint32_t vb = rowok ? 0xffffu : 0u;
-    if (vis == 1) {
-      for (int f = 0; f < 4; ++f)
-        for (int r = 0; r < 4; ++r) {
-          const int key = kbase + 16 * f + 4 * g + r;
-          const int kp = key < NK ? kidx[key] : INT_MAX;
-          if (!(key < NK && kp <= qpos)) {
-            vb &= ~(1u << (4 * f + r));
-            acc[f][r] = -__builtin_inff();
-          }
-        }
-    }
-    return vb;
+  // One pass over the visible key blocks: body(u, kt, partial, visb, acc)
+  // for each, u = (ordinal of the block) % U known at compile time.  The K
+  // quarters of the next two tiles are in flight while a tile is used.  In
+  // partially visible tiles (partial = true), bit 4 cb + r of visb is
+  // cleared and acc set to -inf where key 16 w + 4 g + r is not visible to
+  // row 16 cb + c.  The first 64 list entries are held one per lane.
+  const int vl0 = L < nvis ? s_vlist[L] : 0;
+  auto entry = [&](int i) {
+    return i < kWave ? __builtin_amdgcn_readlane(vl0, i) : __builtin_amdgcn_readfirstlane(s_vlist[i]);
   };
-
-  // One pass over the visible key blocks: body(u, kt, vb, acc) for each, with
-  // u = (ordinal of the block) % U known at compile time.  The next tile is
-  // stored to the other LDS buffer and the one after it fetched into
-  // registers while the current tile is in use.
   auto sweep = [&](auto u_tag, auto&& body) {
     constexpr int U = decltype(u_tag)::value;
+    if (nvis == 0) return;  // block-uniform
+    KQuarter<T, D> kq[2];
+    auto fetch = [&](KQuarter<T, D>& f, int e) {
+      f.load(Kb, (e & 0xffffff) * kBlock + kq0, NK, g);
+    };
+    // The loads are unconditional (past the end of the list they repeat its
+    // last tile), so the number in flight is the same on every path and the
+    // waits before a tile's products cover that tile's loads only.
+    int ent[2] = {entry(0), entry(nvis > 1 ? 1 : 0)};  // the tiles in kq[0], kq[1]
     if constexpr (kTiles) {
-      if (nvis > 0) {
-        ks.load(Kb, (s_vlist[0] & 0xffffff) * kBlock, NK, t);
-        ks.store(s_tiles, t);
-      }
-      if (nvis > 1) ks.load(Kb, (s_vlist[1] & 0xffffff) * kBlock, NK, t);
-      __syncthreads();
+      // issued in the loop's order (kq[0]'s loads first), so that the
+      // loop head's wait is the same from the prologue and the back edge
+      fetch(kq[0], ent[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      fetch(kq[1], ent[1]);
+      __builtin_amdgcn_sched_barrier(0);
     }
     for (int i0 = 0; i0 < nvis; i0 += U) {
       static_for<0, U>([&](auto uc) {
         constexpr int u = decltype(uc)::value;
         const int i = i0 + u;
-        if (i < nvis) {
-          const int e = s_vlist[i];
-          const int kt = e & 0xffffff, vis = e >> 24;
-          const T* buf = s_tiles + (i & 1) * kTileElems;
-          f32x4 acc[4];
-          const uint32_t vb = sweep_values(buf, kt, vis, acc);
-          body(uc, kt, vb, acc);
-          if constexpr (kTiles) {
-            if (i + 1 < nvis) {
-              ks.store(s_tiles + ((i + 1) & 1) * kTileElems, t);
-              if (i + 2 < nvis) ks.load(Kb, (s_vlist[i + 2] & 0xffffff) * kBlock, NK, t);
+        const int e = ent[u & 1];
+        const int kt = e & 0xffffff;
+        const int kb0 = kt * kBlock + 16 * w + 4 * g;  // the lane's first key
+        f32x4 acc[4];
+        if constexpr (MODE == kGivenScores) {
+          for (int cb = 0; cb < 4; ++cb)
+            for (int r = 0; r < 4; ++r) {
+              const int key = kb0 + r;
+              acc[cb][r] = rowok[cb] && key < NK
+                               ? clamp_score(p.scores[(grow0 + 16 * cb + c) * NK + key])
+                               : 0.0f;
             }
-            __syncthreads();
+          ent[u & 1] = entry(i + 2 < nvis ? i + 2 : nvis - 1);
+        } else {
+          kq[u & 1].product(acc, qf);
+          ent[u & 1] = entry(i + 2 < nvis ? i + 2 : nvis - 1);
+          fetch(kq[u & 1], ent[u & 1]);
+          if constexpr (MODE == kExactScores)
+            for (int cb = 0; cb < 4; ++cb)
+              for (int r = 0; r < 4; ++r) acc[cb][r] = clamp_score(acc[cb][r] * scale);
+        }
+        if (i >= nvis) {  // padding of the last group of U tiles: nothing visible
+          for (int cb = 0; cb < 4; ++cb)
+            for (int r = 0; r < 4; ++r) acc[cb][r] = -__builtin_inff();
+          body(uc, kb0, std::true_type{}, 0u, acc);
+        } else if ((e >> 24) == 1) {  // wave-uniform
+          uint32_t visb = 0xffffu;
+          for (int r = 0; r < 4; ++r) {
+            const int key = kb0 + r;
+            const int kp = key < NK ? kidx[key] : INT_MAX;
+            for (int cb = 0; cb < 4; ++cb)
+              if (!(key < NK && kp <= qpos[cb])) {
+                visb &= ~(1u << (4 * cb + r));
+                acc[cb][r] = -__builtin_inff();
+              }
           }
+          body(uc, kb0, std::true_type{}, visb, acc);
+        } else {
+          body(uc, kb0, std::false_type{}, 0xffffu, acc);
         }
       });
     }
-    __syncthreads();
   };
 
   // ---------------- sweep 1: class maxima ----------------
-  float cm[16][R];
+  float cm[4][4 * R];
   const float pinf = opaque_inf();
-  for (int i = 0; i < 16; ++i)
-    for (int j = 0; j < R; ++j) cm[i][j] = -__builtin_inff();
-  sweep(std::integral_constant<int, R>{}, [&](auto uc, int, uint32_t, f32x4 (&acc)[4]) {
-    constexpr int u = decltype(uc)::value;
-    for (int f = 0; f < 4; ++f)
-      for (int r = 0; r < 4; ++r) cm[4 * f + r][u] = vmax(cm[4 * f + r][u], acc[f][r], pinf);
+  for (int cb = 0; cb < 4; ++cb)
+    for (int j = 0; j < 4 * R; ++j) cm[cb][j] = -__builtin_inff();
+  sweep(std::integral_constant<int, UR>{}, [&](auto uc, int, auto, uint32_t, f32x4 (&acc)[4]) {
+    constexpr int j = decltype(uc)::value % R;
+    for (int cb = 0; cb < 4; ++cb)
+      for (int r = 0; r < 4; ++r) cm[cb][r + 4 * j] = vmax(cm[cb][r + 4 * j], acc[cb][r], pinf);
   });
 
-  // Per row: a value x with at least k class maxima >= x (bisection between
-  // the smallest and largest class maximum), then the sweep-2 floor.
-  float floor_v;
+  // Exchange: row 16 cb + c's 64 R class maxima, 4 R from each of its 16
+  // lanes (4 waves x 4 lane groups), then wave w finds the floors of rows
+  // 16 w + c, lane group g holding classes [16 R g, 16 R (g + 1)).
+  for (int cb = 0; cb < 4; ++cb)
+    for (int r = 0; r < 4; ++r)
+      for (int j = 0; j < R; ++j)
+        s_cm[(16 * cb + c) * lay.scm + ((w * 4 + g) * 4 + r) * R + j] = cm[cb][r + 4 * j];
+  __syncthreads();
   {
+    const int row = 16 * w + c;
+    float v[16 * R];
+    for (int i = 0; i < 16 * R; i += 4) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(s_cm + row * lay.scm + 16 * R * g + i);
+      for (int j = 0; j < 4; ++j) v[i + j] = x[j];
+    }
+    // a value x with at least k class maxima >= x (bisection between the
+    // smallest and largest class maximum), then the sweep-2 floor
     float lo = __builtin_inff(), hi = -__builtin_inff();
     uint32_t nfin = 0;
-    for (int i = 0; i < 16; ++i)
-      for (int j = 0; j < R; ++j) {
-        const float v = cm[i][j];
-        nfin = count_ge(nfin, v, -3.0e38f);
-        if (v >= -3.0e38f) {
-          lo = fminf(lo, v);
-          hi = fmaxf(hi, v);
-        }
+    for (int i = 0; i < 16 * R; ++i) {
+      nfin = count_ge(nfin, v[i], -3.0e38f);
+      if (v[i] >= -3.0e38f) {
+        lo = fminf(lo, v[i]);
+        hi = fmaxf(hi, v[i]);
       }
+    }
     const int nf = group_sum(int(nfin));
     lo = group_min(lo);
     hi = group_max(hi);
@@ -475,68 +580,109 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
       for (int it = 0; it < 8; ++it) {
         const float mid = 0.5f * (lo + hi);
         uint32_t cnt = 0;
-        for (int i = 0; i < 16; ++i)
-          for (int j = 0; j < R; ++j) cnt = count_ge(cnt, cm[i][j], mid);
+        for (int i = 0; i < 16 * R; ++i) cnt = count_ge(cnt, v[i], mid);
         if (group_sum(int(cnt)) >= k) lo = mid;
         else hi = mid;
       }
       x = lo;
     }
     const float th = kExact ? x : (x == -__builtin_inff() ? x : clamp_score(x * scale));
-    floor_v = sweep_floor(th, kExact, scale);
+    // NaN marks a row that collects nothing (past NQ)
+    if (g == 0) s_fl[row] = q0 + row < NQ ? sweep_floor(th, kExact, scale) : __builtin_nanf("");
   }
+  __syncthreads();
 
   // ---------------- sweep 2 (and overflow rounds): candidates ----------------
-  uint64_t* my_cand = s_cand + size_t(lq) * cap;
-  bool take = rowok;  // this lane's row collects in the current round
-  uint64_t tkey = 0;  // exact key threshold of the row (rounds > 0)
+  // A key of row 16 cb + c is a candidate when visible and !(v < fl[cb]):
+  // with fl[cb] = -inf (the row's threshold is <= -10) every visible key is
+  // one.  NaN dots (score -10) always pass; where the threshold is above -10
+  // they cannot reach the top-k and only take a slot.  In rounds > 0 the
+  // candidate's key must also reach the row's exact threshold s_tkey.
+  // selection key of a stored candidate
+  auto raw_key = [&](uint64_t raw) {
+    const float v = __uint_as_float(uint32_t(raw));
+    return make_key(kExact ? v : clamp_score(v * scale), int(raw >> 32));
+  };
+  float fl[4];
+  int max_round = 0;
+  const int round_bound = select_round_bound(NK, k, cap);
   for (int round = 0;; ++round) {
-    sweep(std::integral_constant<int, 1>{}, [&](auto, int kt, uint32_t vb, f32x4 (&acc)[4]) {
-      // bit 4f + r <- value >= floor (or NaN), highest bit first
-      uint32_t cand = 0;
-      for (int f = 3; f >= 0; --f)
-        for (int r = 3; r >= 0; --r) cand = shift_in_nlt(cand, acc[f][r], floor_v);
-      cand &= take ? vb : 0u;
-      if (!__any(cand != 0)) return;
-      const int kbase = kt * kBlock + 4 * g;
-      // key of value b = 4f + r: score, index kbase + 16f + r
-      auto key_of = [&](int b) {
-        const float v = pick16(acc, b);
-        const float sc = kExact ? v : clamp_score(v * scale);
-        return make_key(sc, kbase + 16 * (b >> 2) + (b & 3));
-      };
-      if (round > 0) {
-        // exact key threshold: drop the candidates below it first
-        uint32_t c2 = cand;
-        while (c2) {
-          const int b = __builtin_ctz(c2);
-          c2 &= c2 - 1;
-          if (key_of(b) < tkey) cand &= ~(1u << b);
+    // fl = NaN marks a row that collects nothing this round
+    // A zero floor is held as -0, so that v - fl is +0 for both signed
+    // zeros v (with +0, -0 - +0 = -0 would read as v < fl).
+    // Rows with fl = -inf take every visible key (amask), whatever the sign
+    // of a NaN difference.
+    uint32_t cmask = 0, amask = 0;
+    for (int cb = 0; cb < 4; ++cb) {
+      fl[cb] = s_fl[16 * cb + c];
+      if (fl[cb] == 0.0f) fl[cb] = -0.0f;
+      if (!__builtin_isnan(fl[cb])) cmask |= 0xfu << (4 * cb);
+      if (fl[cb] == -__builtin_inff()) amask |= 0xfu << (4 * cb);
+    }
+    // Candidates are stored raw, (index << 32) | bits of the sweep value,
+    // and turned into selection keys when they are sorted.  Per tile, the
+    // lane's candidate bits m (bit 4 cb + r: key kb0 + r of row 16 cb + c)
+    // come branch-free, two instructions per score; the few lanes with
+    // candidates then park their 16 values in their LDS scratch and append
+    // one candidate per round (LDS atomic on the row's count), so the wave
+    // runs as many rounds as its busiest lane has candidates (about two at
+    // the headline shape) instead of visiting every slot.
+    auto collect = [&](int kb0, auto partial, uint32_t visb, f32x4 (&acc)[4], auto later) {
+      // bit 4 cb + r <- sign of v - fl: set where v < fl, so that the
+      // complement marks !(v < fl) (NaN differences have a clear sign bit)
+      uint32_t m = 0;
+      for (int cb = 3; cb >= 0; --cb)
+        for (int r = 3; r >= 0; --r)
+          m = __builtin_amdgcn_alignbit(m, __float_as_uint(acc[cb][r] - fl[cb]), 31);
+      m = (~m | amask) & cmask;
+      if constexpr (decltype(partial)::value) m &= visb;
+      if (m != 0u) {
+        for (int cb = 0; cb < 4; ++cb) *reinterpret_cast<f32x4*>(s_scr + ((4 * cb) ^ scr_sw)) = acc[cb];
+      }
+      while (m != 0u) {
+        const int b = __builtin_ctz(m);
+        m &= m - 1u;
+        const int row = 4 * (b & 12) + c, key = kb0 + (b & 3);
+        const float v = s_scr[b ^ scr_sw];
+        if constexpr (decltype(later)::value) {
+          if (make_key(kExact ? v : clamp_score(v * scale), key) < s_tkey[row]) continue;
         }
+        const uint32_t pos = atomicAdd(&s_cnt[row], 1u);
+        if (pos < uint32_t(cap))
+          s_cand[pos * kBlock + row] = (uint64_t(uint32_t(key)) << 32) | __float_as_uint(v);
       }
-      uint32_t pos = cand ? atomicAdd(&s_cnt[lq], uint32_t(__builtin_popcount(cand))) : 0u;
-      while (cand) {
-        const int b = __builtin_ctz(cand);
-        cand &= cand - 1;
-        const uint64_t key = key_of(b);
-        if (pos < uint32_t(cap)) my_cand[pos] = key;
-        ++pos;
-      }
-    });
-    // (the sweep ends with a block barrier: every count is final)
-    const bool over = rowok && s_cnt[lq] > uint32_t(cap);
-    if (__any(over) && L == 0) s_ctl[0] = uint32_t(round + 1);
+    };
+    if (round == 0)
+      sweep(std::integral_constant<int, 2>{}, [&](auto, int kb0, auto partial, uint32_t visb, f32x4 (&acc)[4]) {
+        collect(kb0, partial, visb, acc, std::false_type{});
+      });
+    else
+      sweep(std::integral_constant<int, 2>{}, [&](auto, int kb0, auto partial, uint32_t visb, f32x4 (&acc)[4]) {
+        collect(kb0, partial, visb, acc, std::true_type{});
+      });
     __syncthreads();
-    if (s_ctl[0] != uint32_t(round + 1) || round >= 64) break;  // block-uniform
-    // Rows that overflowed: the k-th best stored key becomes the row's exact
-    // threshold (every top-k key is >= it), the row's list restarts.
+    max_round = round;
+    // rows that overflowed: the k-th best stored key becomes the row's exact
+    // threshold (every top-k key is >= it) and the row's list restarts
+    if (t < kBlock && q0 + t < NQ && s_cnt[t] > uint32_t(cap)) s_ctl[0] = uint32_t(round + 1);
+    __syncthreads();
+    if (s_ctl[0] != uint32_t(round + 1)) break;  // block-uniform
+    if (round + 1 >= round_bound) {
+      // cannot happen (select_round_bound); reported, not looped on
+      if (t == 0 && p.status) atomicOr(p.status, kStatusSelectRounds);
+      break;
+    }
     for (int j = 0; j < 16; ++j) {
       const int r = 16 * w + j;
-      if (!(q0 + r < NQ && s_cnt[r] > uint32_t(cap))) continue;  // wave-uniform
+      const bool over = q0 + r < NQ && s_cnt[r] > uint32_t(cap);  // wave-uniform
+      if (!over) {
+        if (L == 0) s_fl[r] = __builtin_nanf("");
+        continue;
+      }
       uint64_t v[8];
       for (int pp = 0; pp < 8; ++pp) {
         const int e = (L & 31) * 8 + pp;
-        v[pp] = e < cap ? s_cand[size_t(r) * cap + e] : 0ull;
+        v[pp] = e < cap ? raw_key(s_cand[e * kBlock + r]) : 0ull;
       }
       segment_sort_desc<32>(v, L);
       // element k-1 lives in lane (k-1)/8, slot (k-1)%8 (both halves agree)
@@ -547,17 +693,17 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
       const uint64_t th =
           (static_cast<uint64_t>(__shfl(static_cast<uint32_t>(mine >> 32), src, kWave)) << 32) |
           __shfl(static_cast<uint32_t>(mine), src, kWave);
-      if (c == j) {
-        tkey = th;
-        floor_v = sweep_floor(key_score(th), kExact, scale);
+      if (L == 0) {
+        s_tkey[r] = th;
+        s_fl[r] = sweep_floor(key_score(th), kExact, scale);
       }
     }
     __syncthreads();  // all overflow reads of the lists and counts are done
-    take = rowok && s_cnt[lq] > uint32_t(cap);
+    if (t < kBlock && !__builtin_isnan(s_fl[t])) s_cnt[t] = 0u;
     __syncthreads();
-    if (take && g == 0) s_cnt[lq] = 0u;
-    // (the next sweep's prologue barrier orders this reset before any append)
   }
+  if (max_round > 0 && t == 0 && p.status)
+    atomicMax(p.status, (uint32_t(max_round > 255 ? 255 : max_round) << 8));
 
   // ---------------- select: sort each row's candidates ----------------
   // The top-k key blocks go into the block's mask bitmap: with at most 64
@@ -583,29 +729,106 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
     }
   };
   auto ncand = [&](int r) -> int { return (q0 + r < NQ) ? min(int(s_cnt[r]), cap) : 0; };
-  // Segments of LS lanes x 8 keys sort one row each; a group of 8 rows runs as
-  // one LS=8 pass (<= 64 keys per row), two LS=16 or four LS=32 passes.
+  // With top-k outputs requested: segments of LS lanes x 8 keys sort one
+  // row's (score, index) keys each; a group of 8 rows runs as one LS=8 pass
+  // (<= 64 keys per row), two LS=16 or four LS=32 passes.
   auto sort_rows = [&](auto ls_tag, int row0) {
     constexpr int LS = decltype(ls_tag)::value;
     const int r = row0 + L / LS, i = L & (LS - 1), n = ncand(r);
     uint64_t v[8];
     for (int pp = 0; pp < 8; ++pp) {
       const int e = i * 8 + pp;
-      v[pp] = e < n ? s_cand[size_t(r) * cap + e] : 0ull;
+      v[pp] = e < n ? raw_key(s_cand[e * kBlock + r]) : 0ull;
     }
     segment_sort_desc<LS>(v, L);
     for (int pp = 0; pp < 8; ++pp) emit(r, i * 8 + pp, v[pp]);
   };
+  // Otherwise only the values are sorted (32-bit order codes, no payload):
+  // tau needs the top-k values in order, and the block mask needs the set of
+  // top-k keys, which is every candidate scoring above the k-th value v_k
+  // plus, of those scoring v_k, the ones with the lowest indices.  The
+  // candidates are then read once more, unsorted, for the mask bits.
+  auto select_rows = [&](auto ls_tag, int row0) {
+    constexpr int LS = decltype(ls_tag)::value;
+    const int r = row0 + L / LS, i = L & (LS - 1), n = ncand(r);
+    const bool rok = q0 + r < NQ;
+    auto ord_raw = [&](uint64_t raw) {
+      const float x = __uint_as_float(uint32_t(raw));
+      return ord_of(kExact ? x : clamp_score(x * scale));
+    };
+    uint32_t v[8];
+    for (int pp = 0; pp < 8; ++pp) {
+      const int e = i * 8 + pp;
+      v[pp] = e < n ? ord_raw(s_cand[e * kBlock + r]) : 0u;  // 0: empty slot
+    }
+    segment_sort_desc32<LS>(v, L);
+    for (int pp = 0; pp < 8; ++pp) {
+      const int e = i * 8 + pp;
+      if (e < k && rok) s_tk[e * kWave + r] = v[pp] ? score_of_ord(v[pp]) : kSentinel;
+    }
+    // v_k and, over the row's sorted values, how many exceed / equal it
+    const int src = (k - 1) >> 3, sp = (k - 1) & 7;
+    uint32_t mine = v[0];
+    for (int pp = 1; pp < 8; ++pp)
+      if (pp == sp) mine = v[pp];
+    const uint32_t vk = src < LS ? uint32_t(__shfl(int(mine), (L & ~(LS - 1)) + src, kWave)) : 0u;
+    int gt = 0, eq = 0;
+    for (int pp = 0; pp < 8; ++pp) {
+      gt += v[pp] > vk ? 1 : 0;
+      eq += v[pp] == vk ? 1 : 0;
+    }
+    for (int d = 1; d < LS; d <<= 1) {
+      gt += __shfl_xor(gt, d, kWave);
+      eq += __shfl_xor(eq, d, kWave);
+    }
+    // vk == 0: fewer than k candidates, all selected; else take the ties'
+    // lowest indices when not all of them fit
+    const int need = k - gt;
+    const bool split = vk != 0u && eq > need;
+    for (int pp = 0; pp < 8; ++pp) {
+      const int e = i * 8 + pp;
+      if (e >= n) continue;
+      const uint64_t raw = s_cand[e * kBlock + r];
+      const uint32_t o = ord_raw(raw);
+      const int idx = int(raw >> 32);
+      bool sel = vk == 0u || o > vk || (o == vk && !split);
+      if (split && o == vk) {
+        int before = 0;  // ties with a lower index
+        for (int f = 0; f < n; ++f) {
+          const uint64_t q = s_cand[f * kBlock + r];
+          before += (ord_raw(q) == vk && int(q >> 32) < idx) ? 1 : 0;
+        }
+        sel = before < need;
+      }
+      if (sel) {
+        const int kb = idx / kBlock;
+        if (kb_word) kbm |= uint64_t(1) << kb;
+        else atomicOr(&s_bits[kb >> 5], 1u << (kb & 31));
+      }
+    }
+  };
+  const bool want_topk = p.topk_idx != nullptr;
   for (int base = 16 * w; base < 16 * w + 16; base += 8) {
     int need = k;
     for (int j = 0; j < 8; ++j) need = max(need, ncand(base + j));
-    if (need <= 64) {
-      sort_rows(std::integral_constant<int, 8>{}, base);
-    } else if (need <= 128) {
-      sort_rows(std::integral_constant<int, 16>{}, base);
-      sort_rows(std::integral_constant<int, 16>{}, base + 4);
+    if (want_topk) {
+      if (need <= 64) {
+        sort_rows(std::integral_constant<int, 8>{}, base);
+      } else if (need <= 128) {
+        sort_rows(std::integral_constant<int, 16>{}, base);
+        sort_rows(std::integral_constant<int, 16>{}, base + 4);
+      } else {
+        for (int h = 0; h < 4; ++h) sort_rows(std::integral_constant<int, 32>{}, base + 2 * h);
+      }
     } else {
-      for (int h = 0; h < 4; ++h) sort_rows(std::integral_constant<int, 32>{}, base + 2 * h);
+      if (need <= 64) {
+        select_rows(std::integral_constant<int, 8>{}, base);
+      } else if (need <= 128) {
+        select_rows(std::integral_constant<int, 16>{}, base);
+        select_rows(std::integral_constant<int, 16>{}, base + 4);
+      } else {
+        for (int h = 0; h < 4; ++h) select_rows(std::integral_constant<int, 32>{}, base + 2 * h);
+      }
     }
   }
   if (kb_word) {  // block-uniform
@@ -635,9 +858,11 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
 
 // Smallest and largest position of every 64-key block of every (batch,
 // head): kbounds[bh * nKB + kb] = (min, max) over the block's keys < NK.
-// One wave per key block.
+// One wave per key block.  Also clears the per-call status word: this is the
+// first kernel of a forward on the stream.
 __global__ __launch_bounds__(kThreads) void bounds_kernel(SelectParams p) {
   const int nKB = p.d.nKB, NK = p.d.NK;
+  if (blockIdx.x == 0 && threadIdx.x == 0 && p.status) *p.status = 0u;
   const int blk = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6);
   if (blk >= p.d.BH * nKB) return;  // wave-uniform
   const int bh = blk / nKB, kb = blk % nKB, L = threadIdx.x & 63;
@@ -669,7 +894,7 @@ __global__ __launch_bounds__(kThreads) void tau_kernel(SelectParams p) {
 
 template <typename T, int D, int MODE, int R>
 hipError_t launch_one(const SelectParams& p, hipStream_t s) {
-  const SelLayout l = sel_layout(p.d.k, p.cap, p.d.nKB, D, int(sizeof(T)), MODE == kGivenScores);
+  const SelLayout l = sel_layout(p.d.k, p.cap, p.d.nKB);
   auto kern = select_kernel<T, D, MODE, R>;
   if (l.total > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -684,9 +909,8 @@ hipError_t launch_one(const SelectParams& p, hipStream_t s) {
 // larger k, the more candidates a loose floor admits.
 template <typename T, int D, int MODE>
 hipError_t launch_r(const SelectParams& p, hipStream_t s) {
-  if (p.d.k <= 32) return launch_one<T, D, MODE, 2>(p, s);
-  if (p.d.k <= 64) return launch_one<T, D, MODE, 4>(p, s);
-  return launch_one<T, D, MODE, 8>(p, s);
+  if (classes_per_lane(p.d.k) == 2) return launch_one<T, D, MODE, 2>(p, s);
+  return launch_one<T, D, MODE, 4>(p, s);
 }
 
 template <typename T, int D>
@@ -695,8 +919,6 @@ hipError_t launch_mode(const SelectParams& p, hipStream_t s) {
   return launch_r<T, D, kExactScores>(p, s);
 }
 
-int tbytes_of(bool bf16) { return bf16 ? 2 : 4; }
-int dim_of(const Dims& d, bool from_scores) { return from_scores ? 64 : d.D; }
 
 }  // namespace
 
@@ -733,8 +955,9 @@ hipError_t launch_tau(const SelectParams& p, hipStream_t s) {
 }
 
 size_t select_lds_bytes(const Dims& d, bool bf16, bool from_scores, int cap) {
-  return size_t(sel_layout(d.k, cap, d.nKB, dim_of(d, from_scores),
-                           from_scores ? 4 : tbytes_of(bf16), from_scores).total);
+  (void)bf16;
+  (void)from_scores;
+  return size_t(sel_layout(d.k, cap, d.nKB).total);
 }
 
 int select_capacity(const Dims& d, bool bf16, bool from_scores, size_t max_lds) {

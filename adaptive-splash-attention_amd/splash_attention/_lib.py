@@ -12,7 +12,7 @@ import threading
 
 from . import _build
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 ASA_OK = 0
 ASA_ERR_INVALID_ARGUMENT = 1
@@ -26,6 +26,10 @@ TAU_REFERENCE = 0
 TAU_EXACT = 1
 GRAD_ENTMAX = 0
 GRAD_REFERENCE = 1
+
+# bits of asa_state.status (ASA_STATUS_* in adasplash.h)
+STATUS_SELECT_ROUNDS = 0x1
+STATUS_REFINE_SWEEPS = 0x2
 
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTS = (
@@ -69,6 +73,7 @@ class State(ctypes.Structure):
         ("topk_idx", ctypes.c_void_p),
         ("topk_val", ctypes.c_void_p),
         ("sup_mask", ctypes.c_void_p),
+        ("status", ctypes.c_void_p),
     ]
 
 

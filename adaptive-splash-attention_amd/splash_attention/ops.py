@@ -48,6 +48,9 @@ class SplashState:
     # support masks (asa_state.sup_mask): the (row, key) pairs with u > 0,
     # 16 bits per (tile, 16-row wave, lane) as uint16 bit patterns
     sup_mask: torch.Tensor | None = None  # [BH, nQB*nKB, 4, 64] int16
+    # per-call status word (asa_state.status): written on the stream by the
+    # forward, read only by check_status()
+    status: torch.Tensor | None = None    # [1] int32
 
     SUPPORT = ("sup_mask",)
 
@@ -56,7 +59,31 @@ class SplashState:
             return None if t is None else t.data_ptr()
         return _lib.State(ptr(self.taus), ptr(self.norms), ptr(self.mask), ptr(self.q_ptr),
                           ptr(self.q_list), ptr(self.k_ptr), ptr(self.k_list),
-                          ptr(self.topk_idx), ptr(self.topk_val), ptr(self.sup_mask))
+                          ptr(self.topk_idx), ptr(self.topk_val), ptr(self.sup_mask),
+                          ptr(self.status))
+
+    def status_word(self) -> int:
+        """The forward's status word (synchronises with the device)."""
+        if self.status is None:
+            return 0
+        return int(self.status.item()) & 0xFFFFFFFF
+
+    def overflow_rounds(self) -> int:
+        """Largest number of candidate overflow rounds a query block of the
+        score pass ran (information; synchronises)."""
+        return (self.status_word() >> 8) & 0xFF
+
+    def check_status(self) -> None:
+        """Debug check (synchronises): raises RuntimeError if the forward
+        reported a truncated iteration (ASA_STATUS_* in adasplash.h)."""
+        w = self.status_word()
+        msgs = []
+        if w & _lib.STATUS_SELECT_ROUNDS:
+            msgs.append("score pass stopped at its candidate round bound (top-k may be incomplete)")
+        if w & _lib.STATUS_REFINE_SWEEPS:
+            msgs.append("exact tau: a row's iteration stopped at the sweep cap (tau not converged)")
+        if msgs:
+            raise RuntimeError("; ".join(msgs))
 
     def tensors(self) -> tuple:
         """The tensors a backward needs (support lists included when present)."""
@@ -229,6 +256,7 @@ def alloc_state(p: _lib.Problem, device, with_topk: bool = False,
         q_list=torch.empty((BH, nQB * nKB), **i32),
         k_ptr=torch.empty((BH, nKB + 1), **i32),
         k_list=torch.empty((BH, nKB * nQB), **i32),
+        status=torch.empty((1,), **i32),
     )
     if with_topk:
         st.topk_idx = torch.empty((BH, p.nq, p.k_keep), **i32)
@@ -304,10 +332,12 @@ def splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st: SplashState, alpha: fl
 
 
 def select_from_scores(scores, Q_idx, K_idx, alpha: float, k_keep: int, batch: int = 1,
-                       heads: int | None = None) -> SplashState:
+                       heads: int | None = None, with_topk: bool = True) -> SplashState:
     """Top-k, tau, block mask and CSR lists from given fp32 scores [BH, NQ, NK]
     (no reference counterpart: exposes the reference's selection stage,
-    adasplashattention.cu:199-216, for checks on identical scores)."""
+    adasplashattention.cu:199-216, for checks on identical scores).
+    with_topk=False leaves the top-k index/value outputs out, which is the
+    selection path asa_forward takes."""
     lib = _lib.load()
     if scores.dim() == 4:
         batch, heads = scores.shape[0], scores.shape[1]
@@ -326,7 +356,7 @@ def select_from_scores(scores, Q_idx, K_idx, alpha: float, k_keep: int, batch: i
     qi = _index(Q_idx, BH, NQ, batch, heads, scores.device, "Q_idx")
     ki = _index(K_idx, BH, NK, batch, heads, scores.device, "K_idx")
     p = make_problem(batch, heads, NQ, NK, 64, torch.float32, alpha, k_keep, 1.0)
-    st = alloc_state(p, scores.device, with_topk=True)
+    st = alloc_state(p, scores.device, with_topk=with_topk)
     scores = scores.contiguous()
     ws = workspace(p, scores.device)
     cst = st.c_struct()

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define ASA_ABI_VERSION 3
+#define ASA_ABI_VERSION 4
 
 typedef enum asa_status {
   ASA_OK = 0,
@@ -127,7 +127,25 @@ typedef struct asa_problem {
  *                                   the rows' exact supports, on which
  *                                   every backward term lives: with them
  *                                   the backward visits only those pairs.
+ * Status word, optional (NULL: not written):
+ *   status   uint32  [1]            written by asa_forward and
+ *                                   asa_select_from_scores on the stream
+ *                                   (cleared by their first kernel): the
+ *                                   ASA_STATUS_* bits below, and in bits
+ *                                   8-15 the largest number of candidate
+ *                                   overflow rounds a query block of the
+ *                                   score pass ran (saturating at 255).  Read
+ *                                   it after the call has completed (e.g.
+ *                                   in a debug check); the call itself never
+ *                                   synchronises.
  */
+/* Score pass: a query block's candidate rounds reached their proven bound
+ * (2 + (nk - cap) / (cap - k) rounds always suffice; set only if that proof
+ * were wrong, never observed).  Top-k of that block may be incomplete.     */
+#define ASA_STATUS_SELECT_ROUNDS 0x1u
+/* tau_mode = ASA_TAU_EXACT: a row's Newton iteration reached the refine
+ * pass's sweep cap before |f| <= 1e-6; its tau is the last iterate.        */
+#define ASA_STATUS_REFINE_SWEEPS 0x2u
 typedef struct asa_state {
   float *taus;
   float *norms;
@@ -139,6 +157,7 @@ typedef struct asa_state {
   int32_t *topk_idx;
   float *topk_val;
   uint16_t *sup_mask;
+  uint32_t *status;
 } asa_state;
 
 /* Byte sizes of every state buffer and of the workspace the entry points

@@ -14,12 +14,13 @@ from tests._util import causal_idx
 pytestmark = pytest.mark.gpu
 
 
-def _run(dev, S, vis_qidx, vis_kidx, k, alpha, B, H):
+def _run(dev, S, vis_qidx, vis_kidx, k, alpha, B, H, with_topk=True):
     import splash_attention as sa
 
     BH, NQ, NK = S.shape
     st = sa.ops.select_from_scores(torch.from_numpy(S).to(dev), vis_qidx.to(dev),
-                                   vis_kidx.to(dev), alpha, k, batch=B, heads=H)
+                                   vis_kidx.to(dev), alpha, k, batch=B, heads=H,
+                                   with_topk=with_topk)
     torch.cuda.synchronize()
     return st
 
@@ -35,8 +36,9 @@ def _oracle(S, qidx, kidx, k, alpha):
 
 
 def _compare(st, sel, c):
-    np.testing.assert_array_equal(st.topk_idx.cpu().numpy(), sel.topk_idx)
-    np.testing.assert_array_equal(st.topk_val.cpu().numpy(), sel.topk_val)
+    if st.topk_idx is not None:
+        np.testing.assert_array_equal(st.topk_idx.cpu().numpy(), sel.topk_idx)
+        np.testing.assert_array_equal(st.topk_val.cpu().numpy(), sel.topk_val)
     np.testing.assert_array_equal(st.mask.cpu().numpy(), sel.mask)
     np.testing.assert_array_equal(st.q_ptr.cpu().numpy(), c.q_ptr)
     np.testing.assert_array_equal(st.q_list.cpu().numpy(), c.q_list)
@@ -59,9 +61,15 @@ CASES = [
 ]
 
 
+# with_topk=False is the path asa_forward takes: values sorted alone, the
+# mask from the candidates scoring above the k-th value plus the
+# lowest-index ties (the "ties" and "saturated" cases split tie runs at the
+# k-th value)
+@pytest.mark.parametrize("with_topk", [True, False], ids=["topk", "values"])
 @pytest.mark.parametrize("name,B,H,NQ,NK,k,alpha,kind", CASES, ids=[c[0] for c in CASES])
-def test_select_bit_exact(dev, name, B, H, NQ, NK, k, alpha, kind):
-    print(f"[select] {name} B={B} H={H} NQ={NQ} NK={NK} k={k} alpha={alpha}", flush=True)
+def test_select_bit_exact(dev, name, B, H, NQ, NK, k, alpha, kind, with_topk):
+    print(f"[select] {name} B={B} H={H} NQ={NQ} NK={NK} k={k} alpha={alpha} "
+          f"topk={with_topk}", flush=True)
     rng = np.random.default_rng(hash(name) % 2**32)
     BH = B * H
     if kind == "normal":
@@ -72,7 +80,7 @@ def test_select_bit_exact(dev, name, B, H, NQ, NK, k, alpha, kind):
         S = (rng.normal(size=(BH, NQ, NK)) * 30).astype(np.float32)
     qidx = causal_idx(BH, NQ) + (NK - NQ if NK > NQ else 0)
     kidx = causal_idx(BH, NK)
-    st = _run(dev, S, qidx, kidx, k, alpha, B, H)
+    st = _run(dev, S, qidx, kidx, k, alpha, B, H, with_topk)
     sel, c = _oracle(S, qidx, kidx, k, alpha)
     _compare(st, sel, c)
 
