@@ -289,15 +289,15 @@ int asa_query_sizes(const asa_problem* p, asa_sizes* out) {
   return ok();
 }
 
-int asa_forward(const asa_problem* p, const void* q, const void* k, const void* v,
-                const int32_t* q_idx, const int32_t* k_idx, void* out, const asa_state* st,
-                void* workspace, void* stream) {
-  Shape sh;
-  if (int rc = validate(p, &sh)) return rc;
-  if (!q || !k || !v || !q_idx || !k_idx || !out)
-    return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
-  if (int rc = check_state(st, true)) return rc;
-  if (!workspace) return fail(ASA_ERR_INVALID_ARGUMENT, "workspace is NULL");
+}  // extern "C"
+
+namespace {
+
+// The forward's kernel sequence on `workspace` (asa_sizes.workspace bytes);
+// the problem is already validated.
+int forward_impl(const Shape& sh, const void* q, const void* k, const void* v,
+                 const int32_t* q_idx, const int32_t* k_idx, void* out, const asa_state* st,
+                 void* workspace, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (int rc = run_select(sh, q, k, nullptr, q_idx, k_idx, st, workspace, s)) return rc;
@@ -321,6 +321,69 @@ int asa_forward(const asa_problem* p, const void* q, const void* k, const void* 
   asa::profile_end(s);
   if (int rc = check_hip(e, "forward kernel launch")) return rc;
   return ok();
+}
+
+// Workspace of asa_forward_noalloc: a file-scope device array (each GPU the
+// library runs on holds its own copy until the process ends).  In host code
+// `scratch` only names the symbol; its device address comes from
+// hipGetSymbolAddress, once per device, and only that address is passed on.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's `scratch`.
+int scratch_address(void** ptr) {
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(ASA_ERR_UNSUPPORTED, "device ordinal %d above %d", dev, kMaxDevices - 1);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* a = nullptr;
+    if (int rc = check_hip(hipGetSymbolAddress(&a, HIP_SYMBOL(scratch)), "hipGetSymbolAddress"))
+      return rc;
+    g_scratch_ptr[dev] = a;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return ASA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int asa_forward(const asa_problem* p, const void* q, const void* k, const void* v,
+                const int32_t* q_idx, const int32_t* k_idx, void* out, const asa_state* st,
+                void* workspace, void* stream) {
+  Shape sh;
+  if (int rc = validate(p, &sh)) return rc;
+  if (!q || !k || !v || !q_idx || !k_idx || !out)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
+  if (int rc = check_state(st, true)) return rc;
+  if (!workspace) return fail(ASA_ERR_INVALID_ARGUMENT, "workspace is NULL");
+  return forward_impl(sh, q, k, v, q_idx, k_idx, out, st, workspace, stream);
+}
+
+int asa_forward_noalloc(const asa_problem* p, const void* q, const void* k, const void* v,
+                        const int32_t* q_idx, const int32_t* k_idx, void* out,
+                        const asa_state* st, void* stream) {
+  Shape sh;
+  if (int rc = validate(p, &sh)) return rc;
+  asa_sizes z;
+  sizes_of(sh, &z);
+  if (z.workspace > kScratchBytes)
+    return fail(ASA_ERR_UNSUPPORTED,
+                "problem needs %zu bytes of workspace; asa_forward_noalloc holds %zu "
+                "(use asa_forward with a caller-owned workspace)",
+                z.workspace, kScratchBytes);
+  if (!q || !k || !v || !q_idx || !k_idx || !out)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
+  if (int rc = check_state(st, true)) return rc;
+  void* ws = nullptr;
+  if (int rc = scratch_address(&ws)) return rc;
+  return forward_impl(sh, q, k, v, q_idx, k_idx, out, st, ws, stream);
 }
 
 int asa_backward(const asa_problem* p, int32_t grad_mode, const void* q, const void* k,

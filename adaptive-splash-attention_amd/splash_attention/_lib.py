@@ -27,6 +27,9 @@ TAU_EXACT = 1
 GRAD_ENTMAX = 0
 GRAD_REFERENCE = 1
 
+# workspace held by asa_forward_noalloc (ASA_NOALLOC_WORKSPACE_BYTES)
+NOALLOC_WORKSPACE_BYTES = 64 << 20
+
 # bits of asa_state.status (ASA_STATUS_* in adasplash.h)
 STATUS_SELECT_ROUNDS = 0x1
 STATUS_REFINE_SWEEPS = 0x2
@@ -37,6 +40,7 @@ EXPORTS = (
     "asa_last_error",
     "asa_query_sizes",
     "asa_forward",
+    "asa_forward_noalloc",
     "asa_backward",
     "asa_select_from_scores",
     "asa_profile_enable",
@@ -128,6 +132,9 @@ def load() -> ctypes.CDLL:
         lib.asa_forward.restype = ctypes.c_int
         lib.asa_forward.argtypes = [ctypes.POINTER(Problem), _V, _V, _V, _V, _V, _V,
                                     ctypes.POINTER(State), _V, _V]
+        lib.asa_forward_noalloc.restype = ctypes.c_int
+        lib.asa_forward_noalloc.argtypes = [ctypes.POINTER(Problem), _V, _V, _V, _V, _V, _V,
+                                            ctypes.POINTER(State), _V]
         lib.asa_backward.restype = ctypes.c_int
         lib.asa_backward.argtypes = [ctypes.POINTER(Problem), _I, _V, _V, _V, _V, _V, _V, _V,
                                      ctypes.POINTER(State), _V, _V, _V, _V, _V]

@@ -274,18 +274,27 @@ def workspace(p: _lib.Problem, device) -> torch.Tensor:
 
 def splash_forward(Q, K, V, Q_idx, K_idx, alpha: float, k_keep: int, sm_scale=None,
                    with_topk: bool = False, with_support: bool = True,
-                   tau_mode: str = "reference"):
+                   tau_mode: str = "reference", noalloc: bool = False):
     """Forward pass; returns (out, SplashState).  Inputs as check_inputs() returns them.
     with_support records the rows' support masks for the sparse backward
     (skip it for inference).  tau_mode "exact" solves tau over the whole
-    visible row instead of the top-k (see TAU_MODES)."""
+    visible row instead of the top-k (see TAU_MODES).  noalloc=True calls
+    asa_forward_noalloc, whose workspace is the library's own device array
+    (no workspace tensor is allocated; calls that overlap on one GPU race)."""
     lib = _lib.load()
     B, H, NQ, d = Q.shape
     p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale, tau_mode)
     st = alloc_state(p, Q.device, with_topk, with_support)
     out = torch.empty_like(Q)
-    ws = workspace(p, Q.device)
     cst = st.c_struct()
+    if noalloc:
+        with torch.cuda.device(Q.device):
+            rc = lib.asa_forward_noalloc(ctypes.byref(p), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
+                                         Q_idx.data_ptr(), K_idx.data_ptr(), out.data_ptr(),
+                                         ctypes.byref(cst), _stream(Q.device))
+        _lib.check(rc)
+        return out, st
+    ws = workspace(p, Q.device)
     with torch.cuda.device(Q.device):
         rc = lib.asa_forward(ctypes.byref(p), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
                              Q_idx.data_ptr(), K_idx.data_ptr(), out.data_ptr(),

@@ -188,6 +188,21 @@ int asa_forward(const asa_problem *p, const void *q, const void *k, const void *
                 const int32_t *q_idx, const int32_t *k_idx, void *out, const asa_state *st,
                 void *workspace, void *stream);
 
+/* asa_forward without a workspace argument.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Its workspace is a file-scope device array of the library
+ * of ASA_NOALLOC_WORKSPACE_BYTES, one per GPU, held until the process ends;
+ * the call allocates nothing.  Problems whose asa_sizes.workspace exceeds it
+ * (batch*heads*nq*k_keep*4 + batch*heads*ceil(nk/64)*8 bytes, rounded; the
+ * B4 H16 N4096 k32 shape needs 33.6 MB) fail with ASA_ERR_UNSUPPORTED.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (other streams or threads) race.  Same outputs as asa_forward.       */
+#define ASA_NOALLOC_WORKSPACE_BYTES (64u << 20)
+int asa_forward_noalloc(const asa_problem *p, const void *q, const void *k, const void *v,
+                        const int32_t *q_idx, const int32_t *k_idx, void *out,
+                        const asa_state *st, void *stream);
+
 /* Backward pass (reference: backward_splash, adasplashattention.cu:611-700)
  * from the state a matching asa_forward wrote.  `out` is that forward's
  * output (read in ASA_GRAD_REFERENCE mode only; may be NULL otherwise).
