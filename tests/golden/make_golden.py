@@ -57,6 +57,8 @@ def main():
             {"s": [3.0], "alpha": 1.5, "tau": 1.5},
             {"s": [2.0, 2.0, 2.0, 2.0], "alpha": 1.25, "tau": 0.5},
             {"s": [0.3, -1e6, -1e6, -1e6], "alpha": 2.0, "tau": -0.7},
+            # two rounds take the bisection fallback (cu:102-104)
+            {"s": [9.0, -2.0, -14.0], "alpha": 1.5, "tau": 3.5000000555768707},
         ],
         "forward_outside_topk": {
             "scores": [1.0, 0.9, 0.8], "alpha": 2.0, "k": 2,

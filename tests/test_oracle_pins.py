@@ -157,6 +157,37 @@ def test_tau_known_answers_by_hand():
     assert orc.entmax_threshold([1.0, 0.9], 2.0, "f64") == pytest.approx(0.45, abs=1e-15)
 
 
+def test_tau_bisection_fallback_by_hand():
+    """The step that leaves the bracket (cu:102-104).  s = [9, -2, -14],
+    alpha = 1.5, so a = 2, z = s / 2 = (4.5, -1, -7), f = sum u^2 - 1 over
+    u = z - tau > 0, f' = -2 sum u, and the reference's f'' = 3 per term.
+    Bracket [lo, hi] = [-7 - 2, 4.5 + 2] = [-9, 6.5], start at its midpoint
+    -1.25, where u = (5.75, 0.25): f = 32.125, f' = -12, f'' = 6, and the
+    Halley step -1.25 + 2 * 32.125 * 12 / (2 * 144 - 6 * 32.125)
+    = -1.25 + 3084/381 = 6.8445 lies above hi: the fallback takes the
+    midpoint, -1.25 again; f > 0 there makes it lo.  The next round repeats
+    the same step (same tau), which again leaves the bracket, and the
+    fallback gives (-1.25 + 6.5) / 2 = 2.625, where one key is active,
+    u = 15/8, f = 161/64 > 0 (lo).  The last three rounds are single-key
+    Halley steps, the map x -> x (x^2 + 7) / (5 x^2 + 3) on u (pinned in
+    test_tau_single_real_key_follows_reference_f2_coefficient), each inside
+    the bracket, none with |f| < 1e-4: tau = 4.5 - phi(phi(phi(15/8)))."""
+    from fractions import Fraction as Fr
+
+    step0 = Fr(-5, 4) + Fr(3084, 381)
+    assert step0 > Fr(13, 2)  # leaves the bracket: the fallback is taken
+    x = Fr(15, 8)
+    for _ in range(3):
+        x = x * (x * x + 7) / (5 * x * x + 3)
+    want = float(Fr(9, 2) - x)
+    assert want == pytest.approx(3.5000000555768707, rel=1e-15)
+    assert orc.entmax_threshold([9.0, -2.0, -14.0], 1.5, "f64") == pytest.approx(want, rel=1e-14)
+    assert orc.entmax_threshold([9.0, -2.0, -14.0], 1.5, "f32") == pytest.approx(want, rel=1e-6)
+    # Taking the step instead of the midpoint would leave no key active at
+    # 6.8445 and the iteration would stop moving there.
+    assert abs(float(step0) - want) > 3.0
+
+
 @pytest.mark.parametrize("alpha,closed", [(2.0, D.tau_sparsemax), (1.5, D.tau_entmax15)])
 def test_tau_converged_rows_match_closed_forms(alpha, closed):
     """When the recurrence stops on |f| < 1e-4 and the top-k holds the whole
@@ -337,3 +368,30 @@ def test_sparsemax_gradient_centres_dp_on_support():
     dQ, _, _ = orc.backward(Q, K, V, idx, idx, dO, 2.0, 0.125, taus, fw.csr.q_ptr,
                             fw.csr.q_list, orc.GRAD_ENTMAX, precision="f64")
     np.testing.assert_allclose(dQ, np.einsum("bij,bjd->bid", dS, K) * 0.125, rtol=1e-8, atol=1e-10)
+
+
+# ---------------------------------------------------------------- key blocks
+
+
+@pytest.mark.parametrize("mode", [orc.GRAD_ENTMAX, orc.GRAD_REFERENCE])
+@pytest.mark.parametrize("alpha,causal", [(1.5, True), (2.0, False), (1.25, True)])
+def test_key_block_grads_match_oracle_backward(mode, alpha, causal):
+    """oracle/keyblock.py (the chunked restatement the full-size GPU tests
+    use for sampled key blocks) equals asao_backward on whole heads."""
+    from oracle import keyblock as KB
+
+    rng = np.random.default_rng(21)
+    BH, N, d, k, scale = 2, 320, 64, 6, 0.125
+    Q, K, V, dO = (rng.normal(size=(BH, N, d)) for _ in range(4))
+    ki = np.tile(np.arange(N, dtype=np.int32), (BH, 1))
+    qi = ki.copy() if causal else np.full((BH, N), N - 1, np.int32)
+    fw = orc.forward(Q, K, V, qi, ki, alpha, scale, k, precision="f64")
+    gq, gk, gv = orc.backward(Q, K, V, qi, ki, dO, alpha, scale, fw.taus, fw.csr.q_ptr,
+                              fw.csr.q_list, mode, precision="f64")
+    blocks = [0, 2, 4]
+    rows = np.concatenate([np.arange(b * 64, min(b * 64 + 64, N)) for b in blocks])
+    for bh in range(BH):
+        dK, dV = KB.key_block_grads(Q[bh], K[bh], V[bh], dO[bh], qi[bh], ki[bh], fw.taus[bh],
+                                    fw.mask[bh], alpha, scale, blocks, mode, chunk=96)
+        np.testing.assert_allclose(dK, gk[bh][rows], rtol=1e-9, atol=1e-12 * np.abs(gk).max())
+        np.testing.assert_allclose(dV, gv[bh][rows], rtol=1e-9, atol=1e-12 * np.abs(gv).max())
