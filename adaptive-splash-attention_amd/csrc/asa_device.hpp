@@ -157,6 +157,25 @@ struct ClippedU {
   }
 };
 
+// ClippedU whose floor is -0 instead of +0 where u can reach it: v is u
+// where u > 0 and a zero with the sign bit set elsewhere (u = 0 itself may
+// give either zero), so the sign bit tells u <= 0 apart without a compare:
+// one v_alignbit per score shifts it into a mask.  Rows that get no weight
+// give -0 for every score.  Every power below maps -0 to a zero weight.
+struct SignedClip {
+  float c, nt, lo, hi;
+  __device__ __forceinline__ SignedClip(float am1, float scale, float tau, bool valid) {
+    const float l = fmaf(-10.0f, am1, -tau), h = fmaf(10.0f, am1, -tau);
+    c = valid ? am1 * scale : 0.0f;
+    nt = valid ? -tau : 0.0f;
+    lo = valid && l > 0.0f ? l : -0.0f;
+    hi = valid && h > 0.0f ? h : -0.0f;
+  }
+  __device__ __forceinline__ float operator()(float s) const {
+    return __builtin_amdgcn_fmed3f(fmaf(c, s, nt), lo, hi);
+  }
+};
+
 // v^e for v = max(u, 0) from ClippedU: 0 where v = 0, like the reference's
 // (u > 0) ? max(u, EPS)^e : 0.  The positive integer classes give 0 at v = 0
 // by themselves; they drop the EPS floor, which changes a weight by at most

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   const int qpos = qok ? p.q_idx[row] : 0;
   const float am1 = p.d.alpha - 1.0f;
   const float a = 1.0f / am1;
-  const ClippedU clip(am1, p.d.scale, qok ? p.taus[row] : 0.0f, qok);  // invalid rows: p = 0
+  const SignedClip clip(am1, p.d.scale, qok ? p.taus[row] : 0.0f, qok);  // invalid rows: p = 0
   // smallest position of the block's valid rows: a key block whose largest
   // position (from the score pass's bounds) is at most this, and that lies
   // wholly below NK, is visible to every row of the block
@@ -95,24 +95,22 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
     const int b = (e - e0) & 1;
     f32x4 acc[4];
     rows_x_frag<D>(acc, sm.K[b], qf, lane);
-    // p for every score, then masked: no per-score branches.  With support
-    // masks, v = max(u, 0) of all 16 scores is formed first and the lane's
-    // 16-bit mask of v > 0 is stored before the powers are taken.
+    // p for every score, then masked: no per-score branches.  v = max(u, 0)
+    // carries its sign bit where u <= 0 (SignedClip); with support masks the
+    // lane's 16 bits of u > 0 are those sign bits, complemented.  The row
+    // sums are of the float32 weights (the bf16 copies the P^T V product
+    // takes would bias sums of many equal weights by up to 2^-9).
     auto weights = [&](auto partial) {
-      for (int f = 0; f < 4; ++f)
-        for (int r = 0; r < 4; ++r) {
+      uint32_t nm = 0;  // bit 4f + r <- u <= 0, highest bit first
+      for (int f = 3; f >= 0; --f)
+        for (int r = 3; r >= 0; --r) {
           float v = clip(acc[f][r]);  // max(u, 0)
           if constexpr (decltype(partial)::value)
-            v = sm.kid[b][16 * f + 4 * g + r] <= qpos ? v : 0.0f;
+            v = sm.kid[b][16 * f + 4 * g + r] <= qpos ? v : -0.0f;
           acc[f][r] = v;
+          if constexpr (EMIT) nm = __builtin_amdgcn_alignbit(nm, __float_as_uint(v), 31);
         }
-      if constexpr (EMIT) {
-        // bit 4f + r <- u > 0 for key 16f + 4g + r of the lane's row
-        uint32_t m = 0;
-        for (int f = 3; f >= 0; --f)
-          for (int r = 3; r >= 0; --r) m = 2u * m + (acc[f][r] > 0.0f ? 1u : 0u);
-        smask[size_t(e) * 256] = uint16_t(m);
-      }
+      if constexpr (EMIT) smask[size_t(e) * 256] = uint16_t(~nm);
       for (int f = 0; f < 4; ++f)
         for (int r = 0; r < 4; ++r) {
           const float pv = pow_clipped<PC>(acc[f][r], a);
