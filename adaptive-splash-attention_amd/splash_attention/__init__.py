@@ -18,6 +18,8 @@ there is no CPU or PyTorch fallback.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import ops
@@ -39,8 +41,13 @@ __version__ = "0.1.0"
 
 
 def forward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, k_keep: int = 8):
-    """Reference-compatible native forward (adasplashattention.cu:537-609)."""
+    """Reference-compatible native forward (adasplashattention.cu:537-609).
+    ``sm_scale=None`` means 1/sqrt(d) of the caller's head dimension (before
+    any zero padding)."""
+    ops.check_shapes(Q, K, V)
     d, dtype = Q.size(-1), Q.dtype
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
     Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     out, _ = ops.splash_forward(Q, K, V, qi, ki, ops.clamp_alpha(alpha), k_keep, sm_scale,
                                 with_support=False)
@@ -50,12 +57,15 @@ def forward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, k_keep: int = 
 def backward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, dOut, k_keep: int = 8,
              grad_mode: str = "reference"):
     """Reference-compatible native backward (adasplashattention.cu:611-700):
-    reruns the selection, then returns [dQ, dK, dV]."""
+    reruns the selection, then returns [dQ, dK, dV].  ``sm_scale=None`` as
+    in ``forward``."""
     ops.check_shapes(Q, K, V)
     if not isinstance(dOut, torch.Tensor) or dOut.shape != Q.shape:
         raise ValueError(f"dOut shape {tuple(getattr(dOut, 'shape', ()))} must equal Q shape "
                          f"{tuple(Q.shape)}")
     d, dtype = Q.size(-1), Q.dtype
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
     Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     a = ops.clamp_alpha(alpha)
     out, st = ops.splash_forward(Q, K, V, qi, ki, a, k_keep, sm_scale)

@@ -134,6 +134,12 @@ def _index(idx, BH: int, N: int, B: int, H: int, device, name: str) -> torch.Ten
     return idx.contiguous()
 
 
+class HeadDimError(RuntimeError, ValueError):
+    """Head dimension above the kernels' limit.  The reference raises it as a
+    RuntimeError (TORCH_CHECK, adasplashattention.cu:542); it is also a
+    ValueError, like this module's other argument errors."""
+
+
 def check_shapes(Q, K, V, k_keep=None):
     """The reference's argument checks (adasplashattention.cu:542-558) that
     need no tensor data: ranks, shapes, dtypes, head dimension, device."""
@@ -143,7 +149,7 @@ def check_shapes(Q, K, V, k_keep=None):
         if t.dim() != 4:
             raise ValueError(f"{name} must be 4-D [B, H, N, d], got shape {tuple(t.shape)}")
     if Q.size(3) > MAX_HEAD_DIM:
-        raise ValueError("Head dimension too large; increase D_MAX")
+        raise HeadDimError("Head dimension too large; increase D_MAX")
     if Q.dtype not in INPUT_DTYPES:
         raise TypeError(f"unsupported dtype {Q.dtype}; use torch.float32, torch.bfloat16 "
                         "or torch.float16")

@@ -49,13 +49,55 @@ ELEM = 2                 # bf16 bytes
 COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # HBM bytes per launch of each kernel at this workload, measured with
 # rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), the factors a plain
-# 256 MiB device copy gives (profiles/headline_hbm_traffic.md).
-# refine (exact tau mode only) from the same two passes over
-# `bench.py --tau-mode exact` (profiles/exact_mode_kernel_stats.md).
-# bwd_dq_sparse includes the position map it writes for bwd_dkdv_sparse;
-# bwd_dq and bwd_dkdv are the dense passes (run when no support masks were
-# recorded).
-HBM_TRAFFIC = {'refine': 74134323, 'bounds': 1108138, 'select': 103819594, 'tau': 34748757, 'compact': 2751317, 'forward': 207541610, 'bwd_dq_sparse': 248106329, 'bwd_dkdv_sparse': 277114956, 'bwd_dq': 174715008, 'bwd_dkdv': 208030987}
+# 256 MiB device copy gives (profiles/headline_hbm_traffic.md), on the
+# library built from the sources whose hash is HBM_TRAFFIC_SOURCES
+# (source_hash()).  A line from a library built from other sources reports
+# traffic null and says why: counters of another build are not evidence.
+HBM_TRAFFIC_SOURCES = "unmeasured"
+HBM_TRAFFIC: dict = {}
+# L2-resident read bandwidth measured on the box (profiles/l2_read_bandwidth.md):
+# the ceiling of the passes whose tiles and gathered rows come from L2.
+L2_READ_MEASURED = 15.39e12
+
+
+def source_hash() -> str:
+    """sha256 (first 16 hex digits) of the library's sources: csrc/* and the
+    C ABI header, in name order."""
+    import hashlib
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "adaptive-splash-attention_amd", "csrc")
+    files = sorted(os.path.join(csrc, f) for f in os.listdir(csrc)
+                   if f.endswith((".hip", ".hpp", ".cpp")))
+    files.append(os.path.join(ROOT, "include", "adasplash.h"))
+    for f in files:
+        h.update(os.path.basename(f).encode())
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def host_cpu() -> dict:
+    """Model name and core counts of the host (from /proc/cpuinfo)."""
+    model, cores = "unknown", set()
+    phys = core = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                k, _, v = ln.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+    except OSError:
+        pass
+    return {"model": model, "physical_cores": len(cores) or None,
+            "logical_cpus": os.cpu_count()}
 
 
 def effective_flops(B, H, N, d):
@@ -95,7 +137,9 @@ def kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep, nsup):
                        bytes=rows * d * ELEM + vis_blocks * tile + rows * k_keep * 4),
         "bounds": dict(bound="hbm", flops=0.0, bytes=BH * N * 4 + BH * nKB * 8),
         "compact": dict(bound="hbm", flops=0.0, bytes=2 * BH * nQB * nKB + csr),
-        "forward": dict(bound="hbm", flops=4.0 * 64 * 64 * d * nnzb,
+        # the forward's tile bytes are mostly L2-served (its algorithmic byte
+        # rate exceeds the HBM peak); its MFMA work is the bound
+        "forward": dict(bound="mfma", flops=4.0 * 64 * 64 * d * nnzb,
                         bytes=nnzb * 2 * tile + 2 * rows * d * ELEM + 2 * rows * 4
                         + 4 * BH * (nQB + 1 + nnzb // BH)),
         "bwd_dq": dict(bound="hbm", flops=8.0 * 64 * 64 * d * nnzb,
@@ -122,16 +166,23 @@ def roofline_of(model, ms):
         ach, peak, unit = model["flops"] / t / 1e12, PEAK_MFMA_BF16 / 1e12, "TFLOP/s"
     else:
         ach, peak, unit = model["bytes"] / t / 1e9, PEAK_HBM / 1e9, "GB/s"
-    return {"bound": model["bound"], "achieved": round(ach, 3), "peak": peak, "unit": unit,
-            "frac": round(ach / peak, 4), "traffic": None, "avg_ms": round(ms, 5),
-            "mfma_frac": round(mf, 4), "hbm_frac_algorithmic": round(hb, 4),
-            "alg_flops": model["flops"], "alg_bytes": model["bytes"]}
+    r = {"bound": model["bound"], "achieved": round(ach, 3), "peak": peak, "unit": unit,
+         "frac": round(ach / peak, 4), "traffic": None, "avg_ms": round(ms, 5),
+         "mfma_frac": round(mf, 4), "hbm_frac_algorithmic": round(hb, 4),
+         "alg_flops": model["flops"], "alg_bytes": model["bytes"]}
+    if hb > 1.0:
+        # more algorithmic bytes than HBM can deliver in this time: they come
+        # from L2, so the byte model is not an HBM bound for this kernel
+        r["l2_frac_algorithmic"] = round(model["bytes"] / t / L2_READ_MEASURED, 4)
+        r["model_note"] = "algorithmic bytes above the HBM peak rate: L2-served, not an HBM bound"
+    return r
 
 
-def dense_gpu_baseline(Q, K, V, dO, alpha, scale, iters=40):
+def dense_gpu_baseline(Q, K, V, dO, alpha, scale, iters=40, runs=5):
     """Dense exact alpha-entmax attention fwd+bwd in PyTorch on the GPU (fp32
     math, materialised [BH, N, N] scores, tau by bisection, exact entmax
-    Jacobian); returns ms per fwd+bwd."""
+    Jacobian); returns (median, min) ms per fwd+bwd over `runs` runs after
+    one warm-up, and the run count."""
     import torch
 
     def run():
@@ -164,40 +215,80 @@ def dense_gpu_baseline(Q, K, V, dO, alpha, scale, iters=40):
 
     run()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    run()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        run()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(times), min(times), runs
 
 
-def cpu_baseline(heads=64, trials=2):
-    """The CPU oracle (C restatement of the reference algorithm, OpenMP over
-    rows / heads) on the headline workload: `heads` of its 64 (batch, head)
-    slices (all of them by default, about 6 s per trial on 16 cores), full
-    N=4096, bf16-rounded inputs in fp32."""
+def _oracle_run(heads, N, d, k, alpha, scale, seed=0):
     import numpy as np
     import torch
 
     from oracle import oracle as orc
 
-    N, d = WORK["N"], WORK["d"]
-    g = torch.Generator().manual_seed(0)
+    g = torch.Generator().manual_seed(seed)
     Q, K, V, dO = (torch.randn(heads, N, d, generator=g).to(torch.bfloat16).float().numpy()
                    for _ in range(4))
     idx = np.broadcast_to(np.arange(N, dtype=np.int32), (heads, N)).copy()
+    return lambda: orc.attention(Q, K, V, idx, idx, dO, alpha, scale, k)
+
+
+def _time(fn, warmup, trials):
+    for _ in range(warmup):
+        fn()
     times = []
     for _ in range(trials):
         t0 = time.perf_counter()
-        orc.attention(Q, K, V, idx, idx, dO, WORK["alpha"], WORK["sm_scale"], WORK["k_keep"])
+        fn()
         times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    flops = effective_flops(1, heads, N, d)
+    return statistics.median(times), min(times)
+
+
+def cpu_baseline(heads=16, warmup=3, trials=10):
+    """The CPU oracle (C restatement of the reference algorithm, OpenMP over
+    (batch, head) slices) on a bounded sample of the headline workload:
+    `heads` of its 64 slices at full N = 4096 (one slice per core of a
+    16-core share), bf16-rounded inputs in fp32; 3 warm-ups and 10 timed
+    trials (the notebook's counts, nb:1757-1758), median and min.  Also a
+    1-thread figure on one slice (1 warm-up, 3 trials: a 1-thread trial
+    takes ~1.5 s), and the c1 / c2 configurations (BASELINE configs[0, 1])
+    at the same thread count."""
+    N, d = WORK["N"], WORK["d"]
+    alpha, scale, k = WORK["alpha"], WORK["sm_scale"], WORK["k_keep"]
+    from oracle import oracle as orc
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(flops / t / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"oracle fwd+bwd (entmax grad) on {heads} of 64 (batch,head) slices, "
-                      f"N={N} d={d} k={WORK['k_keep']}, median of {trials} trials: {t:.2f} s each",
-            "ms_per_step_scaled": round(t * 1e3 * 64 / heads, 1)}
+    orc.set_num_threads(threads)
+    med, mn = _time(_oracle_run(heads, N, d, k, alpha, scale), warmup, trials)
+    flops = effective_flops(1, heads, N, d)
+    out = {"value": round(flops / med / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+           "kind": "port",
+           "sample": f"oracle fwd+bwd (entmax grad) on {heads} of the 64 (batch, head) slices, "
+                     f"N={N} d={d} k={k}, {threads} OpenMP threads, median of {trials} trials "
+                     f"after {warmup} warm-ups: {med:.3f} s (min {mn:.3f} s)",
+           "ms_per_step_scaled": round(med * 1e3 * 64 / heads, 1),
+           "host": host_cpu()}
+    # one thread, one slice (the OpenMP loops are over slices)
+    from oracle import oracle as orc
+    prev = orc.set_num_threads(1)
+    try:
+        m1, _ = _time(_oracle_run(1, N, d, k, alpha, scale), 1, 3)
+    finally:
+        orc.set_num_threads(prev)
+    out["one_thread"] = {"value": round(effective_flops(1, 1, N, d) / m1 / 1e12, 6),
+                         "unit": "TFLOP/s", "ms_per_slice": round(m1 * 1e3, 1),
+                         "ms_per_step_scaled": round(m1 * 1e3 * 64, 1),
+                         "sample": "1 of 64 slices, 1 thread, median of 3 after 1 warm-up"}
+    cfgs = {}
+    for name, (BH, Nc, kc) in {"c1": (2, 256, 8), "c2": (16, 1024, 8)}.items():
+        mc, mnc = _time(_oracle_run(BH, Nc, 64, kc, 1.5, 0.125), warmup, trials)
+        cfgs[name] = {"ms": round(mc * 1e3, 3), "min_ms": round(mnc * 1e3, 3),
+                      "shape": f"BH={BH} N={Nc} d=64 fp32 k={kc} alpha=1.5 causal, fwd+bwd"}
+    out["configs"] = cfgs
+    return out
 
 
 def main():
@@ -276,16 +367,18 @@ def main():
     nsup = support_pairs(st)
     nQB = nKB = N // 64
     models = kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep, nsup)
+    src = source_hash()
+    traffic_ok = src == HBM_TRAFFIC_SOURCES
     kernels = {}
     for name, (cnt, tot) in kern.items():
         if name in models:
             kernels[name] = roofline_of(models[name], tot / cnt)
             kernels[name]["launches"] = cnt
-            kernels[name]["traffic"] = HBM_TRAFFIC.get(name)
+            kernels[name]["traffic"] = HBM_TRAFFIC.get(name) if traffic_ok else None
             # measured HBM bytes over the same time: the algorithmic tile
             # bytes of the dense passes are mostly served by L2 (their
             # algorithmic HBM fraction can exceed 1)
-            if HBM_TRAFFIC.get(name):
+            if traffic_ok and HBM_TRAFFIC.get(name):
                 kernels[name]["hbm_frac_measured"] = round(
                     HBM_TRAFFIC[name] / (tot / cnt / 1e3) / PEAK_HBM, 4)
     dominant = max(kernels, key=lambda n: kernels[n]["avg_ms"])
@@ -317,7 +410,11 @@ def main():
                    "active_block_density_of_causal": round(nnzb / (B * H * nQB * (nQB + 1) / 2), 4)},
         "roofline": roof,
         "kernels": kernels,
+        "library_sources": src,
     }
+    if not traffic_ok:
+        line["traffic_note"] = (f"HBM traffic table measured on sources {HBM_TRAFFIC_SOURCES}, "
+                                f"this build is {src}: traffic not reported")
     if not args.no_exact_line:
         # the other tau mode on the same workload, timed the same way (the
         # headline fields above are the --tau-mode run's)
@@ -343,11 +440,12 @@ def main():
                                      "what": "same workload and step with tau_mode=" + repr(other)}
     if not args.no_dense_baseline:
         try:
-            dms = dense_gpu_baseline(Q, K, V, dO, alpha, scale)
-            line["dense_gpu_baseline"] = {"ms_per_step": round(dms, 3),
+            dms, dmin, dn = dense_gpu_baseline(Q, K, V, dO, alpha, scale)
+            line["dense_gpu_baseline"] = {"ms_per_step": round(dms, 3), "min_ms": round(dmin, 3),
                                           "speedup": round(dms / ms, 2),
                                           "what": "PyTorch dense exact alpha-entmax fwd+bwd, fp32 "
-                                                  "math, [64,4096,4096] scores, 40 bisection steps"}
+                                                  "math, [64,4096,4096] scores, 40 bisection "
+                                                  f"steps; median of {dn} runs after 1 warm-up"}
         except Exception as e:  # report, do not fail the bench line
             line["dense_gpu_baseline"] = {"error": repr(e)[:200]}
     if not args.no_cpu_baseline:

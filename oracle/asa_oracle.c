@@ -45,6 +45,7 @@
  *               g = P^(2-a), P = p / (sum p + EPS), dp = dO . v.
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -57,12 +58,16 @@ typedef float real;
 #define ASAO_REAL_BYTES 4
 #endif
 
-#define ASAO_ABI 3
+#define ASAO_ABI 4
 #define ASAO_EPS ((real)1e-8f)
 #define ASAO_TAU_ITERS 5
 #define ASAO_SENTINEL_S ((real)-1e6f)
 
 int asao_abi_version(void) { return ASAO_ABI; }
+/* Thread count of the OpenMP regions that follow (the CPU baseline times one
+ * thread and the host's share). */
+void asao_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int asao_max_threads(void) { return omp_get_max_threads(); }
 int asao_real_bytes(void) { return ASAO_REAL_BYTES; }
 
 static real rmax(real a, real b) { return a > b ? a : (b != b ? a : b); }

@@ -22,7 +22,7 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIBDIR = os.path.join(_HERE, "lib")
-_ABI = 3
+_ABI = 4
 
 _libs: dict[str, ctypes.CDLL] = {}
 
@@ -59,6 +59,9 @@ def _lib(precision: str) -> ctypes.CDLL:
     lib.asao_forward.restype = None
     lib.asao_forward.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, R, R, _I, _I, _I,
                                  _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]
+    lib.asao_set_threads.restype = None
+    lib.asao_set_threads.argtypes = [_I]
+    lib.asao_max_threads.restype = _I
     lib.asao_backward.restype = None
     lib.asao_backward.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, R, R, _I, _I,
                                   _P, _P, _P, _I, _P, _P, _P]
@@ -213,6 +216,15 @@ def backward(Q, K, V, Q_idx, K_idx, dO, alpha: float, sm_scale: float, taus, q_p
                       alpha, sm_scale, block_m, block_n, _ptr(taus), _ptr(qp), _ptr(ql),
                       int(mode), _ptr(dQ), _ptr(dK), _ptr(dV))
     return dQ, dK, dV
+
+
+def set_num_threads(n: int) -> int:
+    """Set the OpenMP thread count of both back ends; returns the previous
+    count of the f32 one."""
+    prev = _lib("f32").asao_max_threads()
+    for p in ("f32", "f64"):
+        _lib(p).asao_set_threads(int(n))
+    return prev
 
 
 def attention(Q, K, V, Q_idx, K_idx, dO, alpha: float, sm_scale: float, k: int,

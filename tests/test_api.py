@@ -28,7 +28,9 @@ def test_module_rejects_bad_config(kw):
 
 
 def test_head_dim_limit_message_matches_reference():
-    # adasplashattention.cu:542
+    # adasplashattention.cu:542 (TORCH_CHECK: a RuntimeError)
+    with pytest.raises(RuntimeError, match="Head dimension too large; increase D_MAX"):
+        ops.check_inputs(_t(1, 1, 8, 256), _t(1, 1, 8, 256), _t(1, 1, 8, 256))
     with pytest.raises(ValueError, match="Head dimension too large; increase D_MAX"):
         ops.check_inputs(_t(1, 1, 8, 256), _t(1, 1, 8, 256), _t(1, 1, 8, 256))
 

@@ -51,6 +51,26 @@ def test_reference_style_entry_points(dev):
     assert_close("dV", np32(dV), gv, 1e-5)
 
 
+def test_reference_style_default_scale_uses_callers_head_dim(dev):
+    """sm_scale=None in the reference-order entry points is 1/sqrt(d) of the
+    caller's d (here 40, zero-padded to 64 inside), not of the padded d."""
+    print("[api] reference-style sm_scale=None, d=40", flush=True)
+    B, H, N, d = 1, 2, 160, 40
+    Q, K, V, dO = make_inputs(B, H, N, N, d, seed=7)
+    idx = causal_idx(B * H, N).to(dev)
+    args = (Q.to(dev), K.to(dev), V.to(dev), idx, idx)
+    a = sa.forward(*args, None, 1.5)
+    b = sa.forward(*args, d ** -0.5, 1.5)
+    assert torch.equal(a, b)
+    ga = sa.backward(*args, None, 1.5, dO.to(dev))
+    gb = sa.backward(*args, d ** -0.5, 1.5, dO.to(dev))
+    for x, y in zip(ga, gb):
+        assert torch.equal(x, y)
+    fw, _ = orc.attention(np32(Q), np32(K), np32(V), idx.cpu().numpy(), idx.cpu().numpy(),
+                          np32(dO), 1.5, d ** -0.5, 8, mode=orc.GRAD_REFERENCE)
+    assert_close("out", np32(a), fw.out, 1e-5)
+
+
 def test_default_int64_arange_indices_are_accepted(dev):
     """README.md:120-121 passes int64 arange indices (the reference would
     reject them, adasplashattention.cu:571); they are converted."""
