@@ -53,11 +53,10 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "unmeasured"
-HBM_TRAFFIC: dict = {}
-# L2-resident read bandwidth measured on the box (profiles/l2_read_bandwidth.md):
-# the ceiling of the passes whose tiles and gathered rows come from L2.
-L2_READ_MEASURED = 15.39e12
+HBM_TRAFFIC_SOURCES = "8051109d2a9e1562"
+HBM_TRAFFIC = {'bounds': 1109205, 'select': 103116095, 'tau': 34745407, 'refine': 74989494,
+               'compact': 2751144, 'forward': 207511046, 'bwd_dq_sparse': 248097115,
+               'bwd_dkdv_sparse': 276792874}
 
 
 def source_hash() -> str:
@@ -173,7 +172,6 @@ def roofline_of(model, ms):
     if hb > 1.0:
         # more algorithmic bytes than HBM can deliver in this time: they come
         # from L2, so the byte model is not an HBM bound for this kernel
-        r["l2_frac_algorithmic"] = round(model["bytes"] / t / L2_READ_MEASURED, 4)
         r["model_note"] = "algorithmic bytes above the HBM peak rate: L2-served, not an HBM bound"
     return r
 
@@ -379,8 +377,14 @@ def main():
             # bytes of the dense passes are mostly served by L2 (their
             # algorithmic HBM fraction can exceed 1)
             if traffic_ok and HBM_TRAFFIC.get(name):
-                kernels[name]["hbm_frac_measured"] = round(
-                    HBM_TRAFFIC[name] / (tot / cnt / 1e3) / PEAK_HBM, 4)
+                kr = kernels[name]
+                kr["hbm_frac_measured"] = round(HBM_TRAFFIC[name] / (tot / cnt / 1e3) / PEAK_HBM, 4)
+                if kr["bound"] == "hbm" and HBM_TRAFFIC[name] < 0.5 * kr["alg_bytes"]:
+                    # gathered rows that L2 serves: the byte model is an L2
+                    # rate, not an HBM one
+                    kr["model_note"] = (f"measured HBM traffic is "
+                                        f"{HBM_TRAFFIC[name] / kr['alg_bytes']:.2f} of the "
+                                        "algorithmic bytes: L2-served gathers")
     dominant = max(kernels, key=lambda n: kernels[n]["avg_ms"])
     roof = {kk: kernels[dominant][kk] for kk in ("bound", "achieved", "peak", "unit", "frac",
                                                  "traffic")}

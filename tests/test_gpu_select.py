@@ -96,3 +96,36 @@ def test_select_noncausal_and_scattered_positions(dev):
     st = _run(dev, S, qidx, kidx, k, 1.5, 1, 2)
     sel, c = _oracle(S, qidx, kidx, k, 1.5)
     _compare(st, sel, c)
+
+
+@pytest.mark.parametrize("with_topk", [True, False], ids=["topk", "values"])
+@pytest.mark.parametrize("kind,k", [("constant", 8), ("constant", 32), ("top_ties", 8),
+                                    ("top_ties", 32)])
+def test_select_overflow_rounds_bit_exact(dev, kind, k, with_topk):
+    """Rows whose candidates exceed the per-row capacity (k + 32 keys) run
+    overflow rounds; with every visible score equal ("constant") a row of n
+    keys needs about (n - k - 32) / 32 of them, and "top_ties" puts 100
+    equal maxima above random rows.  The rounds must give the oracle's
+    lowest-index ties bit for bit, and the status word must show them
+    without the round-bound flag."""
+    import splash_attention as sa
+
+    B, H, N = 1, 2, 320
+    rng = np.random.default_rng(11 + k)
+    if kind == "constant":
+        S = np.full((B * H, N, N), 0.25, np.float32)
+    else:
+        S = rng.normal(size=(B * H, N, N)).astype(np.float32)
+        for bh in range(B * H):
+            for i in range(N):
+                cols = rng.choice(i + 1, size=min(100, i + 1), replace=False)
+                S[bh, i, cols] = 5.0
+    idx = causal_idx(B * H, N)
+    print(f"[select] overflow rounds {kind} k={k} topk={with_topk}", flush=True)
+    st = _run(dev, S, idx, idx, k, 1.5, B, H, with_topk)
+    rounds = st.overflow_rounds()
+    print(f"[select] overflow rounds {kind} k={k}: {rounds}", flush=True)
+    assert not st.status_word() & sa._lib.STATUS_SELECT_ROUNDS
+    assert rounds >= (3 if kind == "constant" else 2), rounds
+    sel, c = _oracle(S, idx, idx, k, 1.5)
+    _compare(st, sel, c)
