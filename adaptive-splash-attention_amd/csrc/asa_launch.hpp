@@ -24,6 +24,13 @@ struct SupportMasks {
   uint16_t* mask;  // nullptr: no masks (the backward runs the dense passes)
 };
 
+// 32-row mask blocks (the reference's BLOCK_M = 32): the kernels still work
+// on 64-row query blocks, over the union of the two 32-row halves' key
+// blocks, and a half whose own mask row lacks a key block contributes
+// nothing to that tile.  half[(bh * nQH + h) * nKB + kb], nQH = ceil(NQ / 32),
+// is that mask; nullptr for 64-row blocks.
+__host__ __device__ inline int half_blocks(int NQ) { return (NQ + 31) / 32; }
+
 struct SelectParams {
   Dims d;
   const void* q;          // MFMA path
@@ -32,7 +39,8 @@ struct SelectParams {
   const int32_t* q_idx;
   const int32_t* k_idx;
   float* taus;
-  uint8_t* mask;
+  uint8_t* mask;          // [BH, nQB, nKB], 64-row blocks
+  uint8_t* half;          // 32-row blocks: also [BH, nQH, nKB] (else nullptr)
   int32_t* topk_idx;      // optional
   float* topk_val;        // optional
   float* tkv;             // workspace: sorted top-k values, [k][BH * NQ]
@@ -70,6 +78,7 @@ struct ForwardParams {
   void* out;
   float* norms;
   const int2* kbounds;  // (min, max) position per key block [BH * nKB], from the score pass
+  const uint8_t* half;  // 32-row mask (32-row blocks only, else nullptr)
   // Support masks (optional: sup.mask == nullptr writes none).
   SupportMasks sup;
 };
@@ -95,6 +104,7 @@ struct BackwardParams {
   const float* taus;
   const float* norms;
   const uint8_t* mask;
+  const uint8_t* half;  // 32-row mask (32-row blocks only, else nullptr)
   const int32_t* q_ptr;
   const int32_t* q_list;
   const int32_t* k_ptr;
@@ -127,6 +137,10 @@ size_t refine_lds_bytes(const Dims& d, bool bf16, int lcap);
 // 0: none fit, every row sweeps; -1: not even the sweep stage fits).
 int refine_list_capacity(const Dims& d, bool bf16, size_t max_lds);
 hipError_t launch_compact(const CompactParams& p, hipStream_t s);
+// 64-row mask from a 32-row one: mask[bh, qb, kb] = half[bh, 2 qb, kb] |
+// half[bh, 2 qb + 1, kb] (the second row when it exists).
+hipError_t launch_fold_halves(const uint8_t* half, uint8_t* mask, int BH, int NQ, int nQB,
+                              int nKB, hipStream_t s);
 hipError_t launch_forward(const ForwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_delta(const BackwardParams& p, bool bf16, hipStream_t s);
 hipError_t launch_bwd_dq(const BackwardParams& p, bool bf16, hipStream_t s);

@@ -128,6 +128,15 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
   f32x4 a1[D / 16], a2[D / 16];
   for (int db = 0; db < D / 16; ++db) a1[db] = a2[db] = f32x4{0.f, 0.f, 0.f, 0.f};
   float sw = 0.0f, swdp = 0.0f;
+  // 32-row mask blocks: the mask row of this wave's half; a tile that row
+  // lacks contributes nothing to the wave
+  const uint8_t* hrow = nullptr;
+  bool hvalid = true;
+  if (p.half) {
+    const int h = 2 * qb + (w >> 1), nQH = half_blocks(NQ);
+    hvalid = h < nQH;
+    hrow = p.half + (size_t(bh) * nQH + (hvalid ? h : 0)) * nKB;
+  }
 
   const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
   const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
@@ -151,9 +160,8 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
   __syncthreads();
   for (int e = e0; e < e1; ++e) {
     const int b = (e - e0) & 1;
+    const bool act = !hrow || (hvalid && hrow[ql[e]] != 0);  // wave-uniform
     f32x4 sacc[4], dacc[4];
-    rows_x_frag<D>(sacc, sm.K[b], qf, lane);
-    rows_x_frag<D>(dacc, sm.V[b], df, lane);
     auto weights = [&](auto partial) {
       for (int f = 0; f < 4; ++f)
         for (int r = 0; r < 4; ++r) {
@@ -174,10 +182,14 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
           }
         }
     };
-    if (sm.full[b] != 0) weights(std::false_type{});
-    else weights(std::true_type{});
-    tile_t_x_acc<D, true>(a1, sm.K[b], sacc, lane);
-    if constexpr (!REF) tile_t_x_acc<D, true>(a2, sm.K[b], dacc, lane);
+    if (act) {
+      rows_x_frag<D>(sacc, sm.K[b], qf, lane);
+      rows_x_frag<D>(dacc, sm.V[b], df, lane);
+      if (sm.full[b] != 0) weights(std::false_type{});
+      else weights(std::true_type{});
+      tile_t_x_acc<D, true>(a1, sm.K[b], sacc, lane);
+      if constexpr (!REF) tile_t_x_acc<D, true>(a2, sm.K[b], dacc, lane);
+    }
     if (e + 1 < e1) {
       put(b ^ 1);
       if (e + 2 < e1) fetch(e + 2);
@@ -225,10 +237,15 @@ struct alignas(16) QConst {
 };
 struct QConstStager {
   float nt, lo, hi, invn, c, cs;
-  __device__ __forceinline__ void load(const BackwardParams& p, size_t rows, size_t rbase, int qbase,
-                                       int NQ, float am1, int t) {
+  // Row qbase + t of head bh against key block kb: rows past NQ, and with
+  // 32-row mask blocks rows whose half's mask row lacks kb, get p = w = 0.
+  __device__ __forceinline__ void load(const BackwardParams& p, size_t rows, int bh, int qbase,
+                                       int kb, int NQ, float am1, int t) {
     if (t < kWave) {
-      const bool ok = qbase + t < NQ;
+      const size_t rbase = size_t(bh) * NQ;
+      bool ok = qbase + t < NQ;
+      if (p.half && ok)
+        ok = p.half[(size_t(bh) * half_blocks(NQ) + (qbase + t) / 32) * p.d.nKB + kb] != 0;
       const size_t r = rbase + (ok ? qbase + t : 0);
       const ClippedU u(am1, p.d.scale, ok ? p.taus[r] : 0.0f, ok);  // invalid rows: p = w = 0
       nt = u.nt;
@@ -267,7 +284,6 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dkdv_ke
   const bool jok = j < NK;
   const size_t krow = size_t(bh) * NK + (jok ? j : 0);
   const size_t rows = size_t(p.d.BH) * NQ;
-  const size_t rbase = size_t(bh) * NQ;
 
   const T* Qb = static_cast<const T*>(p.q) + size_t(bh) * NQ * D;
   const T* dOb = static_cast<const T*>(p.dout) + size_t(bh) * NQ * D;
@@ -303,7 +319,7 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dkdv_ke
     const int qbase = kl[e] * kBlock;
     st.load(Qb, dOb, qbase, NQ, t);
     ps.load(qidx, qbase, NQ, INT32_MAX, t);
-    qs.load(p, rows, rbase, qbase, NQ, am1, t);
+    qs.load(p, rows, bh, qbase, kb, NQ, am1, t);
   };
   auto put = [&](int b) {
     st.store(sm.Q[b], sm.dO[b], t);

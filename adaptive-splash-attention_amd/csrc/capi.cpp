@@ -44,7 +44,11 @@ int check_hip(hipError_t e, const char* what) {
 }
 
 struct Shape {
-  int BH, NQ, NK, D, k, nQB, nKB;
+  int BH, NQ, NK, D, k;
+  int nQB;  // 64-row query blocks (the kernels' tiles)
+  int nKB;
+  int bm;   // block_m: 64, or 32 (the reference's BLOCK_M)
+  int nQBm; // block_m-row query blocks: rows of the state's mask and CSR
   bool bf16;
   bool exact;  // ASA_TAU_EXACT
   float alpha, scale;
@@ -65,9 +69,12 @@ int validate(const asa_problem* p, Shape* sh) {
     return fail(ASA_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", p->head_dim);
   if (p->k_keep < 1 || p->k_keep > 128)
     return fail(ASA_ERR_INVALID_ARGUMENT, "k_keep %d out of range [1, 128]", p->k_keep);
-  if (p->block_m != 64 || p->block_n != 64)
-    return fail(ASA_ERR_UNSUPPORTED, "block_m x block_n = %d x %d not supported (64 x 64)",
-                p->block_m, p->block_n);
+  if ((p->block_m != 64 && p->block_m != 32) || p->block_n != 64)
+    return fail(ASA_ERR_UNSUPPORTED,
+                "block_m x block_n = %d x %d not supported (64 x 64 or 32 x 64)", p->block_m,
+                p->block_n);
+  if (p->block_m == 32 && p->tau_mode == ASA_TAU_EXACT)
+    return fail(ASA_ERR_UNSUPPORTED, "exact tau mode needs block_m = 64");
   if (p->dtype != ASA_DTYPE_F32 && p->dtype != ASA_DTYPE_BF16)
     return fail(ASA_ERR_INVALID_ARGUMENT, "unknown dtype %d", p->dtype);
   if (p->tau_mode != ASA_TAU_REFERENCE && p->tau_mode != ASA_TAU_EXACT)
@@ -76,7 +83,8 @@ int validate(const asa_problem* p, Shape* sh) {
   if (!std::isfinite(p->sm_scale)) return fail(ASA_ERR_INVALID_ARGUMENT, "sm_scale is not finite");
   const long long bh = (long long)p->batch * p->heads;
   const long long nqb = (p->nq + 63) / 64, nkb = (p->nk + 63) / 64;
-  if (bh > (1LL << 31) - 1 || nqb * nkb > (1LL << 31) - 1 ||
+  const long long nqbm = (p->nq + p->block_m - 1) / p->block_m;
+  if (bh > (1LL << 31) - 1 || nqbm * nkb > (1LL << 31) - 1 ||
       bh * (long long)p->nq > (1LL << 40) || bh * (long long)p->nk > (1LL << 40))
     return fail(ASA_ERR_INVALID_ARGUMENT, "problem too large");
   sh->BH = int(bh);
@@ -86,6 +94,8 @@ int validate(const asa_problem* p, Shape* sh) {
   sh->k = p->k_keep;
   sh->nQB = int(nqb);
   sh->nKB = int(nkb);
+  sh->bm = p->block_m;
+  sh->nQBm = int(nqbm);
   sh->bf16 = p->dtype == ASA_DTYPE_BF16;
   sh->exact = p->tau_mode == ASA_TAU_EXACT;
   // alpha is clamped to [1.05, 3] as the reference does (adasplashattention.cu:547).
@@ -116,24 +126,74 @@ size_t bwd_map_offset(const Shape& s) {
   return bwd_rec_offset(s) + size_t(s.BH) * s.NQ * sizeof(asa::RowRec);
 }
 
+size_t align16(size_t b) { return (b + 15) & ~size_t(15); }
+
+// With 32-row mask blocks the kernels run over the 64-row union of each
+// pair of 32-row mask rows: that mask and its CSR lists live in the
+// workspace (the state holds the block_m-row ones).
+struct Csr64 {
+  uint8_t* mask;
+  int32_t *q_ptr, *q_list, *k_ptr, *k_list;
+};
+
+size_t csr64_bytes(const Shape& s) {
+  const size_t blocks = size_t(s.BH) * s.nQB * s.nKB;
+  return align16(blocks) + align16(size_t(s.BH) * (s.nQB + 1) * 4) + align16(blocks * 4) +
+         align16(size_t(s.BH) * (s.nKB + 1) * 4) + align16(blocks * 4);
+}
+
+Csr64 csr64_at(const Shape& s, char* base) {
+  const size_t blocks = size_t(s.BH) * s.nQB * s.nKB;
+  Csr64 c;
+  c.mask = reinterpret_cast<uint8_t*>(base);
+  base += align16(blocks);
+  c.q_ptr = reinterpret_cast<int32_t*>(base);
+  base += align16(size_t(s.BH) * (s.nQB + 1) * 4);
+  c.q_list = reinterpret_cast<int32_t*>(base);
+  base += align16(blocks * 4);
+  c.k_ptr = reinterpret_cast<int32_t*>(base);
+  base += align16(size_t(s.BH) * (s.nKB + 1) * 4);
+  c.k_list = reinterpret_cast<int32_t*>(base);
+  return c;
+}
+
+// Workspace offsets of that 64-row structure in the forward and backward.
+size_t fwd_csr_offset(const Shape& s) {
+  return tkv_bytes(s) + align16(size_t(s.BH) * s.nKB * 2 * sizeof(int32_t));
+}
+size_t bwd_csr_offset(const Shape& s) {
+  return align16(bwd_map_offset(s) + size_t(s.BH) * s.nQB * s.nKB * sizeof(int32_t));
+}
+
+// The 64-row mask and lists the kernels use: the state's own (64-row
+// blocks) or the workspace's (32-row blocks).
+Csr64 kernel_csr(const Shape& s, const asa_state* st, void* workspace, size_t offset) {
+  if (s.bm == 64) return Csr64{st->mask, st->q_ptr, st->q_list, st->k_ptr, st->k_list};
+  return csr64_at(s, static_cast<char*>(workspace) + offset);
+}
+
 void sizes_of(const Shape& s, asa_sizes* z) {
   const size_t rows = size_t(s.BH) * s.NQ;
-  const size_t blocks = size_t(s.BH) * s.nQB * s.nKB;
+  const size_t blocks = size_t(s.BH) * s.nQB * s.nKB;    // 64-row tiles
+  const size_t mblocks = size_t(s.BH) * s.nQBm * s.nKB;  // block_m-row mask entries
   z->taus = rows * sizeof(float);
   z->norms = rows * sizeof(float);
-  z->mask = blocks;
-  z->q_ptr = size_t(s.BH) * (s.nQB + 1) * sizeof(int32_t);
-  z->q_list = blocks * sizeof(int32_t);
+  z->mask = mblocks;
+  z->q_ptr = size_t(s.BH) * (s.nQBm + 1) * sizeof(int32_t);
+  z->q_list = mblocks * sizeof(int32_t);
   z->k_ptr = size_t(s.BH) * (s.nKB + 1) * sizeof(int32_t);
-  z->k_list = blocks * sizeof(int32_t);
+  z->k_list = mblocks * sizeof(int32_t);
   z->topk_idx = rows * s.k * sizeof(int32_t);
   z->topk_val = rows * s.k * sizeof(float);
   z->sup_mask = blocks * 256 * sizeof(uint16_t);
   // forward: the rows' sorted top-k values and the key blocks' position
   // bounds; backward: two floats per row, a 16-byte record per row and an
-  // int per tile
-  const size_t fwd_ws = tkv_bytes(s) + size_t(s.BH) * s.nKB * 2 * sizeof(int32_t);
-  const size_t bwd_ws = bwd_map_offset(s) + blocks * sizeof(int32_t);
+  // int per tile; both, with 32-row blocks, the 64-row mask and lists
+  const size_t extra = s.bm == 32 ? csr64_bytes(s) : 0;
+  const size_t fwd_ws = s.bm == 32 ? fwd_csr_offset(s) + extra
+                                   : tkv_bytes(s) + size_t(s.BH) * s.nKB * 2 * sizeof(int32_t);
+  const size_t bwd_ws = s.bm == 32 ? bwd_csr_offset(s) + extra
+                                   : bwd_map_offset(s) + blocks * sizeof(int32_t);
   z->workspace = fwd_ws > bwd_ws ? fwd_ws : bwd_ws;
 }
 
@@ -179,9 +239,11 @@ std::mutex g_prof_mu;
 std::vector<Rec> g_recs;
 thread_local int g_open = -1;  // index of this thread's launch being timed
 
+// Score pass and compaction: the kernels' 64-row mask and lists into c64,
+// and with 32-row blocks the state's 32-row mask and lists as well.
 int run_select(const Shape& sh, const void* q, const void* k, const float* scores,
-               const int32_t* q_idx, const int32_t* k_idx, const asa_state* st, void* workspace,
-               hipStream_t s) {
+               const int32_t* q_idx, const int32_t* k_idx, const asa_state* st, const Csr64& c64,
+               void* workspace, hipStream_t s) {
   asa::SelectParams sp{};
   sp.tkv = static_cast<float*>(workspace);
   sp.kbounds = reinterpret_cast<int2*>(static_cast<char*>(workspace) + tkv_bytes(sh));
@@ -207,7 +269,8 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
   sp.q_idx = q_idx;
   sp.k_idx = k_idx;
   sp.taus = st->taus;
-  sp.mask = st->mask;
+  sp.mask = c64.mask;
+  sp.half = sh.bm == 32 ? st->mask : nullptr;
   sp.topk_idx = st->topk_idx;
   sp.topk_val = st->topk_val;
   sp.status = st->status;
@@ -231,12 +294,21 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
     if (int rc = check_hip(e, "refine kernel launch")) return rc;
   }
 
-  asa::CompactParams cp{sh.BH, sh.nQB, sh.nKB, st->mask, st->q_ptr, st->q_list, st->k_ptr,
-                        st->k_list};
+  asa::CompactParams cp{sh.BH, sh.nQB, sh.nKB, c64.mask, c64.q_ptr, c64.q_list, c64.k_ptr,
+                        c64.k_list};
   asa::profile_begin("compact", s);
   e = asa::launch_compact(cp, s);
   asa::profile_end(s);
-  return check_hip(e, "compact kernel launch");
+  if (int rc = check_hip(e, "compact kernel launch")) return rc;
+  if (sh.bm == 32) {
+    asa::CompactParams cm{sh.BH, sh.nQBm, sh.nKB, st->mask, st->q_ptr, st->q_list, st->k_ptr,
+                          st->k_list};
+    asa::profile_begin("compact_m", s);
+    e = asa::launch_compact(cm, s);
+    asa::profile_end(s);
+    if (int rc = check_hip(e, "compact kernel launch")) return rc;
+  }
+  return ASA_OK;
 }
 
 }  // namespace
@@ -300,7 +372,8 @@ int forward_impl(const Shape& sh, const void* q, const void* k, const void* v,
                  void* workspace, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
 
-  if (int rc = run_select(sh, q, k, nullptr, q_idx, k_idx, st, workspace, s)) return rc;
+  const Csr64 c64 = kernel_csr(sh, st, workspace, fwd_csr_offset(sh));
+  if (int rc = run_select(sh, q, k, nullptr, q_idx, k_idx, st, c64, workspace, s)) return rc;
 
   asa::ForwardParams fp{};
   fp.d = dims_of(sh);
@@ -310,8 +383,9 @@ int forward_impl(const Shape& sh, const void* q, const void* k, const void* v,
   fp.q_idx = q_idx;
   fp.k_idx = k_idx;
   fp.taus = st->taus;
-  fp.q_ptr = st->q_ptr;
-  fp.q_list = st->q_list;
+  fp.q_ptr = c64.q_ptr;
+  fp.q_list = c64.q_list;
+  fp.half = sh.bm == 32 ? st->mask : nullptr;
   fp.out = out;
   fp.norms = st->norms;
   fp.kbounds = reinterpret_cast<const int2*>(static_cast<const char*>(workspace) + tkv_bytes(sh));
@@ -414,11 +488,28 @@ int asa_backward(const asa_problem* p, int32_t grad_mode, const void* q, const v
   bp.k_idx = k_idx;
   bp.taus = st->taus;
   bp.norms = st->norms;
-  bp.mask = st->mask;
-  bp.q_ptr = st->q_ptr;
-  bp.q_list = st->q_list;
-  bp.k_ptr = st->k_ptr;
-  bp.k_list = st->k_list;
+  // with 32-row blocks, the 64-row union and its lists first (the same
+  // kernels as the forward's, so the tiles' list positions, which index the
+  // support masks, are the forward's)
+  const Csr64 c64 = kernel_csr(sh, st, workspace, bwd_csr_offset(sh));
+  if (sh.bm == 32) {
+    asa::profile_begin("fold_halves", s);
+    hipError_t ef = asa::launch_fold_halves(st->mask, c64.mask, sh.BH, sh.NQ, sh.nQB, sh.nKB, s);
+    asa::profile_end(s);
+    if (int rc = check_hip(ef, "fold kernel launch")) return rc;
+    asa::CompactParams cp{sh.BH, sh.nQB, sh.nKB, c64.mask, c64.q_ptr, c64.q_list, c64.k_ptr,
+                          c64.k_list};
+    asa::profile_begin("compact", s);
+    ef = asa::launch_compact(cp, s);
+    asa::profile_end(s);
+    if (int rc = check_hip(ef, "compact kernel launch")) return rc;
+  }
+  bp.mask = c64.mask;
+  bp.half = sh.bm == 32 ? st->mask : nullptr;
+  bp.q_ptr = c64.q_ptr;
+  bp.q_list = c64.q_list;
+  bp.k_ptr = c64.k_ptr;
+  bp.k_list = c64.k_list;
   bp.delta = static_cast<float*>(workspace);
   bp.dq = dq;
   bp.dk = dk;
@@ -469,7 +560,9 @@ int asa_select_from_scores(const asa_problem* p, const float* scores, const int3
   if (int rc = check_state(st, false)) return rc;
   if (!workspace) return fail(ASA_ERR_INVALID_ARGUMENT, "workspace is NULL");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (int rc = run_select(sh, nullptr, nullptr, scores, q_idx, k_idx, st, workspace, s)) return rc;
+  const Csr64 c64 = kernel_csr(sh, st, workspace, fwd_csr_offset(sh));
+  if (int rc = run_select(sh, nullptr, nullptr, scores, q_idx, k_idx, st, c64, workspace, s))
+    return rc;
   return ok();
 }
 

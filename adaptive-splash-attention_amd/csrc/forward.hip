@@ -71,6 +71,16 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   uint16_t* smask = nullptr;
   if constexpr (EMIT) smask = p.sup.mask + size_t(bh) * nQB * nKB * 256 + w * 64 + 4 * c16 + g;
 
+  // 32-row mask blocks: the mask row of this wave's half (rows 32 (w / 2)
+  // of the block); a tile that row lacks contributes nothing to the wave
+  const uint8_t* hrow = nullptr;
+  bool hvalid = true;
+  if (p.half) {
+    const int h = 2 * qb + (w >> 1), nQH = half_blocks(NQ);
+    hvalid = h < nQH;  // else every row of the half is past NQ
+    hrow = p.half + (size_t(bh) * nQH + (hvalid ? h : 0)) * nKB;
+  }
+
   const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
   const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
   const int e0 = qp[qb], e1 = qp[qb + 1];
@@ -93,8 +103,10 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   __syncthreads();
   for (int e = e0; e < e1; ++e) {
     const int b = (e - e0) & 1;
+    const int kb = ql[e];
+    const bool act = !hrow || (hvalid && hrow[kb] != 0);  // wave-uniform
     f32x4 acc[4];
-    rows_x_frag<D>(acc, sm.K[b], qf, lane);
+    if (act) rows_x_frag<D>(acc, sm.K[b], qf, lane);
     // p for every score, then masked: no per-score branches.  v = max(u, 0)
     // carries its sign bit where u <= 0 (SignedClip); with support masks the
     // lane's 16 bits of u > 0 are those sign bits, complemented.  The row
@@ -118,10 +130,13 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
           rowsum += pv;
         }
     };
-    const int kb = ql[e];
-    if (kb * kBlock + kBlock <= NK && kbnd[kb].y <= qmin) weights(std::false_type{});
-    else weights(std::true_type{});
-    tile_t_x_acc<D>(o, sm.V[b], acc, lane);
+    if (act) {
+      if (kb * kBlock + kBlock <= NK && kbnd[kb].y <= qmin) weights(std::false_type{});
+      else weights(std::true_type{});
+      tile_t_x_acc<D>(o, sm.V[b], acc, lane);
+    } else if constexpr (EMIT) {
+      smask[size_t(e) * 256] = 0;
+    }
     if (e + 1 < e1) {
       put(b ^ 1);
       if (e + 2 < e1) fetch(e + 2);

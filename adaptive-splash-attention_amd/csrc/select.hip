@@ -361,7 +361,7 @@ __host__ __device__ inline SelLayout sel_layout(int k, int cap, int nKB) {
   l.cnt = l.fl + kBlock * 4;
   l.ctl = l.cnt + kBlock * 4;
   l.bits = l.ctl + 16;
-  l.vlist = l.bits + align_up((nKB + 31) / 32 * 4, 16);
+  l.vlist = l.bits + align_up(2 * ((nKB + 31) / 32) * 4, 16);  // one bitmap per 32-row half
   l.total = l.vlist + align_up(nKB * 4, 16);
   return l;
 }
@@ -423,7 +423,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
 
   if (t < kBlock) s_cnt[t] = 0u;
   if (t < 4) s_ctl[t] = 0u;
-  for (int i = t; i < nbw; i += kThreads) s_bits[i] = 0u;
+  for (int i = t; i < 2 * nbw; i += kThreads) s_bits[i] = 0u;
 
   const int32_t* kidx = p.k_idx + size_t(bh) * NK;
   // Visible key blocks in ascending order, entry = block | class << 24, with
@@ -706,10 +706,12 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
     atomicMax(p.status, (uint32_t(max_round > 255 ? 255 : max_round) << 8));
 
   // ---------------- select: sort each row's candidates ----------------
-  // The top-k key blocks go into the block's mask bitmap: with at most 64
-  // key blocks as one register word per lane, OR-ed over the wave at the
-  // end (the per-entry LDS atomics would all hit the same two words).
+  // The top-k key blocks go into the mask bitmap of the row's 32-row half
+  // (wave w sorts rows 16 w .. 16 w + 15, half w / 2): with at most 64 key
+  // blocks as one register word per lane, OR-ed over the wave at the end
+  // (the per-entry LDS atomics would all hit the same two words).
   const bool kb_word = nKB <= 64;
+  uint32_t* s_hbits = s_bits + (w >> 1) * nbw;
   uint64_t kbm = 0;
   auto emit = [&](int r, int e, uint64_t key) {
     if (e >= k || q0 + r >= NQ) return;
@@ -725,7 +727,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
     if (idx >= 0) {
       const int kb = idx / kBlock;
       if (kb_word) kbm |= uint64_t(1) << kb;
-      else atomicOr(&s_bits[kb >> 5], 1u << (kb & 31));
+      else atomicOr(&s_hbits[kb >> 5], 1u << (kb & 31));
     }
   };
   auto ncand = [&](int r) -> int { return (q0 + r < NQ) ? min(int(s_cnt[r]), cap) : 0; };
@@ -803,7 +805,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
       if (sel) {
         const int kb = idx / kBlock;
         if (kb_word) kbm |= uint64_t(1) << kb;
-        else atomicOr(&s_bits[kb >> 5], 1u << (kb & 31));
+        else atomicOr(&s_hbits[kb >> 5], 1u << (kb & 31));
       }
     }
   };
@@ -840,15 +842,28 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
     const uint32_t lo = group_reduce_bits(uint32_t(kbm), bor);
     const uint32_t hi = group_reduce_bits(uint32_t(kbm >> 32), bor);
     if (L == 0) {
-      if (lo) atomicOr(&s_bits[0], lo);
-      if (hi) atomicOr(&s_bits[1], hi);
+      if (lo) atomicOr(&s_hbits[0], lo);
+      if (hi) atomicOr(&s_hbits[1], hi);  // nonzero only when nKB > 32 (nbw = 2)
     }
   }
   __syncthreads();
 
   // ---------------- mask row; sorted values for the tau kernel ----------------
+  // the 64-row mask is the union of the halves; with 32-row blocks each
+  // half's row is written too (the second only when the block has one)
   uint8_t* mrow = p.mask + (size_t(bh) * nQB + qb) * nKB;
-  for (int kb = t; kb < nKB; kb += kThreads) mrow[kb] = uint8_t((s_bits[kb >> 5] >> (kb & 31)) & 1u);
+  const int nQH = half_blocks(NQ);
+  uint8_t* hrow = p.half ? p.half + (size_t(bh) * nQH + 2 * qb) * nKB : nullptr;
+  const bool second = 2 * qb + 1 < nQH;
+  for (int kb = t; kb < nKB; kb += kThreads) {
+    const uint32_t b0 = (s_bits[kb >> 5] >> (kb & 31)) & 1u;
+    const uint32_t b1 = (s_bits[nbw + (kb >> 5)] >> (kb & 31)) & 1u;
+    mrow[kb] = uint8_t(b0 | b1);
+    if (hrow) {
+      hrow[kb] = uint8_t(b0);
+      if (second) hrow[nKB + kb] = uint8_t(b1);
+    }
+  }
   const size_t rows = size_t(p.d.BH) * NQ;
   for (int i = t; i < k * kBlock; i += kThreads) {
     const int e = i >> 6, r = i & 63;

@@ -40,22 +40,24 @@ __all__ = [
 __version__ = "0.1.0"
 
 
-def forward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, k_keep: int = 8):
+def forward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, k_keep: int = 8,
+            block_m: int = 64):
     """Reference-compatible native forward (adasplashattention.cu:537-609).
     ``sm_scale=None`` means 1/sqrt(d) of the caller's head dimension (before
-    any zero padding)."""
+    any zero padding).  block_m = 32 gives the reference's default mask blocks
+    (BLOCK_M, :8-9)."""
     ops.check_shapes(Q, K, V)
     d, dtype = Q.size(-1), Q.dtype
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(d)
     Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     out, _ = ops.splash_forward(Q, K, V, qi, ki, ops.clamp_alpha(alpha), k_keep, sm_scale,
-                                with_support=False)
+                                with_support=False, block_m=block_m)
     return ops.from_kernel_layout(out, d, dtype)
 
 
 def backward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, dOut, k_keep: int = 8,
-             grad_mode: str = "reference"):
+             grad_mode: str = "reference", block_m: int = 64):
     """Reference-compatible native backward (adasplashattention.cu:611-700):
     reruns the selection, then returns [dQ, dK, dV].  ``sm_scale=None`` as
     in ``forward``."""
@@ -68,6 +70,6 @@ def backward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, dOut, k_keep:
         sm_scale = 1.0 / math.sqrt(d)
     Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     a = ops.clamp_alpha(alpha)
-    out, st = ops.splash_forward(Q, K, V, qi, ki, a, k_keep, sm_scale)
+    out, st = ops.splash_forward(Q, K, V, qi, ki, a, k_keep, sm_scale, block_m=block_m)
     grads = ops.splash_backward(Q, K, V, qi, ki, out, dOut, st, a, k_keep, sm_scale, grad_mode)
     return [ops.from_kernel_layout(g, d, dtype) for g in grads]

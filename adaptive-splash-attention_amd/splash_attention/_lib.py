@@ -12,7 +12,7 @@ import threading
 
 from . import _build
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 ASA_OK = 0
 ASA_ERR_INVALID_ARGUMENT = 1

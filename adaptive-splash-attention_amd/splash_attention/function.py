@@ -24,11 +24,11 @@ from . import library, ops
 class SplashAttentionFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode,
-                tau_mode="reference"):
+                tau_mode="reference", block_m=64):
         # support lists only when a backward can follow
         out, st = ops.splash_forward(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale,
                                      with_support=any(ctx.needs_input_grad[:3]),
-                                     tau_mode=tau_mode)
+                                     tau_mode=tau_mode, block_m=block_m)
         ctx.params = (alpha, k_keep, sm_scale, grad_mode)
         ctx.save_for_backward(Q, K, V, Q_idx, K_idx, out, *st.tensors())
         return out
@@ -41,12 +41,12 @@ class SplashAttentionFunction(torch.autograd.Function):
         st = ops.SplashState.from_tensors(state)
         dQ, dK, dV = ops.splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st, alpha, k_keep,
                                          sm_scale, grad_mode)
-        return dQ, dK, dV, None, None, None, None, None, None, None
+        return dQ, dK, dV, None, None, None, None, None, None, None, None
 
 
 def splash_attention(Q, K, V, Q_idx=None, K_idx=None, alpha: float = 1.5, k_keep: int = 8,
                      sm_scale: float | None = None, grad_mode: str = "entmax",
-                     tau_mode: str = "reference") -> torch.Tensor:
+                     tau_mode: str = "reference", block_m: int = 64) -> torch.Tensor:
     """Block-sparse alpha-entmax attention, differentiable in Q, K and V.
 
     Q: [B, H, NQ, d]; K, V: [B, H, NK, d], d <= 128; float32, bfloat16 or
@@ -59,13 +59,16 @@ def splash_attention(Q, K, V, Q_idx=None, K_idx=None, alpha: float = 1.5, k_keep
     row's top-k scores; "exact" solves the alpha-entmax threshold over every
     visible key of the row and activates the key blocks of its support, so
     the output is dense alpha-entmax attention (no reference counterpart).
+    block_m: query rows per mask block, 64 (default) or 32 (the reference's
+    compile-time BLOCK_M, adasplashattention.cu:8-9; reference tau mode).
     """
     if grad_mode not in ops.GRAD_MODES:
         raise ValueError(f"grad_mode must be one of {sorted(ops.GRAD_MODES)}")
     ops.check_tau_mode(tau_mode)
+    ops.check_block_m(block_m)
     if torch.compiler.is_compiling():
         return library.attention(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode,
-                                 tau_mode)
+                                 tau_mode, block_m)
     # eager: the autograd function, without the custom-operator dispatch;
     # check_inputs' padding and widening are differentiable torch ops
     d, dtype = Q.size(-1), Q.dtype
@@ -73,5 +76,5 @@ def splash_attention(Q, K, V, Q_idx=None, K_idx=None, alpha: float = 1.5, k_keep
         sm_scale = d ** -0.5
     Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     out = SplashAttentionFunction.apply(Q, K, V, qi, ki, float(alpha), int(k_keep),
-                                        float(sm_scale), grad_mode, tau_mode)
+                                        float(sm_scale), grad_mode, tau_mode, int(block_m))
     return ops.from_kernel_layout(out, d, dtype)

@@ -32,7 +32,7 @@ def _nblocks(n: int, b: int) -> int:
 @torch.library.custom_op(f"{_NS}::forward", mutates_args=(), device_types="cuda")
 def forward_op(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx: Optional[Tensor],
                alpha: float, k_keep: int, sm_scale: float, grad_mode: str,
-               tau_mode: str = "reference"
+               tau_mode: str = "reference", block_m: int = 64
                ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """out, taus, norms, mask, q_ptr, q_list, k_ptr, k_list and the support
     masks sup_mask (grad_mode is recorded for the backward only).  out is in
@@ -40,17 +40,18 @@ def forward_op(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx: 
     float16 as float32), so that the backward sees the unrounded output."""
     q, k, v, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     out, st = ops.splash_forward(q, k, v, qi, ki, alpha, k_keep, sm_scale, with_support=True,
-                                 tau_mode=tau_mode)
+                                 tau_mode=tau_mode, block_m=block_m)
     return (out, *st.tensors())
 
 
 @forward_op.register_fake
 def _forward_fake(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode,
-                  tau_mode="reference"):
+                  tau_mode="reference", block_m=64):
     B, H, NQ, d = Q.shape
     NK = K.shape[2]
     BH = B * H
-    nQB, nKB = _nblocks(NQ, ops.BLOCK_M), _nblocks(NK, ops.BLOCK_N)
+    nQB, nKB = _nblocks(NQ, block_m), _nblocks(NK, ops.BLOCK_N)
+    nQ64 = _nblocks(NQ, 64)
     f32 = dict(dtype=torch.float32, device=Q.device)
     i32 = dict(dtype=torch.int32, device=Q.device)
     odt = torch.float32 if Q.dtype == torch.float16 else Q.dtype
@@ -59,7 +60,7 @@ def _forward_fake(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode,
             torch.empty((BH, nQB, nKB), dtype=torch.uint8, device=Q.device),
             torch.empty((BH, nQB + 1), **i32), torch.empty((BH, nQB * nKB), **i32),
             torch.empty((BH, nKB + 1), **i32), torch.empty((BH, nKB * nQB), **i32),
-            torch.empty((BH, nQB * nKB, 4, 64), dtype=torch.int16, device=Q.device))
+            torch.empty((BH, nQ64 * nKB, 4, 64), dtype=torch.int16, device=Q.device))
 
 
 @torch.library.custom_op(f"{_NS}::backward", mutates_args=(), device_types="cuda")
@@ -84,7 +85,7 @@ def _backward_fake(Q, K, V, Q_idx, K_idx, out, dout, taus, norms, mask, q_ptr, q
 
 
 def _setup_context(ctx, inputs, output):
-    Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode, tau_mode = inputs
+    Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode, tau_mode, block_m = inputs
     out, *state = output
     ctx.params = (alpha, k_keep, sm_scale, grad_mode)
     ctx.save_for_backward(Q, K, V, Q_idx, K_idx, out, *state)
@@ -95,7 +96,7 @@ def _backward(ctx, dout, *unused_state_grads):
     alpha, k_keep, sm_scale, grad_mode = ctx.params
     dQ, dK, dV = backward_op(Q, K, V, Q_idx, K_idx, out, dout.contiguous(), *state, alpha, k_keep,
                              sm_scale, grad_mode)
-    return dQ, dK, dV, None, None, None, None, None, None, None
+    return dQ, dK, dV, None, None, None, None, None, None, None, None
 
 
 forward_op.register_autograd(_backward, setup_context=_setup_context)
@@ -103,12 +104,12 @@ forward_op.register_autograd(_backward, setup_context=_setup_context)
 
 def attention(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx: Optional[Tensor],
               alpha: float, k_keep: int, sm_scale: Optional[float], grad_mode: str,
-              tau_mode: str = "reference") -> Tensor:
+              tau_mode: str = "reference", block_m: int = 64) -> Tensor:
     """Shape-checked call of ``adasplash::forward``; returns the output in
     the caller's head dimension and dtype."""
     ops.check_shapes(Q, K, V, k_keep)
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(Q.size(-1))
     out = forward_op(Q, K, V, Q_idx, K_idx, float(alpha), int(k_keep), float(sm_scale),
-                     grad_mode, tau_mode)[0]
+                     grad_mode, tau_mode, int(block_m))[0]
     return ops.from_kernel_layout(out, Q.size(-1), Q.dtype)

@@ -16,7 +16,8 @@ import torch.nn.functional as F
 
 from . import _lib
 
-BLOCK_M = 64
+BLOCK_M = 64             # default query rows per mask block
+BLOCK_MS = (64, 32)      # supported block_m values
 BLOCK_N = 64
 MAX_HEAD_DIM = 128
 MAX_K_KEEP = 128
@@ -38,7 +39,7 @@ class SplashState:
     """Selection state of one forward call (see asa_state in adasplash.h)."""
     taus: torch.Tensor       # [BH, NQ] float32
     norms: torch.Tensor      # [BH, NQ] float32, sum of p per row
-    mask: torch.Tensor       # [BH, nQB, nKB] uint8
+    mask: torch.Tensor       # [BH, nQB, nKB] uint8, nQB = ceil(NQ / block_m)
     q_ptr: torch.Tensor      # [BH, nQB+1] int32 (reference Qi_ptr)
     q_list: torch.Tensor     # [BH, nQB*nKB] int32 (reference Qi_idx)
     k_ptr: torch.Tensor      # [BH, nKB+1] int32
@@ -47,7 +48,7 @@ class SplashState:
     topk_val: torch.Tensor | None = None  # [BH, NQ, k] float32
     # support masks (asa_state.sup_mask): the (row, key) pairs with u > 0,
     # 16 bits per (tile, 16-row wave, lane) as uint16 bit patterns
-    sup_mask: torch.Tensor | None = None  # [BH, nQB*nKB, 4, 64] int16
+    sup_mask: torch.Tensor | None = None  # [BH, ceil(NQ/64)*nKB, 4, 64] int16
     # per-call status word (asa_state.status): written on the stream by the
     # forward, read only by check_status()
     status: torch.Tensor | None = None    # [1] int32
@@ -236,13 +237,30 @@ def check_tau_mode(tau_mode: str) -> int:
     return TAU_MODES[tau_mode]
 
 
+def check_block_m(block_m) -> int:
+    """Query rows per mask block: 64, or 32 (the reference's compile-time
+    BLOCK_M, adasplashattention.cu:8-9)."""
+    if int(block_m) not in BLOCK_MS:
+        raise ValueError(f"block_m must be one of {BLOCK_MS}, got {block_m}")
+    return int(block_m)
+
+
+def block_m_of(st: "SplashState", NQ: int) -> int:
+    """The block_m a state was written with, from its mask's row count (for
+    NQ <= 32 both give one identical row; 64 is returned)."""
+    return 64 if st.mask.shape[1] == -(-NQ // 64) else 32
+
+
 def make_problem(B, H, NQ, NK, d, dtype, alpha, k_keep, sm_scale,
-                 tau_mode: str = "reference") -> _lib.Problem:
+                 tau_mode: str = "reference", block_m: int = BLOCK_M) -> _lib.Problem:
     if not (1 <= int(k_keep) <= MAX_K_KEEP):
         raise ValueError(f"k_keep {k_keep} out of range [1, {MAX_K_KEEP}]")
+    block_m = check_block_m(block_m)
+    if block_m == 32 and tau_mode == "exact":
+        raise ValueError("tau_mode 'exact' needs block_m = 64")
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(d)
-    return _lib.Problem(B, H, NQ, NK, d, int(k_keep), BLOCK_M, BLOCK_N, float(alpha),
+    return _lib.Problem(B, H, NQ, NK, d, int(k_keep), block_m, BLOCK_N, float(alpha),
                         float(sm_scale), _DTYPES[dtype] if isinstance(dtype, torch.dtype) else dtype,
                         check_tau_mode(tau_mode))
 
@@ -250,7 +268,8 @@ def make_problem(B, H, NQ, NK, d, dtype, alpha, k_keep, sm_scale,
 def alloc_state(p: _lib.Problem, device, with_topk: bool = False,
                 with_support: bool = False) -> SplashState:
     BH = p.batch * p.heads
-    nQB = -(-p.nq // BLOCK_M)
+    nQB = -(-p.nq // p.block_m)   # rows of the mask and CSR lists
+    nQ64 = -(-p.nq // 64)         # 64-row tiles of the support masks
     nKB = -(-p.nk // BLOCK_N)
     i32 = dict(device=device, dtype=torch.int32)
     f32 = dict(device=device, dtype=torch.float32)
@@ -268,7 +287,7 @@ def alloc_state(p: _lib.Problem, device, with_topk: bool = False,
         st.topk_idx = torch.empty((BH, p.nq, p.k_keep), **i32)
         st.topk_val = torch.empty((BH, p.nq, p.k_keep), **f32)
     if with_support:
-        st.sup_mask = torch.empty((BH, nQB * nKB, 4, 64), device=device, dtype=torch.int16)
+        st.sup_mask = torch.empty((BH, nQ64 * nKB, 4, 64), device=device, dtype=torch.int16)
     return st
 
 
@@ -280,16 +299,19 @@ def workspace(p: _lib.Problem, device) -> torch.Tensor:
 
 def splash_forward(Q, K, V, Q_idx, K_idx, alpha: float, k_keep: int, sm_scale=None,
                    with_topk: bool = False, with_support: bool = True,
-                   tau_mode: str = "reference", noalloc: bool = False):
+                   tau_mode: str = "reference", noalloc: bool = False,
+                   block_m: int = BLOCK_M):
     """Forward pass; returns (out, SplashState).  Inputs as check_inputs() returns them.
     with_support records the rows' support masks for the sparse backward
     (skip it for inference).  tau_mode "exact" solves tau over the whole
     visible row instead of the top-k (see TAU_MODES).  noalloc=True calls
     asa_forward_noalloc, whose workspace is the library's own device array
-    (no workspace tensor is allocated; calls that overlap on one GPU race)."""
+    (no workspace tensor is allocated; calls that overlap on one GPU race).
+    block_m = 32 gives the reference's 32-row mask blocks."""
     lib = _lib.load()
     B, H, NQ, d = Q.shape
-    p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale, tau_mode)
+    p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale, tau_mode,
+                     block_m)
     st = alloc_state(p, Q.device, with_topk, with_support)
     out = torch.empty_like(Q)
     cst = st.c_struct()
@@ -322,12 +344,13 @@ def _as_kernel_operand(t: torch.Tensor, Q: torch.Tensor, name: str) -> torch.Ten
 
 def splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st: SplashState, alpha: float,
                     k_keep: int, sm_scale=None, grad_mode: str = "entmax"):
-    """Gradients (dQ, dK, dV) from a forward's state."""
+    """Gradients (dQ, dK, dV) from a forward's state (of either block_m)."""
     lib = _lib.load()
     if grad_mode not in GRAD_MODES:
         raise ValueError(f"grad_mode must be one of {sorted(GRAD_MODES)}")
     B, H, NQ, d = Q.shape
-    p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale)
+    p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale,
+                     block_m=block_m_of(st, NQ))
     dout = _as_kernel_operand(dout, Q, "dOut")
     if out is not None:
         out = _as_kernel_operand(out, Q, "Out")
@@ -347,7 +370,8 @@ def splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st: SplashState, alpha: fl
 
 
 def select_from_scores(scores, Q_idx, K_idx, alpha: float, k_keep: int, batch: int = 1,
-                       heads: int | None = None, with_topk: bool = True) -> SplashState:
+                       heads: int | None = None, with_topk: bool = True,
+                       block_m: int = BLOCK_M) -> SplashState:
     """Top-k, tau, block mask and CSR lists from given fp32 scores [BH, NQ, NK]
     (no reference counterpart: exposes the reference's selection stage,
     adasplashattention.cu:199-216, for checks on identical scores).
@@ -370,7 +394,8 @@ def select_from_scores(scores, Q_idx, K_idx, alpha: float, k_keep: int, batch: i
         raise ValueError("batch * heads must equal scores.shape[0]")
     qi = _index(Q_idx, BH, NQ, batch, heads, scores.device, "Q_idx")
     ki = _index(K_idx, BH, NK, batch, heads, scores.device, "K_idx")
-    p = make_problem(batch, heads, NQ, NK, 64, torch.float32, alpha, k_keep, 1.0)
+    p = make_problem(batch, heads, NQ, NK, 64, torch.float32, alpha, k_keep, 1.0,
+                     block_m=block_m)
     st = alloc_state(p, scores.device, with_topk=with_topk)
     scores = scores.contiguous()
     ws = workspace(p, scores.device)

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define ASA_ABI_VERSION 4
+#define ASA_ABI_VERSION 5
 
 typedef enum asa_status {
   ASA_OK = 0,
@@ -92,7 +92,10 @@ typedef struct asa_problem {
   int32_t nk;
   int32_t head_dim; /* 64 or 128 (reference limit: <= 128, :542)         */
   int32_t k_keep;   /* 1..128 (reference: compile-time 8, :17-19)        */
-  int32_t block_m;  /* query rows per mask block: 64                      */
+  int32_t block_m;  /* query rows per mask block: 64, or 32 (the
+                     * reference's BLOCK_M, :8-9; reference tau mode
+                     * only): the mask and CSR lists of the state are
+                     * then per 32 rows, as the reference's            */
   int32_t block_n;  /* keys per mask block: 64                            */
   float alpha;      /* clamped to [1.05, 3]                               */
   float sm_scale;
@@ -117,8 +120,14 @@ typedef struct asa_problem {
  *                                   -1e6 in empty slots
  * Support masks, optional (NULL: not written, and the backward computes
  * every active block densely):
- *   sup_mask uint16  [BH, nQB*nKB, 4, 64]  for the tile at the head's q_list
- *                                   position e (query block qb, key block
+ *   sup_mask uint16  [BH, nQ64*nKB, 4, 64], nQ64 = ceil(nq / 64): for the
+ *                                   tile at the head's position e of the
+ *                                   64-row list (q_list itself when
+ *                                   block_m = 64; with block_m = 32 the
+ *                                   list of the union of mask rows 2i and
+ *                                   2i + 1, which the library derives in
+ *                                   its workspace) (64-row query block
+ *                                   qb, key block
  *                                   kb), bit 4f + r of element [e][w][4c + g]
  *                                   is set iff the forward weighted row
  *                                   qb*64 + 16w + c, key kb*64 + 16f + 4g + r

@@ -32,12 +32,15 @@ GRAD_REFERENCE = 1
 
 
 def key_block_grads(Q, K, V, dO, q_idx, k_idx, taus, mask, alpha: float, scale: float,
-                    blocks, mode: int = GRAD_ENTMAX, block: int = 64, chunk: int = 256):
+                    blocks, mode: int = GRAD_ENTMAX, block: int = 64, chunk: int = 256,
+                    block_m: int | None = None):
     """dK, dV of one head's key blocks `blocks` (list of block indices).
 
     Q, dO [NQ, d]; K, V [NK, d]; q_idx [NQ], k_idx [NK]; taus [NQ];
-    mask [nQB, nKB] (nonzero: active).  Returns (dK, dV), each
+    mask [nQB, nKB] (nonzero: active) with query blocks of block_m rows
+    (default: `block`, the key-block width).  Returns (dK, dV), each
     [len(blocks) * block, d] float64 (rows past NK are zero)."""
+    block_m = block if block_m is None else block_m
     Q, K, V, dO = (np.asarray(t, np.float64) for t in (Q, K, V, dO))
     q_idx = np.asarray(q_idx, np.int64)
     k_idx = np.asarray(k_idx, np.int64)
@@ -59,7 +62,7 @@ def key_block_grads(Q, K, V, dO, q_idx, k_idx, taus, mask, alpha: float, scale: 
         r1 = min(r0 + chunk, NQ)
         rows = np.arange(r0, r1)
         s = np.clip((Q[r0:r1] @ K.T) * scale, -10.0, 10.0)
-        live = (k_idx[None, :] <= q_idx[rows, None]) & mask[(rows // block)[:, None],
+        live = (k_idx[None, :] <= q_idx[rows, None]) & mask[(rows // block_m)[:, None],
                                                             key_block[None, :]]
         u = am1 * s - taus[rows, None]
         pos_u = live & (u > 0)

@@ -46,7 +46,7 @@ def assert_close(name, got, want, tol, floor: float = 1e-30):
     return e
 
 
-def oracle_at_gpu_tau(Q, K, V, dO, qidx, kidx, alpha, scale, k, gpu_taus, mode=0):
+def oracle_at_gpu_tau(Q, K, V, dO, qidx, kidx, alpha, scale, k, gpu_taus, mode=0, block_m=64):
     """Oracle forward/backward evaluated at the GPU's taus.
 
     The reference's tau recurrence stops as soon as |f| < 1e-4
@@ -60,10 +60,10 @@ def oracle_at_gpu_tau(Q, K, V, dO, qidx, kidx, alpha, scale, k, gpu_taus, mode=0
     """
     from oracle import oracle as orc
 
-    own = orc.forward(Q, K, V, qidx, kidx, alpha, scale, k)
-    at = orc.forward(Q, K, V, qidx, kidx, alpha, scale, k, taus_in=gpu_taus)
+    own = orc.forward(Q, K, V, qidx, kidx, alpha, scale, k, block_m=block_m)
+    at = orc.forward(Q, K, V, qidx, kidx, alpha, scale, k, block_m=block_m, taus_in=gpu_taus)
     grads = orc.backward(Q, K, V, qidx, kidx, dO, alpha, scale, at.taus, at.csr.q_ptr,
-                         at.csr.q_list, mode)
+                         at.csr.q_list, mode, block_m=block_m)
     return own, at, grads
 
 

@@ -67,7 +67,7 @@ def test_query_sizes_headline():
     (dict(head_dim=96), 2, "head_dim 96 not supported"),
     (dict(k_keep=0), 1, "k_keep"),
     (dict(k_keep=129), 1, "k_keep"),
-    (dict(block_m=32), 2, "block_m"),
+    (dict(block_m=16), 2, "block_m"),
     (dict(nq=0), 1, "nq"),
     (dict(batch=0), 1, "batch"),
     (dict(dtype=7), 1, "dtype"),

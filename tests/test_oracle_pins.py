@@ -65,19 +65,22 @@ def test_topk_matches_brute_force(kind):
     np.testing.assert_array_equal(sel.topk_val.astype(np.float64), val)
 
 
-def test_mask_and_csr_closed_form():
+@pytest.mark.parametrize("block_m", [64, 32])
+def test_mask_and_csr_closed_form(block_m):
+    """The mask is the union over each block_m rows of their top-k key
+    blocks (adasplashattention.cu:210-216), the CSR its ascending lists."""
     rng = np.random.default_rng(5)
     BH, NQ, NK, k = 3, 200, 330, 5
     S = rng.normal(size=(BH, NQ, NK)).astype(np.float32)
     vis = np.ones((BH, NQ, NK), np.uint8)
-    sel = orc.select(S, vis, k, 1.5)
-    nQB, nKB = -(-NQ // 64), -(-NK // 64)
+    sel = orc.select(S, vis, k, 1.5, block_m=block_m)
+    nQB, nKB = -(-NQ // block_m), -(-NK // 64)
     want = np.zeros((BH, nQB, nKB), np.uint8)
     for b in range(BH):
         for i in range(NQ):
             for j in sel.topk_idx[b, i]:
                 if j >= 0:
-                    want[b, i // 64, j // 64] = 1
+                    want[b, i // block_m, j // 64] = 1
     np.testing.assert_array_equal(sel.mask, want)
     c = orc.csr(sel.mask)
     for b in range(BH):
@@ -281,6 +284,46 @@ def test_forward_output_in_convex_hull_of_visible_values():
             assert np.all(fw.out[b, i] >= lo) and np.all(fw.out[b, i] <= hi)
 
 
+def test_forward_block_m32_sums_over_the_rows_own_blocks():
+    """With 32-row mask blocks a row weights the visible keys of the key
+    blocks active for ITS 32-row block (adasplashattention.cu:278-297 with
+    iQB = q / BLOCK_M), not those of its 64-row pair; restated in numpy
+    from the top-k blocks (closed form above) and the oracle's tau."""
+    rng = np.random.default_rng(3)
+    BH, N, d = 2, 256, 64
+    # 32-row half h of the queries has its top-2 keys ("magnets") in key
+    # block h % 4, so the two halves of a 64-row block pick different key
+    # blocks; every other key scores near 0, within the top-2 tau's reach
+    # (u > 0), so a row weights every key of each block active for it
+    Q = rng.normal(size=(BH, N, d)) * 0.1
+    K = rng.normal(size=(BH, N, d)) * 0.1
+    V = rng.normal(size=(BH, N, d))
+    for h in range(N // 32):
+        Q[:, 32 * h:32 * h + 32, h] += 1.0
+        K[:, 64 * (h % 4) + h, h] = 5.0
+        K[:, 64 * (h % 4) + 8 + h, h] = 4.0
+    idx = np.broadcast_to(np.arange(N, dtype=np.int32), (BH, N)).copy()
+    qi = np.full((BH, N), N - 1, np.int32)  # every key visible
+    alpha, scale, k = 1.5, 0.125, 2
+    fw = orc.forward(Q, K, V, qi, idx, alpha, scale, k, block_m=32, precision="f64")
+    fw64 = orc.forward(Q, K, V, qi, idx, alpha, scale, k, block_m=64, precision="f64")
+    assert fw.mask.shape == (2, 8, 4)
+    for h in range(N // 32):
+        np.testing.assert_array_equal(fw.mask[:, h], np.eye(4, dtype=np.uint8)[[h % 4] * BH])
+    for b in range(BH):
+        for i in range(N):
+            blocks = set(j // 64 for r in range(i // 32 * 32, min(i // 32 * 32 + 32, N))
+                         for j in fw.topk_idx[b, r] if j >= 0)
+            keys = [j for j in range(N) if j // 64 in blocks]
+            s = np.clip(Q[b, i] @ K[b, keys].T * scale, -10, 10)
+            u = (alpha - 1) * s - fw.taus[b, i]
+            p = np.where(u > 0, np.maximum(u, 1e-8) ** (1 / (alpha - 1)), 0.0)
+            want = (p[:, None] * V[b, keys]).sum(0) / (p.sum() + 1e-8)
+            np.testing.assert_allclose(fw.out[b, i], want, rtol=1e-10, atol=1e-12)
+    # the 64-row blocks admit the other half's key block: every row differs
+    assert (np.abs(fw.out - fw64.out).max(-1) > 1e-2).all()
+
+
 # ---------------------------------------------------------------- backward
 
 
@@ -374,8 +417,9 @@ def test_sparsemax_gradient_centres_dp_on_support():
 
 
 @pytest.mark.parametrize("mode", [orc.GRAD_ENTMAX, orc.GRAD_REFERENCE])
-@pytest.mark.parametrize("alpha,causal", [(1.5, True), (2.0, False), (1.25, True)])
-def test_key_block_grads_match_oracle_backward(mode, alpha, causal):
+@pytest.mark.parametrize("alpha,causal,block_m", [(1.5, True, 64), (2.0, False, 64),
+                                                  (1.25, True, 64), (1.5, True, 32)])
+def test_key_block_grads_match_oracle_backward(mode, alpha, causal, block_m):
     """oracle/keyblock.py (the chunked restatement the full-size GPU tests
     use for sampled key blocks) equals asao_backward on whole heads."""
     from oracle import keyblock as KB
@@ -385,13 +429,14 @@ def test_key_block_grads_match_oracle_backward(mode, alpha, causal):
     Q, K, V, dO = (rng.normal(size=(BH, N, d)) for _ in range(4))
     ki = np.tile(np.arange(N, dtype=np.int32), (BH, 1))
     qi = ki.copy() if causal else np.full((BH, N), N - 1, np.int32)
-    fw = orc.forward(Q, K, V, qi, ki, alpha, scale, k, precision="f64")
+    fw = orc.forward(Q, K, V, qi, ki, alpha, scale, k, block_m=block_m, precision="f64")
     gq, gk, gv = orc.backward(Q, K, V, qi, ki, dO, alpha, scale, fw.taus, fw.csr.q_ptr,
-                              fw.csr.q_list, mode, precision="f64")
+                              fw.csr.q_list, mode, block_m=block_m, precision="f64")
     blocks = [0, 2, 4]
     rows = np.concatenate([np.arange(b * 64, min(b * 64 + 64, N)) for b in blocks])
     for bh in range(BH):
         dK, dV = KB.key_block_grads(Q[bh], K[bh], V[bh], dO[bh], qi[bh], ki[bh], fw.taus[bh],
-                                    fw.mask[bh], alpha, scale, blocks, mode, chunk=96)
+                                    fw.mask[bh], alpha, scale, blocks, mode, chunk=96,
+                                    block_m=block_m)
         np.testing.assert_allclose(dK, gk[bh][rows], rtol=1e-9, atol=1e-12 * np.abs(gk).max())
         np.testing.assert_allclose(dV, gv[bh][rows], rtol=1e-9, atol=1e-12 * np.abs(gv).max())
