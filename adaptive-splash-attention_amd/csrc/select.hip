@@ -380,8 +380,14 @@ __host__ __device__ inline int select_round_bound(int NK, int k, int cap) {
 // staging, no barrier inside a sweep); lane (c, g) sees rows 16 cb + c and
 // keys 16 w + 4 g + r of each tile.  R class maxima per (lane, row, r)
 // give 64 R classes per row.
+// Waves per SIMD the headline variant (bf16, d = 64, two classes per lane)
+// is held to: three blocks of its ~50 KB of LDS fit a CU, and 168 VGPRs
+// let three waves share a SIMD (one more VGPR would drop it to two).
+template <typename T, int D, int R>
+constexpr int select_waves_per_simd() { return sizeof(T) == 2 && D == 64 && R == 2 ? 3 : 1; }
+
 template <typename T, int D, int MODE, int R>
-__global__ __launch_bounds__(kThreads) void select_kernel(SelectParams p) {
+__global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void select_kernel(SelectParams p) {
   constexpr bool kExact = MODE != kRawDots;
   constexpr bool kTiles = MODE != kGivenScores;
   constexpr int UR = R > 2 ? R : 2;  // sweep-1 unroll: class of a tile = ordinal % R
