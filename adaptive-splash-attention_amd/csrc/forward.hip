@@ -8,10 +8,13 @@
 // stream through double-buffered LDS (asa_stage.hpp); S^T = K Q^T is formed
 // on MFMA,
 // p = max(u, EPS)^(1/(alpha-1)) with u = (alpha-1) s - tau is applied in
-// registers (clamp, scale and tau folded into one fma and one median,
-// ClippedU), and O^T += V^T P^T runs on MFMA with P^T taken directly from
-// the score accumulators.  Row sums of p are kept per lane and reduced
-// across the four lane groups at the end.
+// registers (clamp, scale and tau folded into one fma and one median whose
+// zero bounds are -0.0, SignedClip, so the sign bit of max(u, 0) is the
+// support-mask bit), and O^T += V^T P^T runs on MFMA with P^T taken
+// directly from the score accumulators.  Row sums of p are kept per lane
+// and reduced across the four lane groups at the end.  With 32-row mask
+// blocks the list is the union of the block's two halves' key blocks, and
+// a wave skips the tiles its half's mask row lacks.
 #include <type_traits>
 
 #include "asa_device.hpp"

@@ -1,32 +1,39 @@
-// Score pass: scores, exact per-row top-k, tau and block mask.
+// Score pass: scores, exact per-row top-k and block mask (tau follows in
+// tau_kernel, from the sorted top-k values this pass writes).
 //
 // Reference: build_mask_kernel + insert_topk + entmax_threshold
 // (adasplashattention.cu:35-217), one thread per query that scans every key
 // and keeps a sorted top-k by insertion.  Here one 256-thread block owns one
-// 64-row query block of one (batch, head); wave w owns rows 16w..16w+15 and
-// forms S^T = K Q^T tiles on MFMA.  The K tiles of the visible key blocks
-// stream through a double-buffered LDS stage shared by the four waves (each
-// thread prefetches its share of the next tile into registers while the
-// current one is multiplied).  The top-k is found in two sweeps over the
+// 64-row query block of one (batch, head).  During the sweeps the waves
+// split the keys, not the rows: wave w loads keys 16w..16w+15 of each
+// visible key tile straight from L2 into MFMA operand registers (KQuarter,
+// two tiles in flight, no LDS stage and no barrier per tile) and scores
+// them against all 64 rows.  The top-k is found in two sweeps over the
 // visible key blocks instead of by insertion:
 //
 //   sweep 1  every score updates one of 64*R running "class maxima" of its
-//            row (one v_max per score).  Distinct classes hold distinct keys,
-//            so if at least k class maxima are >= x, at least k keys score
-//            >= x, and every top-k key scores >= x.  A short bisection per
-//            row finds such an x close to the k-th largest class maximum.
+//            row (one v_med3 per score; class = key offset in the tile x
+//            tile ordinal mod R).  Distinct classes hold distinct keys, so
+//            if at least k class maxima are >= x, at least k keys score
+//            >= x, and every top-k key scores >= x.  The class maxima meet
+//            in LDS and an 8-step bisection per row (wave w: rows
+//            16w..16w+15) finds such an x close to the k-th largest.
 //   sweep 2  the scores are recomputed and every key scoring >= x is
-//            appended, as a 64-bit (score, ~index) key, to the row's list in
-//            LDS (about 1.05-1.15 k keys per row on random data).  If a row
+//            appended, as (index, score bits), to the row's list in LDS
+//            (about 1.05-1.15 k keys per row on random data).  If a row
 //            overflows its list, the k-th best stored key becomes an exact
-//            key threshold and the block sweeps again for those rows; the
-//            threshold rises strictly, so this ends.
+//            key threshold and the block sweeps again for those rows; each
+//            round drops at least cap - k keys, so the rounds are bounded
+//            (select_round_bound) and the status word reports them.
 //   select   each row's candidates are sorted (segmented bitonic sort across
-//            lanes, descending key order = score desc, index asc); the first
-//            k are the reference's top-k, padded with the empty slot
-//            (score -1e6, index -1).
-//   finish   the rows' top-k key blocks are OR-ed into the block's mask
-//            bitmap; one wave runs the tau recurrence, one lane per row.
+//            lanes, descending key order = score desc, index asc) when the
+//            caller asked for top-k indices; otherwise only the values are
+//            sorted and the top-k key set is the candidates above the k-th
+//            value plus its lowest-index ties.  The first k values go to the
+//            workspace for tau_kernel, padded with the empty slot (-1e6).
+//   finish   the rows' top-k key blocks are OR-ed into a bitmap per 32-row
+//            half of the block: the 64-row mask is their union, and with
+//            32-row mask blocks each half's row is written as well.
 //
 // Sweep filters compare raw dot products (scale > 0) against a threshold
 // widened by a relative margin, so that no key whose clamped, scaled score
