@@ -33,7 +33,7 @@ template <typename T, int D> struct alignas(16) FwdSmem {
   int kid[2][kBlock];
 };
 
-template <typename T, int D, int PC, bool EMIT>
+template <typename T, int D, int PC, bool EMIT, bool HALF>
 __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   __shared__ FwdSmem<T, D> sm;
   using St = Stager<T, D>;
@@ -78,7 +78,7 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   // of the block); a tile that row lacks contributes nothing to the wave
   const uint8_t* hrow = nullptr;
   bool hvalid = true;
-  if (p.half) {
+  if constexpr (HALF) {
     const int h = 2 * qb + (w >> 1), nQH = half_blocks(NQ);
     hvalid = h < nQH;  // else every row of the half is past NQ
     hrow = p.half + (size_t(bh) * nQH + (hvalid ? h : 0)) * nKB;
@@ -107,7 +107,8 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   for (int e = e0; e < e1; ++e) {
     const int b = (e - e0) & 1;
     const int kb = ql[e];
-    const bool act = !hrow || (hvalid && hrow[kb] != 0);  // wave-uniform
+    bool act = true;  // wave-uniform
+    if constexpr (HALF) act = hvalid && hrow[kb] != 0;
     f32x4 acc[4];
     if (act) rows_x_frag<D>(acc, sm.K[b], qf, lane);
     // p for every score, then masked: no per-score branches.  v = max(u, 0)
@@ -161,20 +162,23 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   }
 }
 
-template <typename T, int D, bool EMIT>
+template <typename T, int D, bool EMIT, bool HALF>
 hipError_t launch_tde(const ForwardParams& p, hipStream_t s) {
   dim3 grid(p.d.nQB * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
-    case kA15: hipLaunchKernelGGL((forward_kernel<T, D, kE2, EMIT>), grid, dim3(kThreads), 0, s, p); break;
-    case kA20: hipLaunchKernelGGL((forward_kernel<T, D, kE1, EMIT>), grid, dim3(kThreads), 0, s, p); break;
-    case kA125: hipLaunchKernelGGL((forward_kernel<T, D, kE4, EMIT>), grid, dim3(kThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((forward_kernel<T, D, kEGen, EMIT>), grid, dim3(kThreads), 0, s, p); break;
+    case kA15: hipLaunchKernelGGL((forward_kernel<T, D, kE2, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
+    case kA20: hipLaunchKernelGGL((forward_kernel<T, D, kE1, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
+    case kA125: hipLaunchKernelGGL((forward_kernel<T, D, kE4, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL((forward_kernel<T, D, kEGen, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
   }
   return hipGetLastError();
 }
 template <typename T, int D>
 hipError_t launch_td(const ForwardParams& p, hipStream_t s) {
-  return p.sup.mask ? launch_tde<T, D, true>(p, s) : launch_tde<T, D, false>(p, s);
+  // 32-row mask blocks: the per-half tile test is compiled in only there
+  if (p.half)
+    return p.sup.mask ? launch_tde<T, D, true, true>(p, s) : launch_tde<T, D, false, true>(p, s);
+  return p.sup.mask ? launch_tde<T, D, true, false>(p, s) : launch_tde<T, D, false, false>(p, s);
 }
 
 }  // namespace
