@@ -18,18 +18,36 @@ Inputs follow the notebook's conventions: N(0, 1) * ``--input-scale``
 (the notebook used 0.1), causal int32 ``arange`` positions, sm_scale =
 1/sqrt(d).  ``--backward`` times forward + backward instead of the forward.
 
+Beyond the notebook's fields:
+
+* ``--kernel-times`` adds each library kernel's average time over the
+  splash trials (HIP events the library records around its launches);
+* ``--cpu-baseline`` times the dense alpha-entmax on the host CPU as well
+  (all cores, and one thread), with the host's model and core count;
+* ``--rocprof-pmc "COUNTER ..."`` runs the same benchmark under
+  ``rocprofv3 --pmc`` (a child process; this process never touches the GPU
+  then) and prints each library kernel's counter averages per dispatch.
+
     python -m splash_attention.benchmark --config 1x4x2048x64 --config 1x4x4096x64
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import gc
+import glob
 import json
 import math
+import os
+import re
+import subprocess
+import sys
+import tempfile
 import time
 
 import torch
 
+from . import _lib
 from .function import splash_attention
 
 
@@ -95,10 +113,71 @@ def _time(fn, warmup: int, trials: int) -> tuple[float, float]:
     return times[len(times) // 2], peak
 
 
+def host_cpu() -> dict:
+    """Model name, physical cores and logical CPUs of the host."""
+    model, cores, phys, core = "unknown", set(), None, None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                k, _, v = ln.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+    except OSError:
+        pass
+    return {"model": model, "physical_cores": len(cores) or None, "logical_cpus": os.cpu_count()}
+
+
+def _time_cpu(fn, warmup: int, trials: int) -> float:
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(trials):
+        t0 = time.perf_counter()
+        fn()
+        times.append((time.perf_counter() - t0) * 1e3)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def cpu_baseline(Q, K, V, dO, alpha: float, sm_scale: float, backward: bool, warmup: int,
+                 trials: int) -> dict:
+    """Dense alpha-entmax (dense_entmax_attention) on the host CPU: median ms
+    with every core, and with one thread (one warm-up, three trials)."""
+    q, k, v, g = (t.detach().float().cpu() for t in (Q, K, V, dO))
+
+    def step():
+        if backward:
+            qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+            dense_entmax_attention(qq, kk, vv, alpha, sm_scale).backward(g)
+        else:
+            with torch.no_grad():
+                dense_entmax_attention(q, k, v, alpha, sm_scale)
+
+    prev = torch.get_num_threads()
+    try:
+        torch.set_num_threads(os.cpu_count() or 1)
+        t_all = _time_cpu(step, warmup, trials)
+        torch.set_num_threads(1)
+        t_one = _time_cpu(step, 1, 3)
+    finally:
+        torch.set_num_threads(prev)
+    return {"cpu_time": round(t_all, 3), "cpu_threads": os.cpu_count(),
+            "cpu_time_1thread": round(t_one, 3), "cpu_host": host_cpu()}
+
+
 def run_config(B: int, H: int, N: int, d: int, alpha: float = 1.5, k_keep: int = 8,
                dtype: torch.dtype = torch.float32, baseline: str = "entmax",
                backward: bool = False, input_scale: float = 0.1, warmup: int = 3,
-               trials: int = 10, seed: int = 42, tau_mode: str = "reference") -> dict:
+               trials: int = 10, seed: int = 42, tau_mode: str = "reference",
+               kernel_times: bool = False, with_cpu: bool = False) -> dict:
     """Benchmark one [B, H, N, d] configuration; returns the notebook's fields.
     tau_mode="exact" makes splash attention compute dense alpha-entmax, so
     against the "entmax" baseline the error fields measure parity."""
@@ -131,6 +210,22 @@ def run_config(B: int, H: int, N: int, d: int, alpha: float = 1.5, k_keep: int =
     mse = float(torch.mean((a - b) ** 2))
     max_err = float((a - b).abs().max())
     cos = float(torch.nn.functional.cosine_similarity(a, b, dim=0))
+    extra = {}
+    if kernel_times:
+        # a second pass of the splash step with the library's launch events
+        step = make(sp)
+        torch.cuda.synchronize()
+        _lib.profile_enable(True)
+        try:
+            for _ in range(trials):
+                step()
+            torch.cuda.synchronize()
+            prof = _lib.profile_read()
+        finally:
+            _lib.profile_enable(False)
+        extra["kernel_us"] = {name: round(ms / cnt * 1e3, 2) for name, (cnt, ms) in prof.items()}
+    if with_cpu:
+        extra.update(cpu_baseline(Q, K, V, dO, alpha, sm_scale, backward, warmup, trials))
     return {
         "config_name": f"{B}x{H}x{N}x{d}", "B": B, "H": H, "NQ": N, "NK": N, "d": d,
         "alpha": alpha, "k_keep": k_keep, "dtype": str(dtype).replace("torch.", ""),
@@ -140,6 +235,7 @@ def run_config(B: int, H: int, N: int, d: int, alpha: float = 1.5, k_keep: int =
         "mse_error": mse, "max_error": max_err, "cosine_similarity": cos,
         "vanilla_memory": round(m_dense, 2), "splash_memory": round(m_splash, 2),
         "memory_saving": round(m_dense / m_splash, 3) if m_splash > 0 else None,
+        **extra,
     }
 
 
@@ -170,17 +266,90 @@ def build_parser() -> argparse.ArgumentParser:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--trials", type=int, default=10)
     ap.add_argument("--json", action="store_true", help="one JSON object per line")
+    ap.add_argument("--kernel-times", action="store_true",
+                    help="add each library kernel's average time (library launch events)")
+    ap.add_argument("--cpu-baseline", action="store_true",
+                    help="also time the dense alpha-entmax on the host CPU")
+    ap.add_argument("--rocprof-pmc", metavar="COUNTERS",
+                    help="run under rocprofv3 --pmc COUNTERS (space separated; one hardware "
+                         "pass, e.g. 'SQ_INSTS_VALU SQ_INSTS_MFMA') and print per-kernel averages")
+    ap.add_argument("--rocprof-dir", help="output directory of --rocprof-pmc (default: a "
+                                          "temporary directory)")
     return ap
 
 
+def rocprof_command(argv: list[str], counters: str, outdir: str) -> list[str]:
+    """The child command of --rocprof-pmc: rocprofv3 with the counters around
+    this benchmark, run by the Python interpreter itself (the program must
+    follow "--" directly) with the rocprof options removed."""
+    rest, skip = [], False
+    for a in argv:
+        if skip:
+            skip = False
+            continue
+        if a in ("--rocprof-pmc", "--rocprof-dir"):
+            skip = True
+            continue
+        if a.startswith("--rocprof-pmc=") or a.startswith("--rocprof-dir="):
+            continue
+        rest.append(a)
+    return ["rocprofv3", "--pmc", *counters.split(), "--output-format", "csv", "-d", outdir,
+            "-o", "run", "--", sys.executable, "-m", "splash_attention.benchmark", *rest]
+
+
+def pmc_summary(outdir: str) -> dict[str, dict[str, float]]:
+    """Per-dispatch counter averages of the library's kernels from a
+    rocprofv3 counter-collection CSV: {kernel: {counter: mean}}."""
+    acc: dict[str, dict[str, list[float]]] = {}
+    for f in glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True):
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                m = re.search(r"asa::[^:]*::(\w+_kernel)", row.get("Kernel_Name", ""))
+                if not m:
+                    continue
+                acc.setdefault(m.group(1), {}).setdefault(row["Counter_Name"], []).append(
+                    float(row["Counter_Value"]))
+    return {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in acc.items()}
+
+
+def run_under_rocprof(argv: list[str], counters: str, outdir: str | None) -> int:
+    """Runs the benchmark under rocprofv3 as a child process (this process
+    does not initialise the GPU) and prints the counter summary."""
+    out = outdir or tempfile.mkdtemp(prefix="asa_pmc_")
+    cmd = rocprof_command(argv, counters, out)
+    print("running:", " ".join(cmd), flush=True)
+    rc = subprocess.run(cmd).returncode
+    summary = pmc_summary(out)
+    if not summary:
+        print(f"no counter records of the library's kernels under {out} (rocprofv3 exit {rc})",
+              flush=True)
+        return rc or 1
+    for kern, cs in sorted(summary.items()):
+        print(f"{kern:>22}: " + "  ".join(f"{c} {v:.4g}" for c, v in sorted(cs.items())),
+              flush=True)
+    print(json.dumps({"rocprof_pmc": summary, "dir": out}), flush=True)
+    if rc:
+        # rocprofv3 can exit non-zero while finalising after the program has
+        # ended and its records are complete; the records are used
+        print(f"note: rocprofv3 exited with {rc} after writing its records", flush=True)
+    return 0
+
+
 def main(argv=None) -> list[dict]:
-    args = build_parser().parse_args(argv)
+    raw = list(sys.argv[1:] if argv is None else argv)
+    args = build_parser().parse_args(raw)
+    if args.rocprof_pmc:
+        rc = run_under_rocprof(raw, args.rocprof_pmc, args.rocprof_dir)
+        if rc:
+            raise SystemExit(rc)
+        return []
     configs = args.config or [(1, 4, 1024, 64), (1, 4, 2048, 64), (1, 4, 4096, 64)]
     dtype = {"fp32": torch.float32, "bf16": torch.bfloat16}[args.dtype]
     results = []
     for B, H, N, d in configs:
         r = run_config(B, H, N, d, args.alpha, args.k_keep, dtype, args.baseline, args.backward,
-                       args.input_scale, args.warmup, args.trials, tau_mode=args.tau_mode)
+                       args.input_scale, args.warmup, args.trials, tau_mode=args.tau_mode,
+                       kernel_times=args.kernel_times, with_cpu=args.cpu_baseline)
         results.append(r)
         if args.json:
             print(json.dumps(r), flush=True)
@@ -190,6 +359,12 @@ def main(argv=None) -> list[dict]:
                   f"(x{r['speedup']:.1f})  mse {r['mse_error']:.2e}  max {r['max_error']:.2e}  "
                   f"cos {r['cosine_similarity']:.6f}  mem {r['vanilla_memory']:.0f} / "
                   f"{r['splash_memory']:.0f} MB", flush=True)
+            if "kernel_us" in r:
+                print("    kernels (us): " + ", ".join(f"{k} {v}" for k, v in r["kernel_us"].items()),
+                      flush=True)
+            if "cpu_time" in r:
+                print(f"    dense CPU: {r['cpu_time']:.2f} ms on {r['cpu_threads']} threads, "
+                      f"{r['cpu_time_1thread']:.2f} ms on 1 ({r['cpu_host']['model']})", flush=True)
     return results
 
 

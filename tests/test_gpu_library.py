@@ -77,3 +77,47 @@ def test_benchmark_cli_exact_mode_matches_dense_entmax(dev):
                              input_scale=1.0, warmup=1, trials=2, tau_mode="exact")
     assert r["tau_mode"] == "exact"
     assert r["max_error"] <= 1e-5 and r["cosine_similarity"] > 1 - 1e-9, r
+
+
+def test_benchmark_cli_kernel_times_and_cpu_baseline(dev):
+    """--kernel-times lists the library's kernels with positive times;
+    --cpu-baseline times the dense alpha-entmax on the host (all cores and
+    one thread) and records the host."""
+    from splash_attention import benchmark
+
+    print("[lib] benchmark cli kernel times + cpu baseline", flush=True)
+    r = benchmark.run_config(1, 2, 128, 64, 1.5, 8, torch.float32, "entmax", True,
+                             input_scale=1.0, warmup=1, trials=2, kernel_times=True,
+                             with_cpu=True)
+    ks = r["kernel_us"]
+    for name in ("select", "tau", "forward", "bwd_dq_sparse", "bwd_dkdv_sparse"):
+        assert ks[name] > 0, ks
+    assert r["cpu_time"] > 0 and r["cpu_time_1thread"] > 0
+    assert r["cpu_threads"] >= 1 and "model" in r["cpu_host"]
+
+
+def test_benchmark_cli_rocprof_pmc(dev, tmp_path):
+    """--rocprof-pmc runs the benchmark under rocprofv3 in a child process
+    and summarises the library kernels' counters (one SQ counter: one
+    hardware pass)."""
+    import json
+    import shutil
+    import subprocess
+    import sys
+
+    if shutil.which("rocprofv3") is None:
+        pytest.skip("rocprofv3 not installed")
+    print("[lib] benchmark cli rocprof pmc SQ_WAVES", flush=True)
+    out = subprocess.run(
+        [sys.executable, "-m", "splash_attention.benchmark", "--config", "1x1x128x64",
+         "--warmup", "1", "--trials", "1", "--rocprof-pmc", "SQ_WAVES",
+         "--rocprof-dir", str(tmp_path)],
+        capture_output=True, text=True, timeout=240, cwd=str(tmp_path),
+        env={**__import__("os").environ,
+             "PYTHONPATH": __import__("os").pathsep.join(sys.path)})
+    assert out.returncode == 0, out.stdout[-2000:] + out.stderr[-2000:]
+    line = [ln for ln in out.stdout.splitlines() if ln.startswith('{"rocprof_pmc"')][-1]
+    s = json.loads(line)["rocprof_pmc"]
+    # one 128-row block per (batch, head): 4 waves per select launch
+    assert s["select_kernel"]["SQ_WAVES"] >= 4, s
+    assert "forward_kernel" in s

@@ -51,3 +51,37 @@ def test_benchmark_cli_parsing():
     assert args.config == [(2, 2, 256, 64)] and args.baseline == "vanilla" and args.backward
     assert args.tau_mode == "reference"
     assert benchmark.build_parser().parse_args(["--tau-mode", "exact"]).tau_mode == "exact"
+
+
+def test_benchmark_cli_rocprof_command_and_summary(tmp_path):
+    """--rocprof-pmc: the child command puts the interpreter right after
+    "--" (rocprofv3 must start the program itself) and drops the rocprof
+    options; the summary averages each library kernel's counters over its
+    dispatches and ignores other kernels."""
+    import sys
+
+    from splash_attention import benchmark
+
+    argv = ["--config", "1x2x256x64", "--rocprof-pmc", "SQ_WAVES SQ_INSTS_VALU",
+            "--rocprof-dir=/x", "--backward"]
+    cmd = benchmark.rocprof_command(argv, "SQ_WAVES SQ_INSTS_VALU", "/out")
+    assert cmd[:4] == ["rocprofv3", "--pmc", "SQ_WAVES", "SQ_INSTS_VALU"]
+    i = cmd.index("--")
+    assert cmd[i + 1:i + 4] == [sys.executable, "-m", "splash_attention.benchmark"]
+    assert cmd[i + 4:] == ["--config", "1x2x256x64", "--backward"]
+    assert cmd[cmd.index("-d") + 1] == "/out"
+    (tmp_path / "host" / "1").mkdir(parents=True)
+    rows = [
+        ("void asa::(anonymous namespace)::select_kernel<unsigned short, 64, 0, 2>(asa::SelectParams)",
+         "SQ_WAVES", 16384.0),
+        ("void asa::(anonymous namespace)::select_kernel<unsigned short, 64, 0, 2>(asa::SelectParams)",
+         "SQ_WAVES", 8192.0),
+        ("void asa::(anonymous namespace)::tau_kernel(asa::SelectParams)", "SQ_WAVES", 64.0),
+        ("void at::native::elementwise_kernel<128, 4>(int)", "SQ_WAVES", 7.0),
+    ]
+    with open(tmp_path / "host" / "1" / "run_counter_collection.csv", "w") as f:
+        f.write('"Dispatch_Id","Kernel_Name","Counter_Name","Counter_Value"\n')
+        for n, (k, c, v) in enumerate(rows):
+            f.write(f'{n},"{k}","{c}",{v}\n')
+    s = benchmark.pmc_summary(str(tmp_path))
+    assert s == {"select_kernel": {"SQ_WAVES": 12288.0}, "tau_kernel": {"SQ_WAVES": 64.0}}
