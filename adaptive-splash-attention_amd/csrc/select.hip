@@ -353,7 +353,7 @@ constexpr int kScrStride = 16;
 __host__ __device__ inline SelLayout sel_layout(int k, int cap, int nKB) {
   SelLayout l;
   const int R = classes_per_lane(k);
-  l.scm = 64 * R;  // floats per row of the class-maxima exchange
+  l.scm = 64 * R + 4;  // floats per row of the class-maxima exchange (+4: rows 4 banks apart)
   const int cand_bytes = kBlock * cap * 8;
   const int cm_bytes = kBlock * l.scm * 4;
   const int scr_bytes = kThreads * kScrStride * 4;
@@ -412,6 +412,10 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
   uint32_t* s_ctl = reinterpret_cast<uint32_t*>(smem + lay.ctl);
   uint32_t* s_bits = reinterpret_cast<uint32_t*>(smem + lay.bits);
   int32_t* s_vlist = reinterpret_cast<int32_t*>(smem + lay.vlist);
+  // Slot of candidate e of row r: rows XOR-ed with bits 3-5 of e (moved to
+  // row bits 1-3), so that the 8 lanes reading entries e = 8i + pp of one
+  // row, and the lanes of two adjacent rows, fall in 16 distinct 8-byte banks.
+  auto cslot = [](int e, int r) { return e * kBlock + (r ^ (((e >> 3) & 7) << 1)); };
 
   const int t = threadIdx.x, w = t >> 6, L = t & 63, g = L >> 4, c = L & 15;
   float* s_scr = reinterpret_cast<float*>(smem + lay.scr) + t * kScrStride;  // this lane's
@@ -662,7 +666,7 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
         }
         const uint32_t pos = atomicAdd(&s_cnt[row], 1u);
         if (pos < uint32_t(cap))
-          s_cand[pos * kBlock + row] = (uint64_t(uint32_t(key)) << 32) | __float_as_uint(v);
+          s_cand[cslot(pos, row)] = (uint64_t(uint32_t(key)) << 32) | __float_as_uint(v);
       }
     };
     if (round == 0)
@@ -695,7 +699,7 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
       uint64_t v[8];
       for (int pp = 0; pp < 8; ++pp) {
         const int e = (L & 31) * 8 + pp;
-        v[pp] = e < cap ? raw_key(s_cand[e * kBlock + r]) : 0ull;
+        v[pp] = e < cap ? raw_key(s_cand[cslot(e, r)]) : 0ull;
       }
       segment_sort_desc<32>(v, L);
       // element k-1 lives in lane (k-1)/8, slot (k-1)%8 (both halves agree)
@@ -753,7 +757,7 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
     uint64_t v[8];
     for (int pp = 0; pp < 8; ++pp) {
       const int e = i * 8 + pp;
-      v[pp] = e < n ? raw_key(s_cand[e * kBlock + r]) : 0ull;
+      v[pp] = e < n ? raw_key(s_cand[cslot(e, r)]) : 0ull;
     }
     segment_sort_desc<LS>(v, L);
     for (int pp = 0; pp < 8; ++pp) emit(r, i * 8 + pp, v[pp]);
@@ -774,7 +778,7 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
     uint32_t v[8];
     for (int pp = 0; pp < 8; ++pp) {
       const int e = i * 8 + pp;
-      v[pp] = e < n ? ord_raw(s_cand[e * kBlock + r]) : 0u;  // 0: empty slot
+      v[pp] = e < n ? ord_raw(s_cand[cslot(e, r)]) : 0u;  // 0: empty slot
     }
     segment_sort_desc32<LS>(v, L);
     for (int pp = 0; pp < 8; ++pp) {
@@ -803,14 +807,14 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
     for (int pp = 0; pp < 8; ++pp) {
       const int e = i * 8 + pp;
       if (e >= n) continue;
-      const uint64_t raw = s_cand[e * kBlock + r];
+      const uint64_t raw = s_cand[cslot(e, r)];
       const uint32_t o = ord_raw(raw);
       const int idx = int(raw >> 32);
       bool sel = vk == 0u || o > vk || (o == vk && !split);
       if (split && o == vk) {
         int before = 0;  // ties with a lower index
         for (int f = 0; f < n; ++f) {
-          const uint64_t q = s_cand[f * kBlock + r];
+          const uint64_t q = s_cand[cslot(f, r)];
           before += (ord_raw(q) == vk && int(q >> 32) < idx) ? 1 : 0;
         }
         sel = before < need;
