@@ -19,8 +19,12 @@ namespace asa {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint16_t u16;
+typedef uint16_t u16;  // bf16 storage (raw bits)
+typedef _Float16 h16;  // fp16 storage
 
 constexpr int kWave = 64;
 constexpr int kBlock = 64;          // query rows per block == key columns per block
@@ -29,6 +33,9 @@ constexpr float kSentinel = -1e6f;  // empty top-k slot score (adasplashattentio
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -45,6 +52,10 @@ __device__ __forceinline__ int lane_rank(uint64_t m) {
 __device__ __forceinline__ bf16x2 opaque_bf16x2(uint32_t bits) {
   asm("" : "+s"(bits));
   return __builtin_bit_cast(bf16x2, bits);
+}
+template <typename V2> __device__ __forceinline__ V2 opaque_pair(uint32_t bits) {
+  asm("" : "+s"(bits));
+  return __builtin_bit_cast(V2, bits);
 }
 
 __device__ __forceinline__ float bf16_to_f32(u16 h) {
@@ -68,6 +79,37 @@ template <> struct Elem<u16> {
   static __device__ __forceinline__ float load(const u16* p) { return bf16_to_f32(*p); }
   static __device__ __forceinline__ void store(u16* p, float v) { *p = f32_to_bf16(v); }
 };
+template <> struct Elem<h16> {
+  static __device__ __forceinline__ float load(const h16* p) { return static_cast<float>(*p); }
+  static __device__ __forceinline__ void store(h16* p, float v) { *p = static_cast<h16>(v); }
+};
+
+// The two 16-bit storage formats (bf16 as raw bits, fp16): MFMA operand
+// vectors, float -> format rounding (nearest even), and the packed-pair dot
+// product with fp32 accumulation (v_dot2_f32_bf16 / v_dot2_f32_f16).
+template <typename T> struct Half;
+template <> struct Half<u16> {
+  using v8 = bf16x8;
+  using v4 = bf16x4;
+  using v2 = bf16x2;
+  using scalar = __bf16;
+  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+  }
+  // bits of the packed pairs (-1, 0) and (0, -1)
+  static constexpr uint32_t kNegLoBits = 0x0000bf80u, kNegHiBits = 0xbf800000u;
+};
+template <> struct Half<h16> {
+  using v8 = f16x8;
+  using v4 = f16x4;
+  using v2 = f16x2;
+  using scalar = _Float16;
+  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) {
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+  }
+  static constexpr uint32_t kNegLoBits = 0x0000bc00u, kNegHiBits = 0xbc000000u;
+};
+template <typename T> constexpr bool is_half = sizeof(T) == 2;
 
 // ---------------------------------------------------------------------------
 // Powers.  x^e for x > 0 with the exponent known at compile time by class:
@@ -234,11 +276,12 @@ __device__ __forceinline__ int xcd_task(int i, int total) {
 // supplies the address of 4 consecutive bf16 values; lane i receives value
 // i % 4 of the rows supplied by lanes 4m + i / 4, m = 0..3.
 typedef short short4_lds __attribute__((vector_size(8)));
-__device__ __forceinline__ bf16x4 read_tr16(const u16* p) {
+template <typename T>
+__device__ __forceinline__ typename Half<T>::v4 read_tr16(const T* p) {
   typedef __attribute__((address_space(3))) short4_lds lds_v4;
   const short4_lds v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_v4*)((__attribute__((address_space(3))) u16*)(p)));
-  return __builtin_bit_cast(bf16x4, v);
+      (lds_v4*)((__attribute__((address_space(3))) T*)(p)));
+  return __builtin_bit_cast(typename Half<T>::v4, v);
 }
 
 // ---------------------------------------------------------------------------

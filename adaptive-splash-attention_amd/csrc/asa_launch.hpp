@@ -6,6 +6,10 @@
 
 namespace asa {
 
+// Storage type of Q, K, V, Out, dOut and the gradients (values as asa_dtype).
+enum ElemType : int { kElemF32 = 0, kElemBF16 = 1, kElemF16 = 2 };
+inline int elem_bytes(int dtype) { return dtype == kElemF32 ? 4 : 2; }
+
 // Problem constants shared by every kernel.
 struct Dims {
   int BH, NQ, NK, D, k, nQB, nKB;
@@ -79,6 +83,7 @@ struct ForwardParams {
   float* norms;
   const int2* kbounds;  // (min, max) position per key block [BH * nKB], from the score pass
   const uint8_t* half;  // 32-row mask (32-row blocks only, else nullptr)
+  const float* top1;    // each row's best score (the score pass's first sorted value)
   // Support masks (optional: sup.mask == nullptr writes none).
   SupportMasks sup;
 };
@@ -120,35 +125,35 @@ struct BackwardParams {
 
 // Each launcher returns the launch status; `name` receives the kernel's
 // name for the profiler.
-hipError_t launch_select(const SelectParams& p, bool bf16, bool from_scores, hipStream_t s);
+hipError_t launch_select(const SelectParams& p, int dtype, bool from_scores, hipStream_t s);
 // LDS bytes of one select block holding `cap` candidate keys per row.
-size_t select_lds_bytes(const Dims& d, bool bf16, bool from_scores, int cap);
+size_t select_lds_bytes(const Dims& d, int dtype, bool from_scores, int cap);
 // Candidate keys per row that fit `max_lds` bytes (k + 32 at most; -1 if
 // not even k + 8 fit).
-int select_capacity(const Dims& d, bool bf16, bool from_scores, size_t max_lds);
+int select_capacity(const Dims& d, int dtype, bool from_scores, size_t max_lds);
 hipError_t launch_bounds(const SelectParams& p, hipStream_t s);
 hipError_t launch_tau(const SelectParams& p, hipStream_t s);
 // Exact-threshold pass (tau mode "exact"): after launch_tau, before
 // compaction; reads tkv and kbounds, rewrites taus and ORs blocks into mask.
-hipError_t launch_refine(const SelectParams& p, bool bf16, hipStream_t s);
+hipError_t launch_refine(const SelectParams& p, int dtype, hipStream_t s);
 // LDS bytes of one refine block holding `lcap` listed keys per row.
-size_t refine_lds_bytes(const Dims& d, bool bf16, int lcap);
+size_t refine_lds_bytes(const Dims& d, int dtype, int lcap);
 // Listed keys per row that fit `max_lds` bytes (max(64, k + 32) at most;
 // 0: none fit, every row sweeps; -1: not even the sweep stage fits).
-int refine_list_capacity(const Dims& d, bool bf16, size_t max_lds);
+int refine_list_capacity(const Dims& d, int dtype, size_t max_lds);
 hipError_t launch_compact(const CompactParams& p, hipStream_t s);
 // 64-row mask from a 32-row one: mask[bh, qb, kb] = half[bh, 2 qb, kb] |
 // half[bh, 2 qb + 1, kb] (the second row when it exists).
 hipError_t launch_fold_halves(const uint8_t* half, uint8_t* mask, int BH, int NQ, int nQB,
                               int nKB, hipStream_t s);
-hipError_t launch_forward(const ForwardParams& p, bool bf16, hipStream_t s);
-hipError_t launch_bwd_delta(const BackwardParams& p, bool bf16, hipStream_t s);
-hipError_t launch_bwd_dq(const BackwardParams& p, bool bf16, hipStream_t s);
-hipError_t launch_bwd_dkdv(const BackwardParams& p, bool bf16, hipStream_t s);
+hipError_t launch_forward(const ForwardParams& p, int dtype, hipStream_t s);
+hipError_t launch_bwd_delta(const BackwardParams& p, int dtype, hipStream_t s);
+hipError_t launch_bwd_dq(const BackwardParams& p, int dtype, hipStream_t s);
+hipError_t launch_bwd_dkdv(const BackwardParams& p, int dtype, hipStream_t s);
 // The support-pair passes: dQ writes the row records and the position map
 // that dK/dV reads, so dK/dV must follow it on the stream.
-hipError_t launch_bwd_dq_sparse(const BackwardParams& p, bool bf16, hipStream_t s);
-hipError_t launch_bwd_dkdv_sparse(const BackwardParams& p, bool bf16, hipStream_t s);
+hipError_t launch_bwd_dq_sparse(const BackwardParams& p, int dtype, hipStream_t s);
+hipError_t launch_bwd_dkdv_sparse(const BackwardParams& p, int dtype, hipStream_t s);
 
 // Kernel-timing hooks implemented in capi.cpp (no-ops unless profiling).
 void profile_begin(const char* name, hipStream_t s);

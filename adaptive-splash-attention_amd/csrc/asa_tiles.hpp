@@ -18,6 +18,8 @@
 //                 soon as it is formed.
 #pragma once
 
+#include <type_traits>
+
 #include "asa_device.hpp"
 
 namespace asa {
@@ -38,6 +40,7 @@ template <int D> struct Tile<u16, D> {
   static constexpr int kRs = D + 8;  // row stride (elements)
   __host__ __device__ static constexpr int sw(int row) { return 8 * (((row >> 2) ^ (row >> 3)) & 1); }
 };
+template <int D> struct Tile<h16, D> : Tile<u16, D> {};  // fp16: the bf16 layout
 template <int D> struct Tile<float, D> {
   static constexpr int kRs = D + 4;
   __host__ __device__ static constexpr int sw(int) { return 0; }
@@ -46,14 +49,18 @@ template <int D> struct Tile<float, D> {
 // B-operand fragment of one row per lane (lane column c16 <- `row`),
 // covering the whole head dimension.
 template <typename T, int D> struct RowFrag;
-template <int D> struct RowFrag<u16, D> {
-  bf16x8 v[D / 32];
-  __device__ void load(const u16* row, bool ok, int lane) {
+// 16-bit formats (bf16, fp16)
+template <typename T, int D> struct RowFrag16 {
+  using V8 = typename Half<T>::v8;
+  V8 v[D / 32];
+  __device__ void load(const T* row, bool ok, int lane) {
     const int g = lane >> 4;
     for (int s = 0; s < D / 32; ++s)
-      v[s] = ok ? *reinterpret_cast<const bf16x8*>(row + 32 * s + 8 * g) : bf16x8{};
+      v[s] = ok ? *reinterpret_cast<const V8*>(row + 32 * s + 8 * g) : V8{};
   }
 };
+template <int D> struct RowFrag<u16, D> : RowFrag16<u16, D> {};
+template <int D> struct RowFrag<h16, D> : RowFrag16<h16, D> {};
 template <int D> struct RowFrag<float, D> {
   f32x4 v[D / 16];
   __device__ void load(const float* row, bool ok, int lane) {
@@ -65,17 +72,18 @@ template <int D> struct RowFrag<float, D> {
 
 // [F0, F1) restricts the product to row blocks f = F0..F1-1 (16 rows each);
 // the other entries of acc are left alone.
-template <int D, int F0 = 0, int F1 = 4>
-__device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const u16* rm,
-                                            const RowFrag<u16, D>& b, int lane) {
+template <int D, int F0 = 0, int F1 = 4, typename T,
+          typename std::enable_if<is_half<T>, int>::type = 0>
+__device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const T* rm,
+                                            const RowFrag<T, D>& b, int lane) {
+  using V8 = typename Half<T>::v8;
   const int g = lane >> 4, c = lane & 15;
   // row 16f + c, chunk 4s + g (swizzled by row bits 2-3, i.e. by c)
-  const u16* base = rm + c * Tile<u16, D>::kRs + ((8 * g) ^ Tile<u16, D>::sw(c));
+  const T* base = rm + c * Tile<T, D>::kRs + ((8 * g) ^ Tile<T, D>::sw(c));
   for (int f = F0; f < F1; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < D / 32; ++s)
     for (int f = F0; f < F1; ++f) {
-      const bf16x8 a =
-          *reinterpret_cast<const bf16x8*>(base + 16 * f * Tile<u16, D>::kRs + 32 * s);
+      const V8 a = *reinterpret_cast<const V8*>(base + 16 * f * Tile<T, D>::kRs + 32 * s);
       acc[f] = mfma(a, b.v[s], acc[f]);
     }
 }
@@ -97,16 +105,17 @@ __device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const float* rm,
 // zero.  The same operands in the same MFMA order as the LDS versions above
 // (the LDS tile holds the same values; its swizzle only moves them), so the
 // results are bit-identical.
-template <int D>
-__device__ __forceinline__ void rows_x_frag_global(f32x4 (&acc)[4], const u16* rows, int nrows,
-                                                   const RowFrag<u16, D>& b, int lane) {
+template <int D, typename T, typename std::enable_if<is_half<T>, int>::type = 0>
+__device__ __forceinline__ void rows_x_frag_global(f32x4 (&acc)[4], const T* rows, int nrows,
+                                                   const RowFrag<T, D>& b, int lane) {
+  using V8 = typename Half<T>::v8;
   const int g = lane >> 4, c = lane & 15;
-  bf16x8 a[D / 32][4];
+  V8 a[D / 32][4];
   for (int s = 0; s < D / 32; ++s)
     for (int f = 0; f < 4; ++f)
       a[s][f] = 16 * f + c < nrows
-                    ? *reinterpret_cast<const bf16x8*>(rows + (16 * f + c) * D + 32 * s + 8 * g)
-                    : bf16x8{};
+                    ? *reinterpret_cast<const V8*>(rows + (16 * f + c) * D + 32 * s + 8 * g)
+                    : V8{};
   for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < D / 32; ++s)
     for (int f = 0; f < 4; ++f) acc[f] = mfma(a[s][f], b.v[s], acc[f]);
@@ -131,22 +140,25 @@ __device__ __forceinline__ void rows_x_frag_global(f32x4 (&acc)[4], const float*
 // by several B fragments (bf16: held in registers; fp32: re-read per
 // product, since D = 128 would take 128 registers).
 template <typename T, int D> struct KFrags;
-template <int D> struct KFrags<u16, D> {
-  bf16x8 a[D / 32][4];
-  __device__ __forceinline__ void load(const u16* rows, int nrows, int lane) {
+template <typename T, int D> struct KFrags16 {
+  using V8 = typename Half<T>::v8;
+  V8 a[D / 32][4];
+  __device__ __forceinline__ void load(const T* rows, int nrows, int lane) {
     const int g = lane >> 4, c = lane & 15;
     for (int s = 0; s < D / 32; ++s)
       for (int f = 0; f < 4; ++f)
         a[s][f] = 16 * f + c < nrows
-                      ? *reinterpret_cast<const bf16x8*>(rows + (16 * f + c) * D + 32 * s + 8 * g)
-                      : bf16x8{};
+                      ? *reinterpret_cast<const V8*>(rows + (16 * f + c) * D + 32 * s + 8 * g)
+                      : V8{};
   }
-  __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<u16, D>& b) const {
+  __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<T, D>& b) const {
     for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < D / 32; ++s)
       for (int f = 0; f < 4; ++f) acc[f] = mfma(a[s][f], b.v[s], acc[f]);
   }
 };
+template <int D> struct KFrags<u16, D> : KFrags16<u16, D> {};
+template <int D> struct KFrags<h16, D> : KFrags16<h16, D> {};
 template <int D> struct KFrags<float, D> {
   const float* rows;
   int nrows, lane;
@@ -160,48 +172,56 @@ template <int D> struct KFrags<float, D> {
   }
 };
 
-// bf16: `rm` is the row-major tile.  The A operand (4 consecutive tile rows
+// bf16 / fp16: `rm` is the row-major tile.  The A operand (4 consecutive tile rows
 // at one column per lane and half) is read with ds_read_b64_tr_b16: in each
 // 16-lane group, lane l reads the 8 bytes at row key0 + l/4, columns
 // col0 + 4 (l % 4) .. +3, and lane c receives rows key0 .. key0 + 3 of
-// column col0 + c.  x is rounded to bf16; with Split, x is carried as the
-// sum of two bf16 terms (hi = bf16(x), lo = bf16(x - hi), 16 significant
+// column col0 + c.  x is rounded to the tile's format; with Split, x is
+// carried as the sum of two such terms (hi = r(x), lo = r(x - hi): 16
+// significant bits with bf16, 22 with fp16 unless lo underflows
 // bits), so that sums with heavy cancellation -- gradient rows whose
 // weights sum to zero against keys that share a common component -- keep
 // fp32-level accuracy at the cost of a second MFMA.
-template <int D, bool Split = false, int CC0 = 0, int CC1 = 2>
-__device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const u16* rm,
+template <int D, bool Split = false, int CC0 = 0, int CC1 = 2, typename T,
+          typename std::enable_if<is_half<T>, int>::type = 0>
+__device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const T* rm,
                                              const f32x4 (&x)[4], int lane) {
+  using H = Half<T>;
+  using V8 = typename H::v8;
+  using V4 = typename H::v4;
+  using V2 = typename H::v2;
+  using S = typename H::scalar;
   const int g = lane >> 4, l = lane & 15;
-  constexpr int rs = Tile<u16, D>::kRs;
+  constexpr int rs = Tile<T, D>::kRs;
   // x - hi is exact in fp32; it is formed from the packed hi pair by
-  // v_dot2c_f32_bf16 (x + hi.lo * -1 + hi.hi * 0), one instruction per value.
-  // The (-1, 0) and (0, -1) pairs are passed in scalar registers: as an
-  // inline constant the compiler encodes (-1, 0) as the float -1.0, whose
-  // bits the instruction reads as the pair (0, -1) (measured on gfx950).
-  const bf16x2 kNegLo = opaque_bf16x2(0x0000bf80u);
-  const bf16x2 kNegHi = opaque_bf16x2(0xbf800000u);
+  // v_dot2c_f32_bf16 / _f16 (x + hi.lo * -1 + hi.hi * 0), one instruction
+  // per value.  The (-1, 0) and (0, -1) pairs are passed in scalar
+  // registers: as an inline constant the compiler encodes (-1, 0) as the
+  // float -1.0, whose bits the instruction reads as the pair (0, -1)
+  // (measured on gfx950).
+  const V2 kNegLo = opaque_pair<V2>(H::kNegLoBits);
+  const V2 kNegHi = opaque_pair<V2>(H::kNegHiBits);
   for (int cc = CC0; cc < CC1; ++cc) {
-    bf16x8 b, bl;
+    V8 b, bl;
     for (int h = 0; h < 2; ++h)
       for (int r = 0; r < 4; r += 2) {
         const float x0 = x[2 * cc + h][r], x1 = x[2 * cc + h][r + 1];
-        const bf16x2 hp = {static_cast<__bf16>(x0), static_cast<__bf16>(x1)};
+        const V2 hp = {static_cast<S>(x0), static_cast<S>(x1)};
         b[4 * h + r] = hp[0];
         b[4 * h + r + 1] = hp[1];
         if (Split) {
-          bl[4 * h + r] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(hp, kNegLo, x0, false));
-          bl[4 * h + r + 1] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(hp, kNegHi, x1, false));
+          bl[4 * h + r] = static_cast<S>(H::dot2(hp, kNegLo, x0));
+          bl[4 * h + r + 1] = static_cast<S>(H::dot2(hp, kNegHi, x1));
         }
       }
     // rows 32cc + 4g + 0..3 (low half) and 32cc + 16 + 4g + 0..3 (high
     // half); the chunk swizzle depends on g only (row bits 2-3)
-    const u16* base = rm + (32 * cc + 4 * g + (l >> 2)) * rs + ((4 * (l & 3)) ^ Tile<u16, D>::sw(4 * g));
-    bf16x8 a[D / 16];
+    const T* base = rm + (32 * cc + 4 * g + (l >> 2)) * rs + ((4 * (l & 3)) ^ Tile<T, D>::sw(4 * g));
+    V8 a[D / 16];
     for (int db = 0; db < D / 16; ++db) {
-      const bf16x4 lo = read_tr16(base + 16 * db);
-      const bf16x4 hi = read_tr16(base + 16 * rs + 16 * db);
-      a[db] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      const V4 lo = read_tr16(base + 16 * db);
+      const V4 hi = read_tr16(base + 16 * rs + 16 * db);
+      a[db] = V8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       o[db] = mfma(a[db], b, o[db]);
     }
     // the lo terms after all hi terms: D/16 independent chains between

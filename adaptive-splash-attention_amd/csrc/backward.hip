@@ -84,6 +84,7 @@ constexpr int dq_waves_per_simd() { return sizeof(T) == 2 && D == 64 ? 3 : 1; }
 
 template <typename T, int D, int AC, bool REF>
 __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kernel(BackwardParams p) {
+  constexpr bool kOpScaled = std::is_same<T, h16>::value;  // see the weights below
   __shared__ DqSmem<T, D> sm;
   using St = Stager<T, D>;
   constexpr int PW = AlphaPow<AC>::W;
@@ -177,8 +178,11 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
           } else {
             sw += wv;
             swdp += wv * dp;
-            sacc[f][r] = wv * dp;
-            dacc[f][r] = wv;
+            // fp16 operands carry c w (c = (sum p + EPS)^(alpha-2) <= 1 per
+            // unit of w's scale): w alone can exceed fp16's range
+            const float wq = kOpScaled ? wv * cfac : wv;
+            sacc[f][r] = wq * dp;
+            dacc[f][r] = wq;
           }
         }
     };
@@ -209,7 +213,7 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
   }
   if (qok) {
     T* out = static_cast<T*>(p.dq) + row * D;
-    const float cs = REF ? scale : scale * cfac;
+    const float cs = (REF || kOpScaled) ? scale : scale * cfac;
     for (int db = 0; db < D / 16; ++db)
       for (int r = 0; r < 4; ++r) {
         const float acc = REF ? a1[db][r] : (a1[db][r] - shift * a2[db][r]);
@@ -445,18 +449,21 @@ hipError_t launch_delta_td(const BackwardParams& p, hipStream_t s) {
 }  // namespace
 
 #define ASA_DISPATCH_TD(fn)                                \
-  if (bf16) {                                              \
+  if (dtype == kElemBF16) {                                \
     if (p.d.D == 64) return fn<u16, 64>(p, s);             \
     if (p.d.D == 128) return fn<u16, 128>(p, s);           \
+  } else if (dtype == kElemF16) {                          \
+    if (p.d.D == 64) return fn<h16, 64>(p, s);             \
+    if (p.d.D == 128) return fn<h16, 128>(p, s);           \
   } else {                                                 \
     if (p.d.D == 64) return fn<float, 64>(p, s);           \
     if (p.d.D == 128) return fn<float, 128>(p, s);         \
   }                                                        \
   return hipErrorInvalidValue;
 
-hipError_t launch_bwd_delta(const BackwardParams& p, bool bf16, hipStream_t s) { ASA_DISPATCH_TD(launch_delta_td) }
-hipError_t launch_bwd_dq(const BackwardParams& p, bool bf16, hipStream_t s) { ASA_DISPATCH_TD(launch_dq_td) }
-hipError_t launch_bwd_dkdv(const BackwardParams& p, bool bf16, hipStream_t s) { ASA_DISPATCH_TD(launch_dkdv_td) }
+hipError_t launch_bwd_delta(const BackwardParams& p, int dtype, hipStream_t s) { ASA_DISPATCH_TD(launch_delta_td) }
+hipError_t launch_bwd_dq(const BackwardParams& p, int dtype, hipStream_t s) { ASA_DISPATCH_TD(launch_dq_td) }
+hipError_t launch_bwd_dkdv(const BackwardParams& p, int dtype, hipStream_t s) { ASA_DISPATCH_TD(launch_dkdv_td) }
 
 #undef ASA_DISPATCH_TD
 

@@ -19,6 +19,10 @@
 #include "../../include/adasplash.h"
 #include "asa_launch.hpp"
 
+static_assert(int(ASA_DTYPE_F32) == asa::kElemF32 && int(ASA_DTYPE_BF16) == asa::kElemBF16 &&
+                  int(ASA_DTYPE_F16) == asa::kElemF16,
+              "asa_dtype and asa::ElemType must agree");
+
 namespace {
 
 thread_local std::string g_error;
@@ -49,7 +53,7 @@ struct Shape {
   int nKB;
   int bm;   // block_m: 64, or 32 (the reference's BLOCK_M)
   int nQBm; // block_m-row query blocks: rows of the state's mask and CSR
-  bool bf16;
+  int dtype;  // asa_dtype (= asa::ElemType)
   bool exact;  // ASA_TAU_EXACT
   float alpha, scale;
 };
@@ -75,7 +79,7 @@ int validate(const asa_problem* p, Shape* sh) {
                 p->block_n);
   if (p->block_m == 32 && p->tau_mode == ASA_TAU_EXACT)
     return fail(ASA_ERR_UNSUPPORTED, "exact tau mode needs block_m = 64");
-  if (p->dtype != ASA_DTYPE_F32 && p->dtype != ASA_DTYPE_BF16)
+  if (p->dtype != ASA_DTYPE_F32 && p->dtype != ASA_DTYPE_BF16 && p->dtype != ASA_DTYPE_F16)
     return fail(ASA_ERR_INVALID_ARGUMENT, "unknown dtype %d", p->dtype);
   if (p->tau_mode != ASA_TAU_REFERENCE && p->tau_mode != ASA_TAU_EXACT)
     return fail(ASA_ERR_INVALID_ARGUMENT, "unknown tau_mode %d", p->tau_mode);
@@ -96,7 +100,7 @@ int validate(const asa_problem* p, Shape* sh) {
   sh->nKB = int(nkb);
   sh->bm = p->block_m;
   sh->nQBm = int(nqbm);
-  sh->bf16 = p->dtype == ASA_DTYPE_BF16;
+  sh->dtype = p->dtype;
   sh->exact = p->tau_mode == ASA_TAU_EXACT;
   // alpha is clamped to [1.05, 3] as the reference does (adasplashattention.cu:547).
   sh->alpha = std::fmax(1.05f, std::fmin(p->alpha, 3.0f));
@@ -217,10 +221,10 @@ int select_cap(const Shape& s, bool from_scores, int* cap) {
                          "hipDeviceGetAttribute"))
     return rc;
   const asa::Dims d = dims_of(s);
-  *cap = asa::select_capacity(d, s.bf16, from_scores, size_t(max_lds));
+  *cap = asa::select_capacity(d, s.dtype, from_scores, size_t(max_lds));
   if (*cap < 0)
     return fail(ASA_ERR_UNSUPPORTED, "k_keep %d needs %zu bytes of LDS per block, device has %d",
-                s.k, asa::select_lds_bytes(d, s.bf16, from_scores, s.k + 8), max_lds);
+                s.k, asa::select_lds_bytes(d, s.dtype, from_scores, s.k + 8), max_lds);
   return ASA_OK;
 }
 
@@ -257,11 +261,11 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
                                                  hipDeviceAttributeMaxSharedMemoryPerBlock, dev),
                            "hipDeviceGetAttribute"))
       return rc;
-    sp.lcap = asa::refine_list_capacity(sp.d, sh.bf16, size_t(max_lds));
+    sp.lcap = asa::refine_list_capacity(sp.d, sh.dtype, size_t(max_lds));
     if (sp.lcap < 0)
       return fail(ASA_ERR_UNSUPPORTED,
                   "exact tau mode needs %zu bytes of LDS per block, device has %d",
-                  asa::refine_lds_bytes(sp.d, sh.bf16, 0), max_lds);
+                  asa::refine_lds_bytes(sp.d, sh.dtype, 0), max_lds);
   }
   sp.q = q;
   sp.k = k;
@@ -279,7 +283,7 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
   asa::profile_end(s);
   if (int rc = check_hip(eb, "bounds kernel launch")) return rc;
   asa::profile_begin(scores ? "select_scores" : "select", s);
-  hipError_t e = asa::launch_select(sp, sh.bf16, scores != nullptr, s);
+  hipError_t e = asa::launch_select(sp, sh.dtype, scores != nullptr, s);
   asa::profile_end(s);
   if (int rc = check_hip(e, "select kernel launch")) return rc;
   asa::profile_begin("tau", s);
@@ -289,7 +293,7 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
   if (sh.exact) {
     // exact threshold over the whole row; adds the support's key blocks
     asa::profile_begin("refine", s);
-    e = asa::launch_refine(sp, sh.bf16, s);
+    e = asa::launch_refine(sp, sh.dtype, s);
     asa::profile_end(s);
     if (int rc = check_hip(e, "refine kernel launch")) return rc;
   }
@@ -386,12 +390,13 @@ int forward_impl(const Shape& sh, const void* q, const void* k, const void* v,
   fp.q_ptr = c64.q_ptr;
   fp.q_list = c64.q_list;
   fp.half = sh.bm == 32 ? st->mask : nullptr;
+  fp.top1 = static_cast<const float*>(workspace);  // slot 0 of the sorted top-k values
   fp.out = out;
   fp.norms = st->norms;
   fp.kbounds = reinterpret_cast<const int2*>(static_cast<const char*>(workspace) + tkv_bytes(sh));
   fp.sup.mask = st->sup_mask;
   asa::profile_begin("forward", s);
-  hipError_t e = asa::launch_forward(fp, sh.bf16, s);
+  hipError_t e = asa::launch_forward(fp, sh.dtype, s);
   asa::profile_end(s);
   if (int rc = check_hip(e, "forward kernel launch")) return rc;
   return ok();
@@ -521,28 +526,28 @@ int asa_backward(const asa_problem* p, int32_t grad_mode, const void* q, const v
   hipError_t e;
   if (grad_mode == ASA_GRAD_REFERENCE) {
     asa::profile_begin("bwd_delta", s);
-    e = asa::launch_bwd_delta(bp, sh.bf16, s);
+    e = asa::launch_bwd_delta(bp, sh.dtype, s);
     asa::profile_end(s);
     if (int rc = check_hip(e, "backward delta kernel launch")) return rc;
   }
   if (bp.sup.mask) {
     // support masks: only the listed (row, key) pairs
     asa::profile_begin("bwd_dq_sparse", s);
-    e = asa::launch_bwd_dq_sparse(bp, sh.bf16, s);
+    e = asa::launch_bwd_dq_sparse(bp, sh.dtype, s);
     asa::profile_end(s);
     if (int rc = check_hip(e, "backward sparse dQ kernel launch")) return rc;
     asa::profile_begin("bwd_dkdv_sparse", s);
-    e = asa::launch_bwd_dkdv_sparse(bp, sh.bf16, s);
+    e = asa::launch_bwd_dkdv_sparse(bp, sh.dtype, s);
     asa::profile_end(s);
     if (int rc = check_hip(e, "backward sparse dK/dV kernel launch")) return rc;
     return ok();
   }
   asa::profile_begin("bwd_dq", s);
-  e = asa::launch_bwd_dq(bp, sh.bf16, s);
+  e = asa::launch_bwd_dq(bp, sh.dtype, s);
   asa::profile_end(s);
   if (int rc = check_hip(e, "backward dQ kernel launch")) return rc;
   asa::profile_begin("bwd_dkdv", s);
-  e = asa::launch_bwd_dkdv(bp, sh.bf16, s);
+  e = asa::launch_bwd_dkdv(bp, sh.dtype, s);
   asa::profile_end(s);
   if (int rc = check_hip(e, "backward dK/dV kernel launch")) return rc;
   return ok();

@@ -480,25 +480,28 @@ hipError_t launch_td(const SelectParams& p, size_t lds, hipStream_t s) {
 
 }  // namespace
 
-size_t refine_lds_bytes(const Dims& d, bool bf16, int lcap) {
-  return size_t(exact_layout(d.nKB, lcap, d.D * (bf16 ? 2 : 4)).total);
+size_t refine_lds_bytes(const Dims& d, int dtype, int lcap) {
+  return size_t(exact_layout(d.nKB, lcap, d.D * elem_bytes(dtype)).total);
 }
 
-int refine_list_capacity(const Dims& d, bool bf16, size_t max_lds) {
+int refine_list_capacity(const Dims& d, int dtype, size_t max_lds) {
   // Per wave and row: the u > 0 keys of random rows at tau_k number at
   // most ~1.7 k at k = 32, a quarter of them per wave on average; (k + 32)
   // / 2 per wave leaves room for uneven splits.  Rows that overflow sweep.
   int lcap = (d.k + 32) / 2 > 32 ? (d.k + 32) / 2 : 32;
-  while (lcap > 0 && refine_lds_bytes(d, bf16, lcap) > max_lds) lcap -= 16;
+  while (lcap > 0 && refine_lds_bytes(d, dtype, lcap) > max_lds) lcap -= 16;
   if (lcap < 0) lcap = 0;
-  return refine_lds_bytes(d, bf16, lcap) <= max_lds ? lcap : -1;
+  return refine_lds_bytes(d, dtype, lcap) <= max_lds ? lcap : -1;
 }
 
-hipError_t launch_refine(const SelectParams& p, bool bf16, hipStream_t s) {
-  const size_t lds = refine_lds_bytes(p.d, bf16, p.lcap);
-  if (bf16) {
+hipError_t launch_refine(const SelectParams& p, int dtype, hipStream_t s) {
+  const size_t lds = refine_lds_bytes(p.d, dtype, p.lcap);
+  if (dtype == kElemBF16) {
     if (p.d.D == 64) return launch_td<u16, 64>(p, lds, s);
     if (p.d.D == 128) return launch_td<u16, 128>(p, lds, s);
+  } else if (dtype == kElemF16) {
+    if (p.d.D == 64) return launch_td<h16, 64>(p, lds, s);
+    if (p.d.D == 128) return launch_td<h16, 128>(p, lds, s);
   } else {
     if (p.d.D == 64) return launch_td<float, 64>(p, lds, s);
     if (p.d.D == 128) return launch_td<float, 128>(p, lds, s);

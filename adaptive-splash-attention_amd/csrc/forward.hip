@@ -56,6 +56,22 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   const float am1 = p.d.alpha - 1.0f;
   const float a = 1.0f / am1;
   const SignedClip clip(am1, p.d.scale, qok ? p.taus[row] : 0.0f, qok);  // invalid rows: p = 0
+  // fp16 P operands: the weights are scaled by 2^-e, e the exponent of the
+  // row's largest weight (that of its best key), so that they fit fp16's
+  // range (rows with fewer visible keys than k carry the -1e6 sentinel
+  // into tau and can have weights far above 65504); the output divides the
+  // scale out again.  bf16 and fp32 have fp32's range and use 1.
+  float pscale = 1.0f;
+  if constexpr (std::is_same<T, h16>::value) {
+    if (qok) {
+      const float s1 = p.top1[row];
+      const float u1 = fmaxf(fminf(fmaf(am1, s1, -p.taus[row]), fmaf(10.0f, am1, -p.taus[row])), 0.0f);
+      const float p1 = pow_clipped<PC>(u1, a);
+      int e = 0;
+      (void)frexpf(p1, &e);
+      pscale = p1 > 0.0f ? (finite(p1) ? ldexpf(1.0f, -e) : 0.0f) : 1.0f;
+    }
+  }
   // smallest position of the block's valid rows: a key block whose largest
   // position (from the score pass's bounds) is at most this, and that lies
   // wholly below NK, is visible to every row of the block
@@ -130,7 +146,8 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
       for (int f = 0; f < 4; ++f)
         for (int r = 0; r < 4; ++r) {
           const float pv = pow_clipped<PC>(acc[f][r], a);
-          acc[f][r] = pv;
+          if constexpr (std::is_same<T, h16>::value) acc[f][r] = pv * pscale;
+          else acc[f][r] = pv;
           rowsum += pv;
         }
     };
@@ -149,7 +166,7 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   }
 
   const float norm = sum_groups(rowsum);
-  const float inv = 1.0f / (norm + kEps);
+  const float inv = 1.0f / ((norm + kEps) * pscale);  // pscale 0: non-finite weights, output 0
   if (qok) {
     T* orow = static_cast<T*>(p.out) + row * D;
     for (int db = 0; db < D / 16; ++db)
@@ -183,10 +200,13 @@ hipError_t launch_td(const ForwardParams& p, hipStream_t s) {
 
 }  // namespace
 
-hipError_t launch_forward(const ForwardParams& p, bool bf16, hipStream_t s) {
-  if (bf16) {
+hipError_t launch_forward(const ForwardParams& p, int dtype, hipStream_t s) {
+  if (dtype == kElemBF16) {
     if (p.d.D == 64) return launch_td<u16, 64>(p, s);
     if (p.d.D == 128) return launch_td<u16, 128>(p, s);
+  } else if (dtype == kElemF16) {
+    if (p.d.D == 64) return launch_td<h16, 64>(p, s);
+    if (p.d.D == 128) return launch_td<h16, 128>(p, s);
   } else {
     if (p.d.D == 64) return launch_td<float, 64>(p, s);
     if (p.d.D == 128) return launch_td<float, 128>(p, s);

@@ -309,21 +309,24 @@ enum SweepMode : int {
 // attention passes' rows_x_frag, so every score is bit-identical to theirs.
 // acc[cb][r] is the score of key 16 w + 4 g + r and row 16 cb + c.
 template <typename T, int D> struct KQuarter;
-template <int D> struct KQuarter<u16, D> {
-  bf16x8 a[D / 32];
+template <typename T, int D> struct KQuarter16 {
+  using V8 = typename Half<T>::v8;
+  V8 a[D / 32];
   // Keys >= NK read key 0 instead: they lie in partially visible tiles,
   // where the visibility test discards their scores, so no zeroing (and no
   // wait for the load where it is issued) is needed.
-  __device__ __forceinline__ void load(const u16* Kb, int key, int NK, int g) {
-    const u16* src = Kb + size_t(key < NK ? key : 0) * D + 8 * g;
-    for (int s = 0; s < D / 32; ++s) a[s] = *reinterpret_cast<const bf16x8*>(src + 32 * s);
+  __device__ __forceinline__ void load(const T* Kb, int key, int NK, int g) {
+    const T* src = Kb + size_t(key < NK ? key : 0) * D + 8 * g;
+    for (int s = 0; s < D / 32; ++s) a[s] = *reinterpret_cast<const V8*>(src + 32 * s);
   }
-  __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<u16, D> (&qf)[4]) const {
+  __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<T, D> (&qf)[4]) const {
     for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < D / 32; ++s)
       for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma(a[s], qf[cb].v[s], acc[cb]);
   }
 };
+template <int D> struct KQuarter<u16, D> : KQuarter16<u16, D> {};
+template <int D> struct KQuarter<h16, D> : KQuarter16<h16, D> {};
 template <int D> struct KQuarter<float, D> {
   f32x4 a[D / 16];
   __device__ __forceinline__ void load(const float* Kb, int key, int NK, int g) {
@@ -986,26 +989,29 @@ hipError_t launch_tau(const SelectParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-size_t select_lds_bytes(const Dims& d, bool bf16, bool from_scores, int cap) {
-  (void)bf16;
+size_t select_lds_bytes(const Dims& d, int dtype, bool from_scores, int cap) {
+  (void)dtype;
   (void)from_scores;
   return size_t(sel_layout(d.k, cap, d.nKB).total);
 }
 
-int select_capacity(const Dims& d, bool bf16, bool from_scores, size_t max_lds) {
+int select_capacity(const Dims& d, int dtype, bool from_scores, size_t max_lds) {
   // k + 32 keys per row holds the candidates of random rows with room to
   // spare; less still works (overflow rounds), as long as it exceeds k.
   int cap = d.k + 32;
   if (cap > 256) cap = 256;
-  while (cap > d.k && select_lds_bytes(d, bf16, from_scores, cap) > max_lds) cap -= 8;
+  while (cap > d.k && select_lds_bytes(d, dtype, from_scores, cap) > max_lds) cap -= 8;
   return cap > d.k ? cap : -1;
 }
 
-hipError_t launch_select(const SelectParams& p, bool bf16, bool from_scores, hipStream_t s) {
+hipError_t launch_select(const SelectParams& p, int dtype, bool from_scores, hipStream_t s) {
   if (from_scores) return launch_r<float, 64, kGivenScores>(p, s);
-  if (bf16) {
+  if (dtype == kElemBF16) {
     if (p.d.D == 64) return launch_mode<u16, 64>(p, s);
     if (p.d.D == 128) return launch_mode<u16, 128>(p, s);
+  } else if (dtype == kElemF16) {
+    if (p.d.D == 64) return launch_mode<h16, 64>(p, s);
+    if (p.d.D == 128) return launch_mode<h16, 128>(p, s);
   } else {
     if (p.d.D == 64) return launch_mode<float, 64>(p, s);
     if (p.d.D == 128) return launch_mode<float, 128>(p, s);

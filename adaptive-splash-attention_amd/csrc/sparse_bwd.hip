@@ -81,6 +81,34 @@ template <> struct Chunk<u16> {
     *reinterpret_cast<uint4*>(p) = uint4{w[0], w[1], w[2], w[3]};
   }
 };
+template <> struct Chunk<h16> {
+  static constexpr int E = 8;
+  static __device__ __forceinline__ uint4 raw(const h16* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ void unpack(const uint4& v, float (&x)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    for (int i = 0; i < 4; ++i) {
+      const f16x2 h = __builtin_bit_cast(f16x2, w[i]);
+      x[2 * i] = static_cast<float>(h[0]);
+      x[2 * i + 1] = static_cast<float>(h[1]);
+    }
+  }
+  static __device__ __forceinline__ void load(const h16* p, float (&x)[8]) { unpack(raw(p), x); }
+  // sum_i a_i b_i of two raw chunks: products exact, fp32 sums (v_dot2_f32_f16)
+  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b) {
+    float s = 0.0f;
+    s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a.x), __builtin_bit_cast(f16x2, b.x), s, false);
+    s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a.y), __builtin_bit_cast(f16x2, b.y), s, false);
+    s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a.z), __builtin_bit_cast(f16x2, b.z), s, false);
+    s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a.w), __builtin_bit_cast(f16x2, b.w), s, false);
+    return s;
+  }
+  static __device__ __forceinline__ void store(h16* p, const float (&x)[8]) {
+    f16x2 h[4];
+    for (int i = 0; i < 4; ++i) h[i] = f16x2{static_cast<h16>(x[2 * i]), static_cast<h16>(x[2 * i + 1])};
+    *reinterpret_cast<uint4*>(p) = uint4{__builtin_bit_cast(uint32_t, h[0]), __builtin_bit_cast(uint32_t, h[1]),
+                                         __builtin_bit_cast(uint32_t, h[2]), __builtin_bit_cast(uint32_t, h[3])};
+  }
+};
 template <> struct Chunk<float> {
   static constexpr int E = 4;
   static __device__ __forceinline__ uint4 raw(const float* p) { return *reinterpret_cast<const uint4*>(p); }
@@ -571,13 +599,18 @@ hipError_t launch_sparse_m(const BackwardParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 template <bool DKDV>
-hipError_t launch_sparse(const BackwardParams& p, bool bf16, hipStream_t s) {
+hipError_t launch_sparse(const BackwardParams& p, int dtype, hipStream_t s) {
   const bool ref = p.mode == 1;
-  if (bf16) {
+  if (dtype == kElemBF16) {
     if (p.d.D == 64)
       return ref ? launch_sparse_m<u16, 64, true, DKDV>(p, s) : launch_sparse_m<u16, 64, false, DKDV>(p, s);
     if (p.d.D == 128)
       return ref ? launch_sparse_m<u16, 128, true, DKDV>(p, s) : launch_sparse_m<u16, 128, false, DKDV>(p, s);
+  } else if (dtype == kElemF16) {
+    if (p.d.D == 64)
+      return ref ? launch_sparse_m<h16, 64, true, DKDV>(p, s) : launch_sparse_m<h16, 64, false, DKDV>(p, s);
+    if (p.d.D == 128)
+      return ref ? launch_sparse_m<h16, 128, true, DKDV>(p, s) : launch_sparse_m<h16, 128, false, DKDV>(p, s);
   } else {
     if (p.d.D == 64)
       return ref ? launch_sparse_m<float, 64, true, DKDV>(p, s) : launch_sparse_m<float, 64, false, DKDV>(p, s);
@@ -589,11 +622,11 @@ hipError_t launch_sparse(const BackwardParams& p, bool bf16, hipStream_t s) {
 
 }  // namespace
 
-hipError_t launch_bwd_dq_sparse(const BackwardParams& p, bool bf16, hipStream_t s) {
-  return launch_sparse<false>(p, bf16, s);
+hipError_t launch_bwd_dq_sparse(const BackwardParams& p, int dtype, hipStream_t s) {
+  return launch_sparse<false>(p, dtype, s);
 }
-hipError_t launch_bwd_dkdv_sparse(const BackwardParams& p, bool bf16, hipStream_t s) {
-  return launch_sparse<true>(p, bf16, s);  // after the dQ pass, which writes the position map
+hipError_t launch_bwd_dkdv_sparse(const BackwardParams& p, int dtype, hipStream_t s) {
+  return launch_sparse<true>(p, dtype, s);  // after the dQ pass, which writes the position map
 }
 
 }  // namespace asa

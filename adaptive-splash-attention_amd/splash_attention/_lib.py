@@ -12,7 +12,7 @@ import threading
 
 from . import _build
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 ASA_OK = 0
 ASA_ERR_INVALID_ARGUMENT = 1
@@ -21,6 +21,7 @@ ASA_ERR_DEVICE = 3
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2
 
 TAU_REFERENCE = 0
 TAU_EXACT = 1

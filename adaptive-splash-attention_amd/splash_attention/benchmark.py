@@ -257,7 +257,7 @@ def build_parser() -> argparse.ArgumentParser:
                     help="BxHxNxd (repeatable); default 1x4x1024x64, 1x4x2048x64, 1x4x4096x64")
     ap.add_argument("--alpha", type=float, default=1.5)
     ap.add_argument("--k-keep", type=int, default=8)
-    ap.add_argument("--dtype", choices=["fp32", "bf16"], default="fp32")
+    ap.add_argument("--dtype", choices=["fp32", "bf16", "fp16"], default="fp32")
     ap.add_argument("--baseline", choices=sorted(BASELINES), default="entmax")
     ap.add_argument("--backward", action="store_true", help="time forward + backward")
     ap.add_argument("--tau-mode", choices=["reference", "exact"], default="reference",
@@ -344,7 +344,7 @@ def main(argv=None) -> list[dict]:
             raise SystemExit(rc)
         return []
     configs = args.config or [(1, 4, 1024, 64), (1, 4, 2048, 64), (1, 4, 4096, 64)]
-    dtype = {"fp32": torch.float32, "bf16": torch.bfloat16}[args.dtype]
+    dtype = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
     results = []
     for B, H, N, d in configs:
         r = run_config(B, H, N, d, args.alpha, args.k_keep, dtype, args.baseline, args.backward,

@@ -50,7 +50,8 @@ def splash_attention(Q, K, V, Q_idx=None, K_idx=None, alpha: float = 1.5, k_keep
     """Block-sparse alpha-entmax attention, differentiable in Q, K and V.
 
     Q: [B, H, NQ, d]; K, V: [B, H, NK, d], d <= 128; float32, bfloat16 or
-    float16 (computed in float32) on one GPU.
+    float16 (16-bit inputs: fp32 arithmetic on 16-bit MFMA operands) on
+    one GPU.
     Q_idx: [B*H, NQ] and K_idx: [B*H, NK] integer positions (None: arange);
     key j is visible to query i iff K_idx[j] <= Q_idx[i].
     grad_mode "entmax" (default) uses the alpha-entmax Jacobian; "reference"

@@ -36,8 +36,7 @@ def forward_op(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx: 
                ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """out, taus, norms, mask, q_ptr, q_list, k_ptr, k_list and the support
     masks sup_mask (grad_mode is recorded for the backward only).  out is in
-    the kernels' layout (ops.to_kernel_layout: head dimension 64 or 128,
-    float16 as float32), so that the backward sees the unrounded output."""
+    the kernels' layout (ops.to_kernel_layout: head dimension 64 or 128)."""
     q, k, v, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     out, st = ops.splash_forward(q, k, v, qi, ki, alpha, k_keep, sm_scale, with_support=True,
                                  tau_mode=tau_mode, block_m=block_m)
@@ -54,7 +53,7 @@ def _forward_fake(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode,
     nQ64 = _nblocks(NQ, 64)
     f32 = dict(dtype=torch.float32, device=Q.device)
     i32 = dict(dtype=torch.int32, device=Q.device)
-    odt = torch.float32 if Q.dtype == torch.float16 else Q.dtype
+    odt = Q.dtype
     return (torch.empty((B, H, NQ, ops.kernel_head_dim(d)), dtype=odt, device=Q.device),
             torch.empty((BH, NQ), **f32), torch.empty((BH, NQ), **f32),
             torch.empty((BH, nQB, nKB), dtype=torch.uint8, device=Q.device),

@@ -31,8 +31,9 @@ class AdaptiveSplashAttention(nn.Module):
 
     forward(Q, K, V, Q_idx=None, K_idx=None): Q [B, H, NQ, d], K and V
     [B, H, NK, d]; Q_idx [B*H, NQ], K_idx [B*H, NK] positions (default
-    arange, i.e. causal).  float32, bfloat16 or float16 (computed in
-    float32).  Returns [B, H, NQ, d] in the input dtype.
+    arange, i.e. causal).  float32, bfloat16 or float16 (fp32 arithmetic;
+    16-bit inputs use 16-bit MFMA operands).  Returns [B, H, NQ, d] in the
+    input dtype.
     """
 
     def __init__(self, head_dim: int = 64, alpha: float = 1.5, k_keep: int = 8,

@@ -24,8 +24,9 @@ MAX_K_KEEP = 128
 KERNEL_HEAD_DIMS = (64, 128)
 
 # dtypes the kernels compute in
-_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
-# dtypes the Python entry points accept (float16 runs on the float32 kernels)
+_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16,
+           torch.float16: _lib.DTYPE_F16}
+# dtypes the Python entry points accept (each has its own kernels)
 INPUT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 GRAD_MODES = {"entmax": _lib.GRAD_ENTMAX, "reference": _lib.GRAD_REFERENCE}
@@ -194,20 +195,18 @@ def kernel_head_dim(d: int) -> int:
 
 def to_kernel_layout(*ts):
     """Tensors [..., d] as the kernels take them: the head dimension
-    zero-padded to 64 or 128, float16 widened to float32.
+    zero-padded to 64 or 128.
 
     The reference accepts any d <= 128 (adasplashattention.cu:542); the
     kernels are built for d = 64 and 128.  Zero columns add exact zeros to
     every dot product, so scores, weights and tau are those of the unpadded
     problem, and the padded columns of the outputs and of dQ, dK, dV are
-    zero.  float16 -> float32 is exact.  Both steps are differentiable
-    torch ops: gradients reach the caller's tensors through them.
+    zero.  The padding is a differentiable torch op: gradients reach the
+    caller's tensors through it.
     """
     dk = kernel_head_dim(ts[0].size(-1))
     out = []
     for t in ts:
-        if t.dtype == torch.float16:
-            t = t.float()
         if t.size(-1) != dk:
             t = F.pad(t, (0, dk - t.size(-1)))
         out.append(t)

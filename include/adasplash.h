@@ -21,7 +21,8 @@
  *     recomputes the mask in backward, :669-676).
  *   - k_keep is a run-time argument (the reference fixes K_KEEP=8 at
  *     compile time, :17-19).
- *   - bf16 is accepted besides fp32 (reference: fp32 only, :575-578).
+ *   - bf16 and fp16 are accepted besides fp32 (reference: fp32 only,
+ *     :575-578); 16-bit inputs compute in fp32 with 16-bit MFMA operands.
  *
  * Semantics kept from the reference: visibility K_idx[j] <= Q_idx[i]
  * (:181); scores clamped to [-10, 10] (:195-197); alpha clamped to
@@ -46,7 +47,7 @@
 extern "C" {
 #endif
 
-#define ASA_ABI_VERSION 5
+#define ASA_ABI_VERSION 6
 
 typedef enum asa_status {
   ASA_OK = 0,
@@ -55,7 +56,7 @@ typedef enum asa_status {
   ASA_ERR_DEVICE = 3            /* a HIP runtime call failed                  */
 } asa_status;
 
-typedef enum asa_dtype { ASA_DTYPE_F32 = 0, ASA_DTYPE_BF16 = 1 } asa_dtype;
+typedef enum asa_dtype { ASA_DTYPE_F32 = 0, ASA_DTYPE_BF16 = 1, ASA_DTYPE_F16 = 2 } asa_dtype;
 
 typedef enum asa_tau_mode {
   /* The reference's threshold: its 5-step recurrence on the row's top-k

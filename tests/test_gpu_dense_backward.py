@@ -16,11 +16,11 @@ from oracle import oracle as orc
 from tests._util import assert_close, causal_idx, make_inputs, np32, oracle_at_gpu_tau
 
 pytestmark = pytest.mark.gpu
-TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 4e-3}
 
 
 @pytest.mark.parametrize("mode", ["entmax", "reference"])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_dense_backward_matches_oracle_and_sparse(dev, dtype, mode):
     print(f"[dense-bwd] {dtype} {mode}", flush=True)
     B, H, NQ, NK, d = 1, 2, 300, 350, 64

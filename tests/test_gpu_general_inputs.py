@@ -3,12 +3,14 @@ against the CPU oracle at the caller's (unpadded) shape.
 
 The reference takes any head dimension up to D_MAX = 128
 (adasplashattention.cu:542).  Such inputs run on the d = 64 / 128 kernels
-with zero-padded columns, and float16 inputs on the float32 kernels
-(ops.to_kernel_layout); the default sm_scale is 1/sqrt(d) of the caller's
-d.  Checked through the autograd function, the custom operator and the
+with zero-padded columns (ops.to_kernel_layout), and float16 inputs on the
+float16 kernels; the default sm_scale is 1/sqrt(d) of the caller's d.
+Checked through the autograd function, the custom operator and the
 reference-style forward/backward.  Tolerances (max-norm relative): 1e-5
-for float32 compute; 2e-2 for bfloat16; 2e-3 for float16 inputs (float32
-compute, outputs and gradients rounded to float16: 2^-11 relative).
+for float32; 2e-2 for bfloat16; 4e-3 for float16 (fp32 arithmetic on
+float16 MFMA operands: the weights P and, in the dense passes, ds rounded
+to 11 significant bits, 2^-11 relative each, plus outputs and gradients
+rounded to float16).
 """
 import numpy as np
 import pytest
@@ -26,8 +28,9 @@ CASES = [
     ("d32_fp32", 32, torch.float32, 1e-5),
     ("d100_fp32", 100, torch.float32, 1e-5),
     ("d96_bf16", 96, torch.bfloat16, 2e-2),
-    ("d64_fp16", 64, torch.float16, 2e-3),
-    ("d48_fp16", 48, torch.float16, 2e-3),
+    ("d64_fp16", 64, torch.float16, 4e-3),
+    ("d48_fp16", 48, torch.float16, 4e-3),
+    ("d128_fp16", 128, torch.float16, 4e-3),
 ]
 
 

@@ -27,10 +27,11 @@ def test_fake_shapes_on_meta_tensors():
 
 def test_fake_shapes_general_inputs():
     """d not in {64, 128} and float16: the operator's output is in the
-    kernels' layout (d padded to 64, float32); the gradients in the caller's."""
+    kernels' layout (d padded to 64, the input dtype); the gradients in the
+    caller's."""
     Q = torch.empty(1, 2, 70, 40, device="meta", dtype=torch.float16)
     outs = torch.ops.adasplash.forward(Q, Q, Q, None, None, 1.5, 8, 40 ** -0.5, "entmax")
-    assert (tuple(outs[0].shape), outs[0].dtype) == ((1, 2, 70, 64), torch.float32)
+    assert (tuple(outs[0].shape), outs[0].dtype) == ((1, 2, 70, 64), torch.float16)
     g = torch.ops.adasplash.backward(Q, Q, Q, None, None, outs[0], outs[0], *outs[1:], 1.5, 8,
                                      40 ** -0.5, "entmax")
     assert [(tuple(x.shape), x.dtype) for x in g] == [((1, 2, 70, 40), torch.float16)] * 3
