@@ -53,10 +53,8 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "8051109d2a9e1562"
-HBM_TRAFFIC = {'bounds': 1109205, 'select': 103116095, 'tau': 34745407, 'refine': 74989494,
-               'compact': 2751144, 'forward': 207511046, 'bwd_dq_sparse': 248097115,
-               'bwd_dkdv_sparse': 276792874}
+HBM_TRAFFIC_SOURCES = "ac8bd49a37dcb9bb"
+HBM_TRAFFIC = {'bounds': 1110085, 'select': 103126348, 'tau': 34745373, 'refine': 73995236, 'compact': 2743578, 'forward': 207486763, 'bwd_dq_sparse': 247608498, 'bwd_dkdv_sparse': 276780559}
 
 
 def source_hash() -> str:
