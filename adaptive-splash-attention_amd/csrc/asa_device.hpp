@@ -290,10 +290,14 @@ __device__ __forceinline__ typename Half<T>::v4 read_tr16(const T* p) {
 //   row_half_mirror 0x141: lane i <- lane i^7 (in 8-lane half rows)
 //   row_mirror 0x140: lane i <- lane i^15 (in 16-lane rows)
 //   row_shr:n 0x110+n, row_bcast:15 0x142, row_bcast:31 0x143
+// dpp_mov sets bound_ctrl (a lane whose source is out of range reads 0):
+// the compiler then folds a move into the VALU operation that consumes it
+// (v_add_f32_dpp and the like) instead of issuing both.  The patterns above
+// other than row_shr never read out of range.
 // ---------------------------------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
-  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xf, 0xf, false));
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xf, 0xf, true));
 }
 // lane i <- lane i ^ M
 template <int M>

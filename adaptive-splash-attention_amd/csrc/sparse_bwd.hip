@@ -132,18 +132,21 @@ template <> struct Chunk<float> {
 
 // Sum over aligned groups of G lanes (G a power of two <= 32) by lane
 // exchanges: each step adds a lane's value and its partner's, so every lane
-// of a group gets a bit-identical sum.
+// of a group gets a bit-identical sum.  After the steps within a quad
+// (partners i^1, i^2) every lane of a quad holds the quad's sum, so the
+// next steps may pair lane i with any lane of the other quad (octet) of its
+// octet (16 lanes): i^7 and i^15 are single DPP mirrors, which the compiler
+// fuses into the adds.
 template <int G>
 __device__ __forceinline__ float group_lanes_sum(float v) {
-  auto x = [](float a, auto m) {
-    constexpr int M = decltype(m)::value;
-    return __uint_as_float(lane_xor<M>(__float_as_uint(a)));
+  auto x = [](float a, auto ctrl) {
+    return __uint_as_float(dpp_mov<decltype(ctrl)::value>(__float_as_uint(a)));
   };
-  if constexpr (G >= 2) v += x(v, std::integral_constant<int, 1>{});
-  if constexpr (G >= 4) v += x(v, std::integral_constant<int, 2>{});
-  if constexpr (G >= 8) v += x(v, std::integral_constant<int, 4>{});
-  if constexpr (G >= 16) v += x(v, std::integral_constant<int, 8>{});
-  if constexpr (G >= 32) v += x(v, std::integral_constant<int, 16>{});
+  if constexpr (G >= 2) v += x(v, std::integral_constant<int, 0xB1>{});   // i^1
+  if constexpr (G >= 4) v += x(v, std::integral_constant<int, 0x4E>{});   // i^2
+  if constexpr (G >= 8) v += x(v, std::integral_constant<int, 0x141>{});  // i^7
+  if constexpr (G >= 16) v += x(v, std::integral_constant<int, 0x140>{}); // i^15
+  if constexpr (G >= 32) v += __uint_as_float(lane_xor<16>(__float_as_uint(v)));
   return v;
 }
 
@@ -169,6 +172,7 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
   __shared__ int s_rn[4][16];                // listed keys per row of the wave
   __shared__ int s_off[4][16];               // start of each row's list in s_flat
   __shared__ int s_rank[4][16];              // rows in descending count order
+  __shared__ float s_cfac[4][16];            // entmax mode: (norm + eps)^(alpha - 2) per row
   __shared__ int s_list[4][RPR][kRowList];   // chunked path
   __shared__ uint64_t s_mw[4][kChunk][16];   // mask words of a chunk of tiles: [tile][row]
   __shared__ int s_kb[4][kChunk];            // first key of each tile
@@ -199,6 +203,22 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
     if constexpr (REF) wv = v > kEps ? wv : 0.0f;  // the reference's u > EPS
     return wv;
   };
+
+  // The rows' (norm + eps)^(alpha - 2), one lane per row of the wave: the
+  // double pow runs once per wave instead of once per lane group and row
+  // (the groups finish their rows at different steps, so per-row calls
+  // would run one after another).
+  if constexpr (!REF) {
+    if (lane < 16) {
+      const int qrow = qb * kBlock + 16 * w + lane;
+      float c = 0.0f;
+      if (qrow < NQ) {
+        const float norm = p.norms[size_t(bh) * NQ + qrow];
+        c = static_cast<float>(pow(static_cast<double>(norm + kEps), static_cast<double>(alpha) - 2.0));
+      }
+      s_cfac[w][lane] = c;
+    }
+  }
 
   // One row's state: its q and dO chunks, clipping, and the fp32 sums
   // A = sum w dp k_j, B = sum w k_j, sum w, sum w dp.
@@ -264,7 +284,7 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
       cfac = p.delta[rows + row];
       shift = p.delta[row];
     } else {
-      cfac = static_cast<float>(pow(static_cast<double>(norm + kEps), static_cast<double>(alpha) - 2.0));
+      cfac = s_cfac[w][rr];
       shift = sw > 0.0f ? swdp / sw : 0.0f;
       if (!finite(shift)) shift = 0.0f;
     }
@@ -280,19 +300,31 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
       p.rowrec[row] = RowRec{clip.nt, 1.0f / (norm + kEps), cfac, -cfac * shift};
   };
 
-  // ---- count the keys each row of the wave lists (lane: row c16, mask g4)
+  // ---- count the keys each row of the wave lists.  A row's four masks of
+  // a tile are one 8-byte word (bit 16 g + 4 f + r <-> key 16 f + 4 g + r);
+  // lane (row c16, slot g4) reads the words of tiles e0 + 4 u + g4, eight
+  // loads (32 tiles) in flight together.  The first 32 tiles' words stay in
+  // registers for the listing below.
   const int c16 = lane & 15, g4 = lane >> 4;
-  const uint16_t* lm = wmask + 4 * c16 + g4;  // this lane's mask of tile e at + e * 256
-  int nl = 0;
-  {
-    int e = e0;
-    for (; e + 4 <= e1; e += 4) {
-      const uint32_t m0 = lm[size_t(e) * 256], m1 = lm[size_t(e + 1) * 256];
-      const uint32_t m2 = lm[size_t(e + 2) * 256], m3 = lm[size_t(e + 3) * 256];
-      nl += __builtin_popcount(m0) + __builtin_popcount(m1) + __builtin_popcount(m2) +
-            __builtin_popcount(m3);
+  const uint64_t* lw = reinterpret_cast<const uint64_t*>(wmask + 4 * c16);  // tile e at + e * 64
+  constexpr int kWords = 8;  // words per lane per batch of 4 * kWords tiles
+  auto load_words = [&](int e8, uint64_t (&wd)[kWords], int (&kbs)[kWords]) {
+    for (int u = 0; u < kWords; ++u) {
+      const int e = e8 + 4 * u + g4;
+      wd[u] = e < e1 ? lw[size_t(e) * 64] : 0ull;
+      kbs[u] = e < e1 ? ql[e] * kBlock : 0;
     }
-    for (; e < e1; ++e) nl += __builtin_popcount(uint32_t(lm[size_t(e) * 256]));
+  };
+  uint64_t wd0[kWords];
+  int kb0[kWords];
+  load_words(e0, wd0, kb0);
+  int nl = 0;
+  for (int u = 0; u < kWords; ++u) nl += __builtin_popcountll(wd0[u]);
+  for (int e8 = e0 + 4 * kWords; e8 < e1; e8 += 4 * kWords) {
+    uint64_t wd[kWords];
+    int kbs[kWords];
+    load_words(e8, wd, kbs);
+    for (int u = 0; u < kWords; ++u) nl += __builtin_popcountll(wd[u]);
   }
   const int rn = int(group_reduce_bits(uint32_t(nl), [](uint32_t x, uint32_t y) { return x + y; }));
   if (lane < 16) s_rn[w][lane] = rn;
@@ -316,27 +348,32 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
       s_rank[w][rank] = lane;
     }
     int base = off;
-    for (int e8 = e0; e8 < e1; e8 += 8) {
-      uint32_t mm[8];  // 8 tiles' masks in flight together
-      for (int u = 0; u < 8; ++u) mm[u] = e8 + u < e1 ? uint32_t(lm[size_t(e8 + u) * 256]) : 0u;
-      for (int u = 0; u < 8 && e8 + u < e1; ++u) {
-        uint32_t m = mm[u];
-        const uint32_t n = uint32_t(__builtin_popcount(m));
-        // prefix of the counts over the row's lanes g4 = 0..3 (lanes c16 + 16 g4)
+    auto list_words = [&](int e8, const uint64_t (&wd)[kWords], const int (&kbs)[kWords]) {
+      for (int u = 0; u < kWords && e8 + 4 * u < e1; ++u) {
+        uint64_t m = wd[u];
+        const uint32_t n = uint32_t(__builtin_popcountll(m));
+        // prefix of the counts over the row's four tiles g4 = 0..3 (lanes c16 + 16 g4)
         const auto pa = __builtin_amdgcn_permlane16_swap(n, n, false, false);
         const uint32_t pair = pa[0] + pa[1];
         const auto pb = __builtin_amdgcn_permlane32_swap(pair, pair, false, false);
         const uint32_t tot = pb[0] + pb[1];
         int pos = base + int(((g4 & 1) ? pair - n : 0u) + ((g4 & 2) ? tot - pair : 0u));
-        const int kb = ql[e8 + u] * kBlock + 4 * g4;
+        const int kb = kbs[u];
         while (m) {
-          const int b = __builtin_ctz(m);
+          const int b = __builtin_ctzll(m);
           m &= m - 1;
-          // bit 4 f + r of mask g4 -> key 16 f + 4 g4 + r
-          s_flat[w][pos++] = kb + 16 * (b >> 2) + (b & 3);
+          // bit 16 g + 4 f + r -> key 16 f + 4 g + r
+          s_flat[w][pos++] = kb + 16 * ((b >> 2) & 3) + 4 * (b >> 4) + (b & 3);
         }
         base += int(tot);
       }
+    };
+    list_words(e0, wd0, kb0);
+    for (int e8 = e0 + 4 * kWords; e8 < e1; e8 += 4 * kWords) {
+      uint64_t wd[kWords];
+      int kbs[kWords];
+      load_words(e8, wd, kbs);
+      list_words(e8, wd, kbs);
     }
     auto rank_row = [&](int j) { return s_rank[w][j * RPR + ((j & 1) ? RPR - 1 - grp : grp)]; };
     int j = 0;
