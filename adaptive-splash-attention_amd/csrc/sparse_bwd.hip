@@ -47,6 +47,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kRowList = 64;   // keys listed per row before a dQ phase B
 constexpr int kKeyList = 128;  // rows listed per key before a dK/dV phase B
+constexpr int kEvents = 128;   // dK/dV phase A events held per wave
 constexpr int kBatch = 2;      // dK/dV entries whose gathers are in flight together
 constexpr int kBatchQ = 3;     // dQ entries whose gathers are in flight together
 constexpr int kChunk = 16;     // tiles whose masks are fetched together
@@ -466,6 +467,8 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   // lane for the phase A stores of lanes with nothing to list
   __shared__ int s_lists[4 * KPW * kKeyList + 4 * kWave];
   __shared__ int s_cnt[4][KPW];
+  __shared__ int s_evr[4][kEvents];      // events: a row listing some of the wave's keys
+  __shared__ uint8_t s_evm[4][kEvents];  //   and its key bits (bit k <-> key jb + k)
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int task = xcd_task(blockIdx.x, nKB * SLICES * p.d.BH);
@@ -545,8 +548,13 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   // Lane L <-> row L of a tile.  The tiles' query blocks and q_list
   // positions are fetched for up to 64 tiles at once (one lane each); the
   // mask words then come kTileGroup tiles at a time, the next group's
-  // loads in flight while the current group is listed.  The list lengths
-  // are wave-uniform (scalar registers); drain() reads them from s_cnt.
+  // loads in flight while the current group is listed.  A tile's rows that
+  // list any of the wave's keys (a few of its 64) become events in LDS: the
+  // row and its KPW key bits.  Every 64 events or so, one lane per event
+  // appends the rows to the keys' lists (one ballot per key), so the
+  // per-key ballots run per 64 events instead of per tile.  Events and
+  // lists keep ascending row order.  The list lengths are wave-uniform
+  // (scalar registers); drain() reads them from s_cnt.
   constexpr int kTileGroup = 8;
   int cnt[KPW];
   for (int k = 0; k < KPW; ++k) cnt[k] = 0;
@@ -556,18 +564,46 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
     drain();
     for (int k = 0; k < KPW; ++k) cnt[k] = 0;
   };
+  const int dump = 4 * KPW * kKeyList + w * kWave + lane;
+  int nev = 0;  // events held (wave-uniform), at most kEvents
+  auto list_events = [&]() {
+    for (int c0 = 0; c0 < nev; c0 += kWave) {
+      // room for 64 more rows in every list of the wave, else drain first
+      bool room = true;
+      for (int k = 0; k < KPW; ++k) room = room && cnt[k] + kWave <= kKeyList;
+      if (!room) drain_lists();
+      const bool live = c0 + lane < nev;
+      const int row = live ? s_evr[w][c0 + lane] : 0;
+      const uint32_t bits = live ? uint32_t(s_evm[w][c0 + lane]) : 0u;
+      // Every lane stores: a lane whose event does not list the key writes
+      // its dump slot instead of branching around the store.
+      for (int k = 0; k < KPW; ++k) {
+        const bool on = ((bits >> k) & 1u) != 0;
+        const uint64_t col = __ballot(on);
+        const int at = (w * KPW + k) * kKeyList + cnt[k] + lane_rank(col);
+        s_lists[on ? at : dump] = row;
+        cnt[k] += __builtin_popcountll(col);
+      }
+    }
+    nev = 0;
+  };
   const int32_t* pm = p.posmap + size_t(bh) * nQB * nKB + kb;  // tile (qb, kb) at + qb * nKB
   const int x0 = kp[kb], x1 = kp[kb + 1];
-  static_assert(KPW <= 8 && kBlock % KPW == 0, "a wave's keys must fit one mask pair");
+  static_assert(KPW == 2 || KPW == 4 || KPW == 8, "a wave's keys must fit one mask pair");
+  // The wave's keys jb .. jb + KPW - 1 in row L's masks g and g + 1 (g =
+  // gb, even; bit 16 (g - gb) + 4 f + r <-> key 16 f + 4 g + r): KPW <= 4
+  // keys are KPW consecutive bits from b0; eight keys (jb a multiple of 8)
+  // are the nibbles at b0 and b0 + 16.
   const int gb = ((jb >> 2) & 3) & ~1;
-  const int dump = 4 * KPW * kKeyList + w * kWave + lane;
+  const int b0 = 16 * (((jb >> 2) & 3) - gb) + 4 * (jb >> 4) + (jb & 3);
+  auto key_bits = [&](uint32_t word) -> uint32_t {
+    if constexpr (KPW == 8) return ((word >> b0) & 0xFu) | (((word >> (b0 + 16)) & 0xFu) << 4);
+    else return (word >> b0) & ((1u << KPW) - 1u);
+  };
   for (int m0 = x0; m0 < x1; m0 += kWave) {
     const int nm = min(kWave, x1 - m0);
     const int my_qb = lane < nm ? kl[m0 + lane] : 0;
     const int my_e = lane < nm ? pm[size_t(my_qb) * nKB] : 0;
-    // Row L's masks g and g + 1 (g = gb, even) of a tile, which hold the
-    // bits of all this wave's keys (KPW <= 8 consecutive keys span at most
-    // two values of (key >> 2) & 3, and an aligned pair covers them).
     const uint16_t* rowm = hmask + (lane >> 4) * 64 + 4 * (lane & 15) + gb;
     // (slots past the last tile re-read the last tile and are not used)
     auto fetch = [&](int g0, uint32_t (&wd)[kTileGroup]) {
@@ -583,27 +619,22 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
 #pragma unroll
       for (int u = 0; u < kTileGroup; ++u) {
         if (g0 + u >= nm) break;
-        // room for a whole tile in every list of the wave, else drain first
-        bool room = true;
-        for (int k = 0; k < KPW; ++k) room = room && cnt[k] + kWave <= kKeyList;
-        if (!room) drain_lists();
-        // bit 16 (g - gb) + 4 f + r of the pair <-> key 16 f + 4 g + r.
-        // Every lane stores: a lane whose row does not list the key writes
-        // its dump slot instead of branching around the store.
-        const int row = __builtin_amdgcn_readlane(my_qb, g0 + u) * kBlock + lane;
-        for (int k = 0; k < KPW; ++k) {
-          const int key = jb + k;
-          const int bit = 16 * (((key >> 2) & 3) - gb) + 4 * (key >> 4) + (key & 3);
-          const bool on = ((word[u] >> bit) & 1u) != 0;
-          const uint64_t col = __ballot(on);
-          const int at = (w * KPW + k) * kKeyList + cnt[k] + lane_rank(col);
-          s_lists[on ? at : dump] = row;
-          cnt[k] += __builtin_popcountll(col);
+        const uint32_t bits = key_bits(word[u]);
+        const uint64_t any = __ballot(bits != 0u);
+        if (any != 0ull) {  // wave-uniform
+          if (bits != 0u) {
+            const int at = nev + lane_rank(any);
+            s_evr[w][at] = __builtin_amdgcn_readlane(my_qb, g0 + u) * kBlock + lane;
+            s_evm[w][at] = uint8_t(bits);
+          }
+          nev += __builtin_popcountll(any);
+          if (nev > kEvents - kWave) list_events();  // room for the next tile's events
         }
       }
       for (int u = 0; u < kTileGroup; ++u) word[u] = next[u];
     }
   }
+  list_events();
   drain_lists();
 
   if (jok) {
