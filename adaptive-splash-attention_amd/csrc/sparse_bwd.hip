@@ -46,9 +46,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRowList = 64;   // keys listed per row before a dQ phase B
-constexpr int kKeyList = 128;  // rows listed per key before a dK/dV phase B
-constexpr int kEvents = 128;   // dK/dV phase A events held per wave
-constexpr int kBatch = 2;      // dK/dV entries whose gathers are in flight together
+// rows listed per key before a dK/dV phase B (KPW keys per wave)
+template <int KPW> constexpr int key_list() { return KPW > 8 ? 96 : 128; }
+constexpr int kBatch = 2;      // dK/dV entries per lane group whose gathers are in flight together
 constexpr int kBatchQ = 3;     // dQ entries whose gathers are in flight together
 constexpr int kChunk = 16;     // tiles whose masks are fetched together
 constexpr int kFlat = 1024;    // keys a dQ wave lists at once on its balanced path
@@ -67,8 +67,7 @@ template <> struct Chunk<u16> {
   }
   static __device__ __forceinline__ void load(const u16* p, float (&x)[8]) { unpack(raw(p), x); }
   // sum_i a_i b_i of two raw chunks: products exact, fp32 sums (v_dot2_f32_bf16)
-  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b) {
-    float s = 0.0f;
+  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b, float s = 0.0f) {
     s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.x), __builtin_bit_cast(bf16x2, b.x), s, false);
     s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.y), __builtin_bit_cast(bf16x2, b.y), s, false);
     s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.z), __builtin_bit_cast(bf16x2, b.z), s, false);
@@ -95,8 +94,7 @@ template <> struct Chunk<h16> {
   }
   static __device__ __forceinline__ void load(const h16* p, float (&x)[8]) { unpack(raw(p), x); }
   // sum_i a_i b_i of two raw chunks: products exact, fp32 sums (v_dot2_f32_f16)
-  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b) {
-    float s = 0.0f;
+  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b, float s = 0.0f) {
     s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a.x), __builtin_bit_cast(f16x2, b.x), s, false);
     s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a.y), __builtin_bit_cast(f16x2, b.y), s, false);
     s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a.z), __builtin_bit_cast(f16x2, b.z), s, false);
@@ -120,8 +118,8 @@ template <> struct Chunk<float> {
     x[3] = __uint_as_float(v.w);
   }
   static __device__ __forceinline__ void load(const float* p, float (&x)[4]) { unpack(raw(p), x); }
-  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b) {
-    float s = __uint_as_float(a.x) * __uint_as_float(b.x);
+  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b, float s = 0.0f) {
+    s = fmaf(__uint_as_float(a.x), __uint_as_float(b.x), s);
     s = fmaf(__uint_as_float(a.y), __uint_as_float(b.y), s);
     s = fmaf(__uint_as_float(a.z), __uint_as_float(b.z), s);
     return fmaf(__uint_as_float(a.w), __uint_as_float(b.w), s);
@@ -452,25 +450,41 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
 // ---------------------------------------------------------------------------
 // dK, dV
 // ---------------------------------------------------------------------------
-template <typename T, int D> constexpr int keys_per_block() { return 4 * (kWave / (D / Chunk<T>::E)); }
+// Each lane holds kKeyChunks 16-byte chunks of a key's rows.  Two chunks
+// (fewer lanes per key, 16 keys per wave at d = 64) spread a pair's fixed
+// work over more of the head dimension but lock-step more keys of unequal
+// list lengths and hold fewer gathers in flight: at the headline shape the
+// dK/dV pass took 330-400 us with two chunks against 271 us with one.
+constexpr int kKeyChunks = 1;
+template <typename T, int D> constexpr int key_lanes() { return D / (kKeyChunks * Chunk<T>::E); }
+template <typename T, int D> constexpr int keys_per_block() { return 4 * (kWave / key_lanes<T, D>()); }
 
 template <typename T, int D, int AC, bool REF>
 __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams p) {
   using C = Chunk<T>;
   constexpr int E = C::E;
-  constexpr int LPR = D / E;          // lanes per key (16 bytes each)
+  constexpr int NC = kKeyChunks;      // 16-byte chunks per lane
+  constexpr int EL = NC * E;          // elements per lane
+  constexpr int LPR = key_lanes<T, D>();  // lanes per key
   constexpr int KPW = kWave / LPR;    // keys per wave
   constexpr int KPB = 4 * KPW;        // keys per block
   constexpr int SLICES = kBlock / KPB;
   constexpr int PP = AlphaPow<AC>::P, PW = AlphaPow<AC>::W;
+  constexpr int kKeyList = key_list<KPW>();
+  // phase A: tiles whose mask words are loaded together, and the events
+  // held per wave (one group's worth beyond a partly listed chunk)
+  constexpr int kTileGroup = KPW > 8 ? 4 : 8;
+  constexpr int kEvents = kWave + kTileGroup * kWave;
   // the waves' key lists, [wave][key][kKeyList], then one dump slot per
   // lane for the phase A stores of lanes with nothing to list
   __shared__ int s_lists[4 * KPW * kKeyList + 4 * kWave];
   __shared__ int s_cnt[4][KPW];
-  __shared__ int s_evr[4][kEvents];      // events: a row listing some of the wave's keys
-  __shared__ uint8_t s_evm[4][kEvents];  //   and its key bits (bit k <-> key jb + k)
+  using Bits = std::conditional_t<(KPW > 8), uint16_t, uint8_t>;
+  __shared__ int s_evr[4][kEvents];   // events: a row listing some of the wave's keys
+  __shared__ Bits s_evm[4][kEvents];  //   and its key bits (bit k <-> key jb + k)
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: w, jb and b0 in scalar registers
   const int task = xcd_task(blockIdx.x, nKB * SLICES * p.d.BH);
   const int slice = task % SLICES, kb = (task / SLICES) % nKB, bh = task / (SLICES * nKB);
   const int sub = lane % LPR, grp = lane / LPR;
@@ -492,13 +506,17 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   const int32_t* kl = p.k_list + size_t(bh) * nKB * nQB;
   const uint16_t* hmask = p.sup.mask + size_t(bh) * nQB * nKB * 256;
 
-  uint4 kv{0u, 0u, 0u, 0u}, vv{0u, 0u, 0u, 0u};  // raw 16-byte chunks of the key's rows
-  if (jok) {
-    kv = C::raw(static_cast<const T*>(p.k) + krow * D + sub * E);
-    vv = C::raw(static_cast<const T*>(p.v) + krow * D + sub * E);
+  uint4 kv[NC], vv[NC];  // raw 16-byte chunks of the key's rows
+  for (int c = 0; c < NC; ++c) {
+    kv[c] = uint4{0u, 0u, 0u, 0u};
+    vv[c] = uint4{0u, 0u, 0u, 0u};
+    if (jok) {
+      kv[c] = C::raw(static_cast<const T*>(p.k) + krow * D + sub * EL + c * E);
+      vv[c] = C::raw(static_cast<const T*>(p.v) + krow * D + sub * EL + c * E);
+    }
   }
-  float dk[E], dv[E];
-  for (int x = 0; x < E; ++x) dk[x] = dv[x] = 0.0f;
+  float dk[EL], dv[EL];
+  for (int x = 0; x < EL; ++x) dk[x] = dv[x] = 0.0f;
 
   const int* mylist = s_lists + (w * KPW + grp) * kKeyList;
   // phase B: this group's listed rows, kBatch at a time in every group
@@ -508,24 +526,36 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
     for (int q = 0; q < nmax; q += kBatch) {
       int r[kBatch];
       bool val[kBatch];
-      uint4 qraw[kBatch], graw[kBatch];
+      uint4 qraw[kBatch][NC], graw[kBatch][NC];
       RowRec rc[kBatch];
       for (int u = 0; u < kBatch; ++u) {
         val[u] = q + u < cnt;
         r[u] = val[u] ? mylist[q + u] : 0;
       }
       for (int u = 0; u < kBatch; ++u) {
-        qraw[u] = C::raw(Qb + size_t(r[u]) * D + sub * E);
-        graw[u] = C::raw(dOb + size_t(r[u]) * D + sub * E);
+        for (int c = 0; c < NC; ++c) {
+          qraw[u][c] = C::raw(Qb + size_t(r[u]) * D + sub * EL + c * E);
+          graw[u][c] = C::raw(dOb + size_t(r[u]) * D + sub * EL + c * E);
+        }
         rc[u] = rec[r[u]];
       }
       for (int u = 0; u < kBatch; ++u) {
-        const float s = group_lanes_sum<LPR>(C::dot(qraw[u], kv));
-        const float dp = group_lanes_sum<LPR>(C::dot(graw[u], vv));
+        float s = 0.0f, dp = 0.0f;
+        for (int c = 0; c < NC; ++c) {
+          s = C::dot(qraw[u][c], kv[c], s);
+          dp = C::dot(graw[u][c], vv[c], dp);
+        }
+        s = group_lanes_sum<LPR>(s);
+        dp = group_lanes_sum<LPR>(dp);
         if (val[u]) {
-          float qr[E], gr[E];
-          C::unpack(qraw[u], qr);
-          C::unpack(graw[u], gr);
+          float qr[EL], gr[EL];
+          for (int c = 0; c < NC; ++c) {
+            float x8[E];
+            C::unpack(qraw[u][c], x8);
+            for (int x = 0; x < E; ++x) qr[c * E + x] = x8[x];
+            C::unpack(graw[u][c], x8);
+            for (int x = 0; x < E; ++x) gr[c * E + x] = x8[x];
+          }
           // ClippedU of a valid row (the lists hold valid rows only)
           const float lo = fmaxf(fmaf(-10.f, am1, rc[u].nt), 0.f);
           const float hi = fmaxf(fmaf(10.f, am1, rc[u].nt), 0.f);
@@ -535,7 +565,7 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
           if constexpr (REF) wv = v > kEps ? wv : 0.0f;  // the reference's u > EPS
           float ds = wv * fmaf(rc[u].c, dp, rc[u].cs);
           ds = finite(ds) ? ds : 0.0f;
-          for (int x = 0; x < E; ++x) {
+          for (int x = 0; x < EL; ++x) {
             dk[x] = fmaf(ds, qr[x], dk[x]);
             dv[x] = fmaf(pn, gr[x], dv[x]);
           }
@@ -550,12 +580,13 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   // mask words then come kTileGroup tiles at a time, the next group's
   // loads in flight while the current group is listed.  A tile's rows that
   // list any of the wave's keys (a few of its 64) become events in LDS: the
-  // row and its KPW key bits.  Every 64 events or so, one lane per event
-  // appends the rows to the keys' lists (one ballot per key), so the
-  // per-key ballots run per 64 events instead of per tile.  Events and
-  // lists keep ascending row order.  The list lengths are wave-uniform
-  // (scalar registers); drain() reads them from s_cnt.
-  constexpr int kTileGroup = 8;
+  // row and its KPW key bits.  Once a group leaves fewer than a group's
+  // worth of free event slots, one lane per event appends the rows to the
+  // keys' lists (one ballot per key and 64 events), so the per-key ballots
+  // run per 64 events instead of per tile, and a drain can start only
+  // between groups.  Events and lists keep ascending row order.  The list
+  // lengths are wave-uniform (scalar registers); drain() reads them from
+  // s_cnt.
   int cnt[KPW];
   for (int k = 0; k < KPW; ++k) cnt[k] = 0;
   auto drain_lists = [&]() {
@@ -568,37 +599,49 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   int nev = 0;  // events held (wave-uniform), at most kEvents
   auto list_events = [&]() {
     for (int c0 = 0; c0 < nev; c0 += kWave) {
-      // room for 64 more rows in every list of the wave, else drain first
-      bool room = true;
-      for (int k = 0; k < KPW; ++k) room = room && cnt[k] + kWave <= kKeyList;
-      if (!room) drain_lists();
       const bool live = c0 + lane < nev;
       const int row = live ? s_evr[w][c0 + lane] : 0;
       const uint32_t bits = live ? uint32_t(s_evm[w][c0 + lane]) : 0u;
+      uint64_t col[KPW];
+      bool room = true;  // for these events in every list of the wave, else drain first
+      for (int k = 0; k < KPW; ++k) {
+        col[k] = __ballot(((bits >> k) & 1u) != 0);
+        room = room && cnt[k] + __builtin_popcountll(col[k]) <= kKeyList;
+      }
+      if (!room) drain_lists();
       // Every lane stores: a lane whose event does not list the key writes
       // its dump slot instead of branching around the store.
       for (int k = 0; k < KPW; ++k) {
         const bool on = ((bits >> k) & 1u) != 0;
-        const uint64_t col = __ballot(on);
-        const int at = (w * KPW + k) * kKeyList + cnt[k] + lane_rank(col);
+        const int at = (w * KPW + k) * kKeyList + cnt[k] + lane_rank(col[k]);
         s_lists[on ? at : dump] = row;
-        cnt[k] += __builtin_popcountll(col);
+        cnt[k] += __builtin_popcountll(col[k]);
       }
     }
     nev = 0;
   };
   const int32_t* pm = p.posmap + size_t(bh) * nQB * nKB + kb;  // tile (qb, kb) at + qb * nKB
   const int x0 = kp[kb], x1 = kp[kb + 1];
-  static_assert(KPW == 2 || KPW == 4 || KPW == 8, "a wave's keys must fit one mask pair");
-  // The wave's keys jb .. jb + KPW - 1 in row L's masks g and g + 1 (g =
-  // gb, even; bit 16 (g - gb) + 4 f + r <-> key 16 f + 4 g + r): KPW <= 4
-  // keys are KPW consecutive bits from b0; eight keys (jb a multiple of 8)
-  // are the nibbles at b0 and b0 + 16.
-  const int gb = ((jb >> 2) & 3) & ~1;
+  static_assert(KPW == 2 || KPW == 4 || KPW == 8 || KPW == 16, "a wave's keys: 2, 4, 8 or 16");
+  // The wave's keys jb .. jb + KPW - 1 in row L's masks (bit 16 g + 4 f + r
+  // of its 64-bit word <-> key 16 f + 4 g + r).  Up to eight keys lie in
+  // masks g and g + 1 (g = gb, even): a 32-bit load at mask gb, where two
+  // or four keys are consecutive bits from b0 and eight (jb a multiple of
+  // 8) the nibbles at b0 and b0 + 16.  Sixteen keys (jb = 16 f) are the nibbles at 4 f, 16 +
+  // 4 f, 32 + 4 f and 48 + 4 f of the whole word.
+  using Word = std::conditional_t<(KPW > 8), uint64_t, uint32_t>;
+  const int gb = KPW > 8 ? 0 : ((jb >> 2) & 3) & ~1;
   const int b0 = 16 * (((jb >> 2) & 3) - gb) + 4 * (jb >> 4) + (jb & 3);
-  auto key_bits = [&](uint32_t word) -> uint32_t {
-    if constexpr (KPW == 8) return ((word >> b0) & 0xFu) | (((word >> (b0 + 16)) & 0xFu) << 4);
-    else return (word >> b0) & ((1u << KPW) - 1u);
+  auto key_bits = [&](Word word) -> uint32_t {
+    if constexpr (KPW == 16) {
+      const uint32_t lo = uint32_t(word), hi = uint32_t(word >> 32);
+      return ((lo >> b0) & 0xFu) | (((lo >> (b0 + 16)) & 0xFu) << 4) | (((hi >> b0) & 0xFu) << 8) |
+             (((hi >> (b0 + 16)) & 0xFu) << 12);
+    } else if constexpr (KPW == 8) {
+      return ((word >> b0) & 0xFu) | (((word >> (b0 + 16)) & 0xFu) << 4);
+    } else {
+      return (word >> b0) & ((1u << KPW) - 1u);
+    }
   };
   for (int m0 = x0; m0 < x1; m0 += kWave) {
     const int nm = min(kWave, x1 - m0);
@@ -606,45 +649,60 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
     const int my_e = lane < nm ? pm[size_t(my_qb) * nKB] : 0;
     const uint16_t* rowm = hmask + (lane >> 4) * 64 + 4 * (lane & 15) + gb;
     // (slots past the last tile re-read the last tile and are not used)
-    auto fetch = [&](int g0, uint32_t (&wd)[kTileGroup]) {
+    auto fetch = [&](int g0, Word (&wd)[kTileGroup]) {
       for (int u = 0; u < kTileGroup; ++u) {
         const int e = __builtin_amdgcn_readlane(my_e, min(g0 + u, nm - 1));
-        wd[u] = *reinterpret_cast<const uint32_t*>(rowm + size_t(e) * 256);
+        wd[u] = *reinterpret_cast<const Word*>(rowm + size_t(e) * 256);
       }
     };
-    uint32_t word[kTileGroup], next[kTileGroup];
+    // A group's words give way to its key bits before the next group's
+    // loads are issued; the listing (and any drain it starts) runs after
+    // the group, with only those loads in flight live.
+    Word word[kTileGroup];
     fetch(0, word);
     for (int g0 = 0; g0 < nm; g0 += kTileGroup) {
-      fetch(g0 + kTileGroup, next);  // unconditional: the waits stay exact
+      uint32_t kbits[kTileGroup];
+      for (int u = 0; u < kTileGroup; ++u) kbits[u] = key_bits(word[u]);
+      fetch(g0 + kTileGroup, word);  // unconditional: the waits stay exact
 #pragma unroll
       for (int u = 0; u < kTileGroup; ++u) {
         if (g0 + u >= nm) break;
-        const uint32_t bits = key_bits(word[u]);
+        const uint32_t bits = kbits[u];
         const uint64_t any = __ballot(bits != 0u);
         if (any != 0ull) {  // wave-uniform
+          // the tile's first row, read in wave-uniform flow: a lane read
+          // inside the divergent branch below could meet a value that the
+          // compiler reloaded there for the active lanes only
+          const int row0 = __builtin_amdgcn_readlane(my_qb, g0 + u) * kBlock;
           if (bits != 0u) {
             const int at = nev + lane_rank(any);
-            s_evr[w][at] = __builtin_amdgcn_readlane(my_qb, g0 + u) * kBlock + lane;
-            s_evm[w][at] = uint8_t(bits);
+            s_evr[w][at] = row0 + lane;
+            s_evm[w][at] = Bits(bits);
           }
           nev += __builtin_popcountll(any);
-          if (nev > kEvents - kWave) list_events();  // room for the next tile's events
         }
       }
-      for (int u = 0; u < kTileGroup; ++u) word[u] = next[u];
+      if (nev > kEvents - kTileGroup * kWave) list_events();  // room for the next group's events
     }
   }
   list_events();
   drain_lists();
 
   if (jok) {
-    for (int x = 0; x < E; ++x) {
+    for (int x = 0; x < EL; ++x) {
       const float vk = p.d.scale * dk[x];
       dk[x] = finite(vk) ? vk : 0.0f;
       dv[x] = finite(dv[x]) ? dv[x] : 0.0f;
     }
-    C::store(static_cast<T*>(p.dk) + krow * D + sub * E, dk);
-    C::store(static_cast<T*>(p.dv) + krow * D + sub * E, dv);
+    for (int c = 0; c < NC; ++c) {
+      float k8[E], v8[E];
+      for (int x = 0; x < E; ++x) {
+        k8[x] = dk[c * E + x];
+        v8[x] = dv[c * E + x];
+      }
+      C::store(static_cast<T*>(p.dk) + krow * D + sub * EL + c * E, k8);
+      C::store(static_cast<T*>(p.dv) + krow * D + sub * EL + c * E, v8);
+    }
   }
 }
 
