@@ -53,8 +53,8 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "ac8bd49a37dcb9bb"
-HBM_TRAFFIC = {'bounds': 1110085, 'select': 103126348, 'tau': 34745373, 'refine': 73995236, 'compact': 2743578, 'forward': 207486763, 'bwd_dq_sparse': 247608498, 'bwd_dkdv_sparse': 276780559}
+HBM_TRAFFIC_SOURCES = "3dc64fe46daddc29"
+HBM_TRAFFIC = {'bounds': 1110227, 'select': 103126821, 'tau': 34744925, 'refine': 74009584, 'compact': 2743570, 'forward': 207484590, 'bwd_dq_sparse': 242899551, 'bwd_dkdv_sparse': 281895405}
 
 
 def source_hash() -> str:
