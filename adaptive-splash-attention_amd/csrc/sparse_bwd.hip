@@ -35,6 +35,7 @@
 //              list the key, appended to the key's list in LDS in row
 //              order; phase B gathers q_i and dO_i for the listed rows:
 //              dK_j += ds q_i, dV_j += P dO_i.
+#include <climits>
 #include <type_traits>
 
 #include "asa_device.hpp"
@@ -479,6 +480,7 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   // lane for the phase A stores of lanes with nothing to list
   __shared__ int s_lists[4 * KPW * kKeyList + 4 * kWave];
   __shared__ int s_cnt[4][KPW];
+  __shared__ int s_rank[4][KPW];  // phase B: the wave's keys by list length
   using Bits = std::conditional_t<(KPW > 8), uint16_t, uint8_t>;
   __shared__ int s_evr[4][kEvents];   // events: a row listing some of the wave's keys
   __shared__ Bits s_evm[4][kEvents];  //   and its key bits (bit k <-> key jb + k)
@@ -519,18 +521,68 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   for (int x = 0; x < EL; ++x) dk[x] = dv[x] = 0.0f;
 
   const int* mylist = s_lists + (w * KPW + grp) * kKeyList;
-  // phase B: this group's listed rows, kBatch at a time in every group
-  auto drain = [&]() {
+  // chunk c of row `key` (jb + key of the block) of K or V, zero past NK
+  // (returned by value: arrays passed by reference here kept the
+  // accumulators out of registers)
+  const T* const Kh = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
+  const T* const Vh = static_cast<const T*>(p.v) + size_t(bh) * NK * D;
+  auto key_chunk = [&](const T* base, int key, int c) -> uint4 {
+    const int jj = kb * kBlock + jb + key;
+    if (jj >= NK) return uint4{0u, 0u, 0u, 0u};
+    return C::raw(base + size_t(jj) * D + sub * EL + c * E);
+  };
+  // phase B: the wave's KPW key lists, kBatch entries at a time in every
+  // lane group.  The keys pair up by list length (longest with shortest,
+  // second with second-shortest, ...): the shorter list's group, after its
+  // own rows, takes the tail of its partner's list, so that both end near
+  // the pair's mean.  Its sums for the tail reach the partner through LDS
+  // after the loop and are added to the head's (a fixed order).  The lists
+  // are heavy-tailed (a key with a large norm scores high for many rows),
+  // and with one group per list the loop ran as long as the longest.
+  auto drain = [&]() __attribute__((always_inline)) {
     const int cnt = s_cnt[w][grp];
-    const int nmax = groups_max<LPR>(cnt);
+    int rank = 0;  // by list length, descending; ties by key
+    for (int k = 0; k < KPW; ++k) {
+      const int ck = s_cnt[w][k];
+      rank += (ck > cnt || (ck == cnt && k < grp)) ? 1 : 0;
+    }
+    if (sub == 0) s_rank[w][rank] = grp;
+    const bool big = rank < KPW / 2;
+    const int partner = s_rank[w][KPW - 1 - rank];
+    const int pcnt = s_cnt[w][partner];
+    const int cb = big ? cnt : pcnt, cs = big ? pcnt : cnt;
+    const int pcs = (cs + 1) & ~1;                         // the shorter list in whole batches
+    const int ob = min(cb, ((cb + pcs + 2) / 4) * 2);      // the longer list's head: even, about half
+    const int hb = cb - ob;                                // its tail, summed by the shorter's group
+    const int tail_at = big || hb == 0 ? INT_MAX : pcs;   // step where this group turns to the tail
+    const int nmax = groups_max<LPR>(big ? ob : pcs + hb);
+    const int* lst = mylist;
+    int lim = big ? ob : cs;  // entries below this step position are valid
+    int off = 0;              // list index = step position - off
+    float sk[EL], sv[EL];     // this group's own sums while it sums the tail
+    for (int x = 0; x < EL; ++x) sk[x] = sv[x] = 0.0f;
     for (int q = 0; q < nmax; q += kBatch) {
+      if (q == tail_at) {  // lane-group uniform
+        for (int x = 0; x < EL; ++x) {
+          sk[x] = dk[x];
+          sv[x] = dv[x];
+          dk[x] = dv[x] = 0.0f;
+        }
+        for (int c = 0; c < NC; ++c) {
+          kv[c] = key_chunk(Kh, partner, c);
+          vv[c] = key_chunk(Vh, partner, c);
+        }
+        lst = s_lists + (w * KPW + partner) * kKeyList;
+        off = pcs - ob;
+        lim = pcs + hb;
+      }
       int r[kBatch];
       bool val[kBatch];
       uint4 qraw[kBatch][NC], graw[kBatch][NC];
       RowRec rc[kBatch];
       for (int u = 0; u < kBatch; ++u) {
-        val[u] = q + u < cnt;
-        r[u] = val[u] ? mylist[q + u] : 0;
+        val[u] = q + u < lim;
+        r[u] = val[u] ? lst[q + u - off] : 0;
       }
       for (int u = 0; u < kBatch; ++u) {
         for (int c = 0; c < NC; ++c) {
@@ -572,6 +624,35 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
         }
       }
     }
+    // The tails' sums, through the wave's (now read) list region: slot
+    // rank of the longer list, LPR lanes x 2 EL floats (at most 8 d bytes
+    // per pair; the region holds KPW * kKeyList ints >= (KPW / 2) * 2 d).
+    float4* slots = reinterpret_cast<float4*>(s_lists + w * KPW * kKeyList);
+    constexpr int F4 = 2 * EL / 4;  // float4s per lane
+    static_assert(KPW * kKeyList >= (KPW / 2) * LPR * 2 * EL, "tail slots must fit the list region");
+    if (tail_at != INT_MAX) {  // the shorter list's group: hand over, take its own sums back
+      float4* sl = slots + ((KPW - 1 - rank) * LPR + sub) * F4;
+      for (int x = 0; x < EL; x += 4) {
+        sl[x / 4] = float4{dk[x], dk[x + 1], dk[x + 2], dk[x + 3]};
+        sl[EL / 4 + x / 4] = float4{dv[x], dv[x + 1], dv[x + 2], dv[x + 3]};
+      }
+      for (int x = 0; x < EL; ++x) {
+        dk[x] = sk[x];
+        dv[x] = sv[x];
+      }
+      for (int c = 0; c < NC; ++c) {
+        kv[c] = key_chunk(Kh, grp, c);
+        vv[c] = key_chunk(Vh, grp, c);
+      }
+    }
+    if (big && hb > 0) {  // the longer list's group: add its tail's sums
+      const float4* sl = slots + (rank * LPR + sub) * F4;
+      for (int x = 0; x < EL; x += 4) {
+        const float4 a4 = sl[x / 4], b4 = sl[EL / 4 + x / 4];
+        dk[x] += a4.x; dk[x + 1] += a4.y; dk[x + 2] += a4.z; dk[x + 3] += a4.w;
+        dv[x] += b4.x; dv[x + 1] += b4.y; dv[x + 2] += b4.z; dv[x + 3] += b4.w;
+      }
+    }
   };
 
   // phase A over the key block's query tiles (ascending query blocks).
@@ -589,7 +670,7 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   // s_cnt.
   int cnt[KPW];
   for (int k = 0; k < KPW; ++k) cnt[k] = 0;
-  auto drain_lists = [&]() {
+  auto drain_lists = [&]() __attribute__((always_inline)) {
     for (int k = 0; k < KPW; ++k)
       if (lane == k) s_cnt[w][k] = cnt[k];
     drain();
@@ -597,7 +678,7 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   };
   const int dump = 4 * KPW * kKeyList + w * kWave + lane;
   int nev = 0;  // events held (wave-uniform), at most kEvents
-  auto list_events = [&]() {
+  auto list_events = [&]() __attribute__((always_inline)) {
     for (int c0 = 0; c0 < nev; c0 += kWave) {
       const bool live = c0 + lane < nev;
       const int row = live ? s_evr[w][c0 + lane] : 0;
