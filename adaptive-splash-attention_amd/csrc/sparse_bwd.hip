@@ -150,6 +150,12 @@ __device__ __forceinline__ float group_lanes_sum(float v) {
   return v;
 }
 
+// Lane i <- lane 4 (i / 4) + J: word J of a quad to all its lanes.
+template <int J>
+__device__ __forceinline__ float quad_bcast(float v) {
+  return __uint_as_float(dpp_mov<J | (J << 2) | (J << 4) | (J << 6)>(__float_as_uint(v)));
+}
+
 // Maximum of a lane-group-uniform value over the wave's groups of G lanes.
 template <int G>
 __device__ __forceinline__ int groups_max(int v) {
@@ -481,14 +487,38 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   __shared__ int s_lists[4 * KPW * kKeyList + 4 * kWave];
   __shared__ int s_cnt[4][KPW];
   __shared__ int s_rank[4][KPW];  // phase B: the wave's keys by list length
+  // phase B: the own sums of the shorter lists' groups while they sum
+  // their partners' tails, [wave][pair][lane of the group][dK, dV]
+  __shared__ float4 s_save[4][KPW / 2][LPR][2 * EL / 4];
   using Bits = std::conditional_t<(KPW > 8), uint16_t, uint8_t>;
   __shared__ int s_evr[4][kEvents];   // events: a row listing some of the wave's keys
   __shared__ Bits s_evm[4][kEvents];  //   and its key bits (bit k <-> key jb + k)
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: w, jb and b0 in scalar registers
-  const int task = xcd_task(blockIdx.x, nKB * SLICES * p.d.BH);
-  const int slice = task % SLICES, kb = (task / SLICES) % nKB, bh = task / (SLICES * nKB);
+  // Block order: the XCD's heads (contiguous, as xcd_task deals them) go
+  // in pairs, and within a pair key block by key block, so the heavy first
+  // key blocks of both heads start first (under the causal mask key block
+  // kb is listed by the rows of every query block >= kb: the first blocks
+  // carry several times the mean work) while two heads' rows share the L2.
+  int slice, kb, bh;
+  {
+    const int BH = p.d.BH;
+    if (BH % kXcds == 0) {
+      const int x = blockIdx.x % kXcds, jj = blockIdx.x / kXcds, hpx = BH / kXcds;
+      const int hg = hpx % 2 == 0 ? 2 : 1;  // heads per group
+      const int per = hg * nKB * SLICES;    // blocks per group
+      const int r = jj % per, rr = r % (hg * SLICES);
+      kb = r / (hg * SLICES);
+      bh = x * hpx + (jj / per) * hg + rr / SLICES;
+      slice = rr % SLICES;
+    } else {
+      const int task = xcd_task(blockIdx.x, nKB * SLICES * BH);
+      slice = task % SLICES;
+      kb = (task / SLICES) % nKB;
+      bh = task / (SLICES * nKB);
+    }
+  }
   const int sub = lane % LPR, grp = lane / LPR;
   const int jb = slice * KPB + w * KPW;  // first key (within the block) of this wave
   const int j = kb * kBlock + jb + grp;  // this group's key
@@ -559,15 +589,14 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
     const int* lst = mylist;
     int lim = big ? ob : cs;  // entries below this step position are valid
     int off = 0;              // list index = step position - off
-    float sk[EL], sv[EL];     // this group's own sums while it sums the tail
-    for (int x = 0; x < EL; ++x) sk[x] = sv[x] = 0.0f;
     for (int q = 0; q < nmax; q += kBatch) {
       if (q == tail_at) {  // lane-group uniform
-        for (int x = 0; x < EL; ++x) {
-          sk[x] = dk[x];
-          sv[x] = dv[x];
-          dk[x] = dv[x] = 0.0f;
+        float4* sv4 = s_save[w][KPW - 1 - rank][sub];
+        for (int x = 0; x < EL; x += 4) {
+          sv4[x / 4] = float4{dk[x], dk[x + 1], dk[x + 2], dk[x + 3]};
+          sv4[EL / 4 + x / 4] = float4{dv[x], dv[x + 1], dv[x + 2], dv[x + 3]};
         }
+        for (int x = 0; x < EL; ++x) dk[x] = dv[x] = 0.0f;
         for (int c = 0; c < NC; ++c) {
           kv[c] = key_chunk(Kh, partner, c);
           vv[c] = key_chunk(Vh, partner, c);
@@ -579,7 +608,8 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
       int r[kBatch];
       bool val[kBatch];
       uint4 qraw[kBatch][NC], graw[kBatch][NC];
-      RowRec rc[kBatch];
+      float rw[kBatch];  // word sub % 4 of the row's record (a 4-byte load: a
+                         // 16-byte one per lane costs the address unit 4x)
       for (int u = 0; u < kBatch; ++u) {
         val[u] = q + u < lim;
         r[u] = val[u] ? lst[q + u - off] : 0;
@@ -589,7 +619,7 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
           qraw[u][c] = C::raw(Qb + size_t(r[u]) * D + sub * EL + c * E);
           graw[u][c] = C::raw(dOb + size_t(r[u]) * D + sub * EL + c * E);
         }
-        rc[u] = rec[r[u]];
+        rw[u] = reinterpret_cast<const float*>(rec + r[u])[sub & 3];
       }
       for (int u = 0; u < kBatch; ++u) {
         float s = 0.0f, dp = 0.0f;
@@ -599,6 +629,9 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
         }
         s = group_lanes_sum<LPR>(s);
         dp = group_lanes_sum<LPR>(dp);
+        // the record's words to every lane of each quad (DPP broadcasts)
+        const RowRec rc{quad_bcast<0>(rw[u]), quad_bcast<1>(rw[u]), quad_bcast<2>(rw[u]),
+                        quad_bcast<3>(rw[u])};
         if (val[u]) {
           float qr[EL], gr[EL];
           for (int c = 0; c < NC; ++c) {
@@ -609,13 +642,13 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
             for (int x = 0; x < E; ++x) gr[c * E + x] = x8[x];
           }
           // ClippedU of a valid row (the lists hold valid rows only)
-          const float lo = fmaxf(fmaf(-10.f, am1, rc[u].nt), 0.f);
-          const float hi = fmaxf(fmaf(10.f, am1, rc[u].nt), 0.f);
-          const float v = __builtin_amdgcn_fmed3f(fmaf(cu, s, rc[u].nt), lo, hi);
-          const float pn = pow_clipped<PP>(v, a) * rc[u].invn;
+          const float lo = fmaxf(fmaf(-10.f, am1, rc.nt), 0.f);
+          const float hi = fmaxf(fmaf(10.f, am1, rc.nt), 0.f);
+          const float v = __builtin_amdgcn_fmed3f(fmaf(cu, s, rc.nt), lo, hi);
+          const float pn = pow_clipped<PP>(v, a) * rc.invn;
           float wv = pow_clipped<PW>(v, ew);
           if constexpr (REF) wv = v > kEps ? wv : 0.0f;  // the reference's u > EPS
-          float ds = wv * fmaf(rc[u].c, dp, rc[u].cs);
+          float ds = wv * fmaf(rc.c, dp, rc.cs);
           ds = finite(ds) ? ds : 0.0f;
           for (int x = 0; x < EL; ++x) {
             dk[x] = fmaf(ds, qr[x], dk[x]);
@@ -636,9 +669,11 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
         sl[x / 4] = float4{dk[x], dk[x + 1], dk[x + 2], dk[x + 3]};
         sl[EL / 4 + x / 4] = float4{dv[x], dv[x + 1], dv[x + 2], dv[x + 3]};
       }
-      for (int x = 0; x < EL; ++x) {
-        dk[x] = sk[x];
-        dv[x] = sv[x];
+      const float4* sv4 = s_save[w][KPW - 1 - rank][sub];
+      for (int x = 0; x < EL; x += 4) {
+        const float4 a4 = sv4[x / 4], b4 = sv4[EL / 4 + x / 4];
+        dk[x] = a4.x; dk[x + 1] = a4.y; dk[x + 2] = a4.z; dk[x + 3] = a4.w;
+        dv[x] = b4.x; dv[x + 1] = b4.y; dv[x + 2] = b4.z; dv[x + 3] = b4.w;
       }
       for (int c = 0; c < NC; ++c) {
         kv[c] = key_chunk(Kh, grp, c);
