@@ -272,6 +272,27 @@ __device__ __forceinline__ int xcd_task(int i, int total) {
   return x * base + (x < rem ? x : rem) + j;
 }
 
+// Heaviest-first order across the heads an XCD serves.  Walking the XCD's
+// heads one after another (xcd_task) starts the heavy blocks of its last
+// heads near the end, and they set the launch's tail (under the causal
+// mask a head's blocks differ several-fold in work).  Here an XCD still
+// serves a contiguous range of heads, but its blocks go by weight rank
+// (rank 0, the heaviest block of each head, first), heads innermost:
+// forward 237 -> 186 us at the headline shape.  Needs BH % 8 == 0, else
+// xcd_task's order.  `nblk` blocks per head; returns the block's weight
+// rank and its head.
+__device__ __forceinline__ void xcd_rank_order(int i, int nblk, int BH, int& rank, int& bh) {
+  if (BH % kXcds == 0) {
+    const int x = i % kXcds, jj = i / kXcds, hpx = BH / kXcds;
+    rank = jj / hpx;
+    bh = x * hpx + jj % hpx;
+  } else {
+    const int task = xcd_task(i, nblk * BH);
+    rank = task % nblk;
+    bh = task / nblk;
+  }
+}
+
 // Transposing LDS read (ds_read_b64_tr_b16): in each 16-lane group, lane l
 // supplies the address of 4 consecutive bf16 values; lane i receives value
 // i % 4 of the rows supplied by lanes 4m + i / 4, m = 0..3.

@@ -230,6 +230,55 @@ __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const T* rm,
       for (int db = 0; db < D / 16; ++db) o[db] = mfma(a[db], bl, o[db]);
   }
 }
+// rows_x_frag for two B fragments at once: each A operand is read from LDS
+// once and feeds both products (the same operands and order per product as
+// rows_x_frag, so each result is bit-identical to it).
+template <int D, typename T, typename std::enable_if<is_half<T>, int>::type = 0>
+__device__ __forceinline__ void rows_x_frag2(f32x4 (&acc0)[4], f32x4 (&acc1)[4], const T* rm,
+                                             const RowFrag<T, D>& b0, const RowFrag<T, D>& b1,
+                                             int lane) {
+  using V8 = typename Half<T>::v8;
+  const int g = lane >> 4, c = lane & 15;
+  const T* base = rm + c * Tile<T, D>::kRs + ((8 * g) ^ Tile<T, D>::sw(c));
+  for (int f = 0; f < 4; ++f) acc0[f] = acc1[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < D / 32; ++s)
+    for (int f = 0; f < 4; ++f) {
+      const V8 a = *reinterpret_cast<const V8*>(base + 16 * f * Tile<T, D>::kRs + 32 * s);
+      acc0[f] = mfma(a, b0.v[s], acc0[f]);
+      acc1[f] = mfma(a, b1.v[s], acc1[f]);
+    }
+}
+
+// tile_t_x_acc (no Split) for two X / accumulator pairs at once: each
+// transposed A read feeds both products (per product, the operands and
+// order of tile_t_x_acc).
+template <int D, typename T, typename std::enable_if<is_half<T>, int>::type = 0>
+__device__ __forceinline__ void tile_t_x_acc2(f32x4 (&o0)[D / 16], f32x4 (&o1)[D / 16], const T* rm,
+                                              const f32x4 (&x0)[4], const f32x4 (&x1)[4], int lane) {
+  using H = Half<T>;
+  using V8 = typename H::v8;
+  using V4 = typename H::v4;
+  using S = typename H::scalar;
+  const int g = lane >> 4, l = lane & 15;
+  constexpr int rs = Tile<T, D>::kRs;
+  for (int cc = 0; cc < 2; ++cc) {
+    V8 b0, b1;
+    for (int h = 0; h < 2; ++h)
+      for (int r = 0; r < 4; ++r) {
+        b0[4 * h + r] = static_cast<S>(x0[2 * cc + h][r]);
+        b1[4 * h + r] = static_cast<S>(x1[2 * cc + h][r]);
+      }
+    const T* base = rm + (32 * cc + 4 * g + (l >> 2)) * rs + ((4 * (l & 3)) ^ Tile<T, D>::sw(4 * g));
+    for (int db = 0; db < D / 16; ++db) {
+      const V4 lo = read_tr16(base + 16 * db);
+      const V4 hi = read_tr16(base + 16 * rs + 16 * db);
+      const V8 a = V8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o0[db] = mfma(a, b0, o0[db]);
+      o1[db] = mfma(a, b1, o1[db]);
+    }
+  }
+}
+
 // fp32: `rm` is the row-major tile (exact operands; Split has no effect).
 template <int D, bool Split = false, int CC0 = 0, int CC1 = 2>
 __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const float* rm,

@@ -91,8 +91,9 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
-  const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
-  const int qb = nQB - 1 - task % nQB, bh = task / nQB;
+  int brank, bh;
+  xcd_rank_order(blockIdx.x, nQB, p.d.BH, brank, bh);
+  const int qb = nQB - 1 - brank;  // heaviest first
   const int q = qb * kBlock + 16 * w + c16;
   const bool qok = q < NQ;
   const size_t rows = size_t(p.d.BH) * NQ;
@@ -282,8 +283,8 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dkdv_ke
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
-  const int task = xcd_task(blockIdx.x, nKB * p.d.BH);
-  const int kb = task % nKB, bh = task / nKB;
+  int kb, bh;
+  xcd_rank_order(blockIdx.x, nKB, p.d.BH, kb, bh);  // ascending key blocks: heaviest first
   const int j = kb * kBlock + 16 * w + c16;  // this lane's key row
   const bool jok = j < NK;
   const size_t krow = size_t(bh) * NK + (jok ? j : 0);

@@ -153,8 +153,9 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
 
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
-  const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
-  const int qb = nQB - 1 - task % nQB, bh = task / nQB;
+  int brank, bh;
+  xcd_rank_order(blockIdx.x, nQB, p.d.BH, brank, bh);
+  const int qb = nQB - 1 - brank;  // heaviest first
   const int q = qb * kBlock + 16 * w + c16;
   const bool rowok = q < NQ;
   const size_t rows = size_t(p.d.BH) * NQ;

@@ -40,8 +40,9 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int g = lane >> 4, c16 = lane & 15;
-  const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
-  const int qb = nQB - 1 - task % nQB, bh = task / nQB;
+  int brank, bh;
+  xcd_rank_order(blockIdx.x, nQB, p.d.BH, brank, bh);
+  const int qb = nQB - 1 - brank;  // heaviest first
   const int q = qb * kBlock + 16 * w + c16;  // this lane's query row
   const bool qok = q < NQ;
   const size_t row = size_t(bh) * NQ + (qok ? q : 0);
@@ -179,8 +180,206 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   }
 }
 
+// Two query blocks per workgroup (16-bit inputs): wave w holds rows
+// 16w..16w+15 of both query blocks 2m and 2m+1, as two B fragments, and the
+// workgroup walks the union of the two blocks' key-block lists (merged on
+// the fly from the CSR).  Each K and V tile read from LDS then feeds two
+// fragments' products (rows_x_frag2, tile_t_x_acc2): half the LDS reads
+// per row of the one-block kernel, whose waves were half-bound by them.  A
+// tile in one block's list only runs that block's half.  Per block and
+// tile the arithmetic, its order and the masks written are those of
+// forward_kernel, so the results are bit-identical to it.
+template <typename T, int D, int PC, bool EMIT, bool HALF>
+__global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams p) {
+  static_assert(is_half<T>, "16-bit inputs only");
+  __shared__ FwdSmem<T, D> sm;
+  using St = Stager<T, D>;
+  const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int nP = (nQB + 1) / 2;
+  int brank, bh;
+  xcd_rank_order(blockIdx.x, nP, p.d.BH, brank, bh);
+  const int qp2 = nP - 1 - brank;  // heaviest first
+
+  const T* Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
+  const T* Vb = static_cast<const T*>(p.v) + size_t(bh) * NK * D;
+  const int32_t* kidx = p.k_idx + size_t(bh) * NK;
+  const int2* kbnd = p.kbounds + size_t(bh) * nKB;
+  const float am1 = p.d.alpha - 1.0f;
+  const float a = 1.0f / am1;
+  const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
+  const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
+
+  // per block h of the pair: rows, fragments, clipping, list, masks
+  int qb[2], qpos[2], qmin[2], lb[2], le[2];
+  bool qok[2], hvalid[2];
+  size_t row[2];
+  RowFrag<T, D> qf[2];
+  SignedClip clip[2] = {SignedClip(am1, 0.0f, 0.0f, false), SignedClip(am1, 0.0f, 0.0f, false)};
+  float pscale[2] = {1.0f, 1.0f}, rowsum[2] = {0.0f, 0.0f};
+  const uint8_t* hrow[2] = {nullptr, nullptr};
+  uint16_t* smask = nullptr;
+  if constexpr (EMIT) smask = p.sup.mask + size_t(bh) * nQB * nKB * 256 + w * 64 + 4 * c16 + g;
+  for (int h = 0; h < 2; ++h) {
+    qb[h] = 2 * qp2 + h;
+    const bool bok = qb[h] < nQB;  // block-uniform
+    const int q = qb[h] * kBlock + 16 * w + c16;
+    qok[h] = bok && q < NQ;
+    row[h] = size_t(bh) * NQ + (qok[h] ? q : 0);
+    qf[h].load(static_cast<const T*>(p.q) + row[h] * D, qok[h], lane);
+    qpos[h] = qok[h] ? p.q_idx[row[h]] : 0;
+    clip[h] = SignedClip(am1, p.d.scale, qok[h] ? p.taus[row[h]] : 0.0f, qok[h]);
+    if constexpr (std::is_same<T, h16>::value) {
+      // fp16 P operands scaled by 2^-e, e the exponent of the row's
+      // largest weight (as in forward_kernel)
+      if (qok[h]) {
+        const float s1 = p.top1[row[h]];
+        const float u1 = fmaxf(fminf(fmaf(am1, s1, -p.taus[row[h]]), fmaf(10.0f, am1, -p.taus[row[h]])), 0.0f);
+        const float p1 = pow_clipped<PC>(u1, a);
+        int e = 0;
+        (void)frexpf(p1, &e);
+        pscale[h] = p1 > 0.0f ? (finite(p1) ? ldexpf(1.0f, -e) : 0.0f) : 1.0f;
+      }
+    }
+    {
+      const int qq = qb[h] * kBlock + lane;
+      qmin[h] = wave_reduce_minmax<false>(bok && qq < NQ ? p.q_idx[size_t(bh) * NQ + qq] : INT32_MAX);
+    }
+    lb[h] = bok ? qp[qb[h]] : 0;
+    le[h] = bok ? qp[qb[h] + 1] : 0;
+    hvalid[h] = bok;
+    if constexpr (HALF) {
+      const int hh = 2 * qb[h] + (w >> 1), nQH = half_blocks(NQ);
+      hvalid[h] = bok && hh < nQH;
+      hrow[h] = p.half + (size_t(bh) * nQH + (hvalid[h] ? hh : 0)) * nKB;
+    }
+  }
+
+  f32x4 o[2][D / 16];
+  for (int h = 0; h < 2; ++h)
+    for (int db = 0; db < D / 16; ++db) o[h][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // The merged list: entry = key block | bit 30 (in block 0's list) | bit
+  // 31 (in block 1's), or -1 past the end.  Two cursors run ahead of the
+  // tile being multiplied (its successor is in LDS, the next one loading).
+  int c0 = lb[0], c1 = lb[1];
+  auto advance = [&]() -> int {
+    const int k0 = c0 < le[0] ? ql[c0] : INT32_MAX;
+    const int k1 = c1 < le[1] ? ql[c1] : INT32_MAX;
+    const int kb = min(k0, k1);
+    if (kb == INT32_MAX) return -1;
+    const bool a0 = k0 == kb, a1 = k1 == kb;
+    c0 += a0 ? 1 : 0;
+    c1 += a1 ? 1 : 0;
+    return kb | (a0 ? 1 << 30 : 0) | (a1 ? int(1u << 31) : 0);
+  };
+  St st;
+  PosStager ps;
+  auto fetch = [&](int ent) {
+    const int kbase = (ent & 0x3fffffff) * kBlock;
+    st.load(Kb, Vb, kbase, NK, t);
+    ps.load(kidx, kbase, NK, INT32_MAX, t);
+  };
+  auto put = [&](int b) {
+    st.store(sm.K[b], sm.V[b], t);
+    ps.store(sm.kid[b], t);
+  };
+  int cur = advance(), nxt = -1;
+  if (cur != -1) {
+    fetch(cur);
+    put(0);
+    nxt = advance();
+    if (nxt != -1) fetch(nxt);
+  }
+  __syncthreads();
+  int e[2] = {lb[0], lb[1]};  // list positions of the blocks' current tiles (their mask slots)
+  for (int i = 0; cur != -1; ++i) {
+    const int b = i & 1;
+    const int kb = cur & 0x3fffffff;
+    bool in[2] = {(cur & (1 << 30)) != 0, cur < 0};
+    bool act[2];
+    for (int h = 0; h < 2; ++h) {
+      act[h] = in[h];  // wave-uniform
+      if constexpr (HALF) act[h] = in[h] && hvalid[h] && hrow[h][kb] != 0;
+    }
+    f32x4 acc[2][4];
+    if (act[0] && act[1]) rows_x_frag2<D>(acc[0], acc[1], sm.K[b], qf[0], qf[1], lane);
+    else if (act[0]) rows_x_frag<D>(acc[0], sm.K[b], qf[0], lane);
+    else if (act[1]) rows_x_frag<D>(acc[1], sm.K[b], qf[1], lane);
+    // forward_kernel's weights, per block
+    auto weights = [&](int h, auto partial) {
+      uint32_t nm = 0;  // bit 4f + r <- u <= 0, highest bit first
+      for (int f = 3; f >= 0; --f)
+        for (int r = 3; r >= 0; --r) {
+          float v = clip[h](acc[h][f][r]);  // max(u, 0)
+          if constexpr (decltype(partial)::value)
+            v = sm.kid[b][16 * f + 4 * g + r] <= qpos[h] ? v : -0.0f;
+          acc[h][f][r] = v;
+          if constexpr (EMIT) nm = __builtin_amdgcn_alignbit(nm, __float_as_uint(v), 31);
+        }
+      if constexpr (EMIT) smask[size_t(e[h]) * 256] = uint16_t(~nm);
+      for (int f = 0; f < 4; ++f)
+        for (int r = 0; r < 4; ++r) {
+          const float pv = pow_clipped<PC>(acc[h][f][r], a);
+          if constexpr (std::is_same<T, h16>::value) acc[h][f][r] = pv * pscale[h];
+          else acc[h][f][r] = pv;
+          rowsum[h] += pv;
+        }
+    };
+    const bool whole_keys = kb * kBlock + kBlock <= NK;
+    for (int h = 0; h < 2; ++h) {
+      if (act[h]) {
+        if (whole_keys && kbnd[kb].y <= qmin[h]) weights(h, std::false_type{});
+        else weights(h, std::true_type{});
+      } else if constexpr (EMIT) {
+        if (in[h]) smask[size_t(e[h]) * 256] = 0;
+      }
+    }
+    if (act[0] && act[1]) tile_t_x_acc2<D>(o[0], o[1], sm.V[b], acc[0], acc[1], lane);
+    else if (act[0]) tile_t_x_acc<D>(o[0], sm.V[b], acc[0], lane);
+    else if (act[1]) tile_t_x_acc<D>(o[1], sm.V[b], acc[1], lane);
+    for (int h = 0; h < 2; ++h) e[h] += in[h] ? 1 : 0;
+    cur = nxt;
+    if (cur != -1) {
+      put(b ^ 1);
+      nxt = advance();
+      if (nxt != -1) fetch(nxt);
+    }
+    __syncthreads();
+  }
+
+  for (int h = 0; h < 2; ++h) {
+    const float norm = sum_groups(rowsum[h]);
+    const float inv = 1.0f / ((norm + kEps) * pscale[h]);  // pscale 0: non-finite weights, output 0
+    if (qok[h]) {
+      T* orow = static_cast<T*>(p.out) + row[h] * D;
+      for (int db = 0; db < D / 16; ++db)
+        for (int r = 0; r < 4; ++r) {
+          float v = o[h][db][r] * inv;
+          if (!finite(v)) v = 0.0f;
+          Elem<T>::store(orow + 16 * db + 4 * g + r, v);
+        }
+      if (g == 0) p.norms[row[h]] = norm;
+    }
+  }
+}
+
+template <typename T, int D, bool EMIT, bool HALF>
+hipError_t launch_pair(const ForwardParams& p, hipStream_t s) {
+  dim3 grid(((p.d.nQB + 1) / 2) * p.d.BH);
+  switch (alpha_class_of(p.d.alpha)) {
+    case kA15: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE2, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
+    case kA20: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE1, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
+    case kA125: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE4, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL((forward_pair_kernel<T, D, kEGen, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
+  }
+  return hipGetLastError();
+}
+
 template <typename T, int D, bool EMIT, bool HALF>
 hipError_t launch_tde(const ForwardParams& p, hipStream_t s) {
+  if constexpr (is_half<T> && D == 64) return launch_pair<T, D, EMIT, HALF>(p, s);
   dim3 grid(p.d.nQB * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
     case kA15: hipLaunchKernelGGL((forward_kernel<T, D, kE2, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;

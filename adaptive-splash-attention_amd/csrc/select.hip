@@ -423,8 +423,9 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
   const int t = threadIdx.x, w = t >> 6, L = t & 63, g = L >> 4, c = L & 15;
   float* s_scr = reinterpret_cast<float*>(smem + lay.scr) + t * kScrStride;  // this lane's
   const int scr_sw = ((L >> 1) & 3) << 2;  // chunk swizzle, in floats
-  const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
-  const int qb = nQB - 1 - task % nQB, bh = task / nQB, q0 = qb * kBlock;
+  int brank, bh;
+  xcd_rank_order(blockIdx.x, nQB, p.d.BH, brank, bh);
+  const int qb = nQB - 1 - brank, q0 = qb * kBlock;  // heaviest first
   const size_t grow0 = size_t(bh) * NQ + q0;  // global index of the block's row 0
   const float scale = p.d.scale;
 
@@ -636,31 +637,33 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
     for (int cb = 0; cb < 4; ++cb) {
       fl[cb] = s_fl[16 * cb + c];
       if (fl[cb] == 0.0f) fl[cb] = -0.0f;
-      if (!__builtin_isnan(fl[cb])) cmask |= 0xfu << (4 * cb);
-      if (fl[cb] == -__builtin_inff()) amask |= 0xfu << (4 * cb);
+      if (!__builtin_isnan(fl[cb])) cmask |= 0xfu << (12 - 4 * cb);  // bit order of collect's m
+      if (fl[cb] == -__builtin_inff()) amask |= 0xfu << (12 - 4 * cb);
     }
     // Candidates are stored raw, (index << 32) | bits of the sweep value,
     // and turned into selection keys when they are sorted.  Per tile, the
-    // lane's candidate bits m (bit 4 cb + r: key kb0 + r of row 16 cb + c)
-    // come branch-free, two instructions per score; the few lanes with
+    // lane's candidate bits m (bit 15 - (4 cb + r): key kb0 + r of row
+    // 16 cb + c) come branch-free, two instructions per score, in the order
+    // the MFMA results arrive (cb = 0 first); the few lanes with
     // candidates then park their 16 values in their LDS scratch and append
     // one candidate per round (LDS atomic on the row's count), so the wave
     // runs as many rounds as its busiest lane has candidates (about two at
     // the headline shape) instead of visiting every slot.
     auto collect = [&](int kb0, auto partial, uint32_t visb, f32x4 (&acc)[4], auto later) {
-      // bit 4 cb + r <- sign of v - fl: set where v < fl, so that the
-      // complement marks !(v < fl) (NaN differences have a clear sign bit)
+      // bit 15 - (4 cb + r) <- sign of v - fl: set where v < fl, so that
+      // the complement marks !(v < fl) (NaN differences have a clear sign
+      // bit)
       uint32_t m = 0;
-      for (int cb = 3; cb >= 0; --cb)
-        for (int r = 3; r >= 0; --r)
+      for (int cb = 0; cb < 4; ++cb)
+        for (int r = 0; r < 4; ++r)
           m = __builtin_amdgcn_alignbit(m, __float_as_uint(acc[cb][r] - fl[cb]), 31);
       m = (~m | amask) & cmask;
-      if constexpr (decltype(partial)::value) m &= visb;
+      if constexpr (decltype(partial)::value) m &= __builtin_bitreverse32(visb) >> 16;
       if (m != 0u) {
         for (int cb = 0; cb < 4; ++cb) *reinterpret_cast<f32x4*>(s_scr + ((4 * cb) ^ scr_sw)) = acc[cb];
       }
       while (m != 0u) {
-        const int b = __builtin_ctz(m);
+        const int b = 15 - __builtin_ctz(m);  // 4 cb + r
         m &= m - 1u;
         const int row = 4 * (b & 12) + c, key = kb0 + (b & 3);
         const float v = s_scr[b ^ scr_sw];
