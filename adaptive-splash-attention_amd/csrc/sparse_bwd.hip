@@ -178,7 +178,10 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
   __shared__ int s_rn[4][16];                // listed keys per row of the wave
   __shared__ int s_off[4][16];               // start of each row's list in s_flat
   __shared__ int s_rank[4][16];              // rows in descending count order
-  __shared__ float s_cfac[4][16];            // entmax mode: (norm + eps)^(alpha - 2) per row
+  __shared__ float s_cfac[4][16];            // per row: c ((norm + eps)^(alpha - 2), or delta's)
+  __shared__ float s_shift[4][16];           //   the reference mode's shift (delta)
+  __shared__ float s_norm[4][16];            //   sum p
+  __shared__ float s_tau[4][16];             //   tau
   __shared__ int s_list[4][RPR][kRowList];   // chunked path
   __shared__ uint64_t s_mw[4][kChunk][16];   // mask words of a chunk of tiles: [tile][row]
   __shared__ int s_kb[4][kChunk];            // first key of each tile
@@ -211,20 +214,28 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
     return wv;
   };
 
-  // The rows' (norm + eps)^(alpha - 2), one lane per row of the wave: the
-  // double pow runs once per wave instead of once per lane group and row
-  // (the groups finish their rows at different steps, so per-row calls
-  // would run one after another).
-  if constexpr (!REF) {
-    if (lane < 16) {
-      const int qrow = qb * kBlock + 16 * w + lane;
-      float c = 0.0f;
-      if (qrow < NQ) {
-        const float norm = p.norms[size_t(bh) * NQ + qrow];
-        c = static_cast<float>(pow(static_cast<double>(norm + kEps), static_cast<double>(alpha) - 2.0));
+  // The rows' constants, one lane per row of the wave, into LDS: the lane
+  // groups start and finish their rows at different steps, so per-row
+  // loads (and the double pow of (norm + eps)^(alpha - 2)) would run one
+  // after another, each a full memory latency.
+  if (lane < 16) {
+    const int qrow = qb * kBlock + 16 * w + lane;
+    float c = 0.0f, sh = 0.0f, nrm = 0.0f, ta = 0.0f;
+    if (qrow < NQ) {
+      const size_t rw = size_t(bh) * NQ + qrow;
+      nrm = p.norms[rw];
+      ta = p.taus[rw];
+      if constexpr (REF) {
+        c = p.delta[rows + rw];
+        sh = p.delta[rw];
+      } else {
+        c = static_cast<float>(pow(static_cast<double>(nrm + kEps), static_cast<double>(alpha) - 2.0));
       }
-      s_cfac[w][lane] = c;
     }
+    s_cfac[w][lane] = c;
+    s_shift[w][lane] = sh;
+    s_norm[w][lane] = nrm;
+    s_tau[w][lane] = ta;
   }
 
   // One row's state: its q and dO chunks, clipping, and the fp32 sums
@@ -233,21 +244,29 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
   bool ok = false;
   size_t row = 0;
   uint4 qv{0u, 0u, 0u, 0u}, dO{0u, 0u, 0u, 0u};
+  uint4 nqv{0u, 0u, 0u, 0u}, ndO{0u, 0u, 0u, 0u};  // the next row's, loaded ahead
   ClippedU clip(am1, scale, 0.0f, false);
   float a1[E], a2[E];
   float sw = 0.0f, swdp = 0.0f;
-  auto start_row = [&](int r) {
+  // q and dO chunks of row r of the wave, for a later start_row(r)
+  auto prefetch = [&](int r) {
+    const int qrow = qb * kBlock + 16 * w + r;
+    nqv = uint4{0u, 0u, 0u, 0u};
+    ndO = uint4{0u, 0u, 0u, 0u};
+    if (qrow < NQ) {
+      const size_t rw = size_t(bh) * NQ + qrow;
+      nqv = C::raw(static_cast<const T*>(p.q) + rw * D + sub * E);
+      ndO = C::raw(static_cast<const T*>(p.dout) + rw * D + sub * E);
+    }
+  };
+  auto start_row = [&](int r) {  // after prefetch(r)
     rr = r;
     const int qrow = qb * kBlock + 16 * w + rr;
     ok = qrow < NQ;
     row = size_t(bh) * NQ + (ok ? qrow : 0);
-    qv = uint4{0u, 0u, 0u, 0u};
-    dO = uint4{0u, 0u, 0u, 0u};
-    if (ok) {
-      qv = C::raw(static_cast<const T*>(p.q) + row * D + sub * E);
-      dO = C::raw(static_cast<const T*>(p.dout) + row * D + sub * E);
-    }
-    clip = ClippedU(am1, scale, ok ? p.taus[row] : 0.0f, ok);
+    qv = nqv;
+    dO = ndO;
+    clip = ClippedU(am1, scale, s_tau[w][rr], ok);
     for (int x = 0; x < E; ++x) a1[x] = a2[x] = 0.0f;
     sw = swdp = 0.0f;
   };
@@ -285,11 +304,11 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
   // dQ and the row's record for the dK/dV pass
   auto finish_row = [&]() {
     if (!ok) return;
-    const float norm = p.norms[row];
+    const float norm = s_norm[w][rr];
     float cfac, shift;
     if constexpr (REF) {
-      cfac = p.delta[rows + row];
-      shift = p.delta[row];
+      cfac = s_cfac[w][rr];
+      shift = s_shift[w][rr];
     } else {
       cfac = s_cfac[w][rr];
       shift = sw > 0.0f ? swdp / sw : 0.0f;
@@ -354,6 +373,8 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
       s_off[w][lane] = off;
       s_rank[w][rank] = lane;
     }
+    // the first row's q and dO load while the lists are built
+    prefetch(s_rank[w][grp]);
     int base = off;
     auto list_words = [&](int e8, const uint64_t (&wd)[kWords], const int (&kbs)[kWords]) {
       for (int u = 0; u < kWords && e8 + 4 * u < e1; ++u) {
@@ -384,13 +405,15 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
     }
     auto rank_row = [&](int j) { return s_rank[w][j * RPR + ((j & 1) ? RPR - 1 - grp : grp)]; };
     int j = 0;
-    start_row(rank_row(0));
+    start_row(rank_row(0));  // prefetched before the listing
+    if (NR > 1) prefetch(rank_row(1));
     int pos = s_off[w][rr], end = pos + s_rn[w][rr];
     for (;;) {
       while (j < NR && pos >= end) {  // group-uniform
         finish_row();
         if (++j < NR) {
           start_row(rank_row(j));
+          if (j + 1 < NR) prefetch(rank_row(j + 1));
           pos = s_off[w][rr];
           end = pos + s_rn[w][rr];
         }
@@ -409,6 +432,7 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
   // tiles and drained in lock step
   int* list = s_list[w][grp];
   for (int r0 = 0; r0 < 16; r0 += RPR) {
+    prefetch(r0 + grp);
     start_row(r0 + grp);
     auto drain = [&](int cnt) {
       const int nmax = groups_max<LPR>(cnt);
