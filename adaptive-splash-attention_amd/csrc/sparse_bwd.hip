@@ -187,9 +187,12 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
   __shared__ int s_kb[4][kChunk];            // first key of each tile
   const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  int brank, bh;
-  xcd_rank_order(blockIdx.x, nQB, p.d.BH, brank, bh);
-  const int qb = nQB - 1 - brank;  // heaviest first
+  // head by head (xcd_task): the pass's work per block hardly depends on
+  // the query block, and two heads' K/V rows at a time stay in the L2
+  // (heaviest-first over all the XCD's heads measured the same time at
+  // twice the HBM traffic)
+  const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
+  const int qb = nQB - 1 - task % nQB, bh = task / nQB;
   const int sub = lane % LPR, grp = lane / LPR;
 
   const float alpha = p.d.alpha, am1 = alpha - 1.0f, ew = (2.0f - alpha) / am1;

@@ -53,8 +53,8 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "3dc64fe46daddc29"
-HBM_TRAFFIC = {'bounds': 1110227, 'select': 103126821, 'tau': 34744925, 'refine': 74009584, 'compact': 2743570, 'forward': 207484590, 'bwd_dq_sparse': 242899551, 'bwd_dkdv_sparse': 281895405}
+HBM_TRAFFIC_SOURCES = "308c008b4d2c8441"
+HBM_TRAFFIC = {'bounds': 1110072, 'select': 141637409, 'tau': 34745398, 'refine': 109599604, 'compact': 2743465, 'forward': 297753286, 'bwd_dq_sparse': 240817863, 'bwd_dkdv_sparse': 288165908}
 
 
 def source_hash() -> str:
@@ -144,14 +144,18 @@ def kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep, nsup):
         "bwd_dkdv": dict(bound="hbm", flops=8.0 * 64 * 64 * d * nnzb,
                          bytes=nnzb * 2 * tile + 4 * rows * d * ELEM + nnzb * 64 * 4 * 5),
         # support-mask backward: per listed pair, two gathered d-rows and
-        # 8 d FLOPs (two dot products, two accumulations); per active tile
-        # its 512 bytes of masks
+        # 8 d FLOPs (two dot products, two accumulations).  `bytes` is what
+        # must cross HBM once (the rows read and written, 512 bytes of masks
+        # per active tile, the row records); `l2_bytes` are the per-pair
+        # gathers of rows that the passes re-read from L2 (a row is listed
+        # by tens of pairs), priced as an L2 rate, not against HBM
         "bwd_dq_sparse": dict(bound="hbm", flops=8.0 * d * nsup,
-                              bytes=nsup * 2 * d * ELEM + 3 * rows * d * ELEM + nnzb * 512
-                              + rows * (8 + 32) + 4 * nnzb),
+                              bytes=5 * rows * d * ELEM + nnzb * 512 + rows * (8 + 16) + 4 * nnzb,
+                              l2_bytes=nsup * 2 * d * ELEM),
         "bwd_dkdv_sparse": dict(bound="hbm", flops=8.0 * d * nsup,
-                                bytes=nsup * (2 * d * ELEM + 32) + 4 * rows * d * ELEM
-                                + nnzb * 512 + 4 * BH * nQB * nKB),
+                                bytes=6 * rows * d * ELEM + nnzb * 512 + rows * 16
+                                + 4 * BH * nQB * nKB,
+                                l2_bytes=nsup * (2 * d * ELEM + 16)),
     }
 
 
@@ -171,6 +175,12 @@ def roofline_of(model, ms):
         # more algorithmic bytes than HBM can deliver in this time: they come
         # from L2, so the byte model is not an HBM bound for this kernel
         r["model_note"] = "algorithmic bytes above the HBM peak rate: L2-served, not an HBM bound"
+    if model.get("l2_bytes"):
+        r["l2_bytes"] = model["l2_bytes"]
+        r["l2_gather_GBps"] = round(model["l2_bytes"] / t / 1e9, 1)
+        r["model_note"] = ("HBM fraction of the bytes that must cross HBM once; the per-pair row "
+                           "gathers (l2_bytes) are L2-served, and the gather latency and the "
+                           "VALU work per pair bound the pass")
     return r
 
 
@@ -377,7 +387,8 @@ def main():
             if traffic_ok and HBM_TRAFFIC.get(name):
                 kr = kernels[name]
                 kr["hbm_frac_measured"] = round(HBM_TRAFFIC[name] / (tot / cnt / 1e3) / PEAK_HBM, 4)
-                if kr["bound"] == "hbm" and HBM_TRAFFIC[name] < 0.5 * kr["alg_bytes"]:
+                if kr["bound"] == "hbm" and HBM_TRAFFIC[name] < 0.5 * kr["alg_bytes"] \
+                        and "l2_bytes" not in kr:
                     # gathered rows that L2 serves: the byte model is an L2
                     # rate, not an HBM one
                     kr["model_note"] = (f"measured HBM traffic is "
