@@ -55,6 +55,12 @@ CASES = [
     ("fp16_small", 1, 2, 256, 256, 64, 1.5, 32, 0.125, torch.float16),
     ("fp16_d128_a125", 1, 2, 256, 256, 128, 1.25, 64, 128 ** -0.5, torch.float16),
     ("fp32_ragged", 2, 1, 100, 150, 64, 1.5, 8, 0.125, torch.float32),
+    # 16-bit, d = 64: the forward runs query blocks in pairs; a ragged last
+    # pair (197 rows: blocks 2 and 3, the second partial) and an odd block
+    # count (130 rows: the last pair has one block), with sparse masks that
+    # differ between the two blocks of a pair
+    ("bf16_ragged_pairs", 2, 1, 197, 300, 64, 1.5, 16, 0.125, torch.bfloat16),
+    ("fp16_odd_blocks", 1, 2, 130, 130, 64, 1.5, 8, 0.125, torch.float16),
     ("fp32_alpha_general", 1, 1, 128, 128, 64, 1.7, 8, 0.125, torch.float32),
 ]
 
