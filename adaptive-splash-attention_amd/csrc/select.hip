@@ -781,10 +781,14 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
       const float x = __uint_as_float(uint32_t(raw));
       return ord_of(kExact ? x : clamp_score(x * scale));
     };
-    uint32_t v[8];
+    uint32_t v[8], o8[8];  // o8: the lane's unsorted order codes, kept for the mask bits
+    int x8[8];             //     and their key indices
     for (int pp = 0; pp < 8; ++pp) {
       const int e = i * 8 + pp;
-      v[pp] = e < n ? ord_raw(s_cand[cslot(e, r)]) : 0u;  // 0: empty slot
+      const uint64_t raw = e < n ? s_cand[cslot(e, r)] : 0ull;
+      o8[pp] = e < n ? ord_raw(raw) : 0u;  // 0: empty slot
+      x8[pp] = int(raw >> 32);
+      v[pp] = o8[pp];
     }
     segment_sort_desc32<LS>(v, L);
     for (int pp = 0; pp < 8; ++pp) {
@@ -813,9 +817,8 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
     for (int pp = 0; pp < 8; ++pp) {
       const int e = i * 8 + pp;
       if (e >= n) continue;
-      const uint64_t raw = s_cand[cslot(e, r)];
-      const uint32_t o = ord_raw(raw);
-      const int idx = int(raw >> 32);
+      const uint32_t o = o8[pp];
+      const int idx = x8[pp];
       bool sel = vk == 0u || o > vk || (o == vk && !split);
       if (split && o == vk) {
         int before = 0;  // ties with a lower index
