@@ -479,12 +479,14 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
   }
   const int kq0 = 16 * w + c;  // the lane's A-operand key within a tile
 
-  // One pass over the visible key blocks: body(u, kt, partial, visb, acc)
-  // for each, u = (ordinal of the block) % U known at compile time.  The K
-  // quarters of the next two tiles are in flight while a tile is used.  In
-  // partially visible tiles (partial = true), bit 4 cb + r of visb is
-  // cleared and acc set to -inf where key 16 w + 4 g + r is not visible to
-  // row 16 cb + c.  The first 64 list entries are held one per lane.
+  // One pass over the visible key blocks: body(u, kt, visb, acc) for each,
+  // u = (ordinal of the block) % U known at compile time.  The K quarters of
+  // the next two tiles are in flight while a tile is used.  In partially
+  // visible tiles bit 15 - (4 cb + r) of visb is cleared and acc set to
+  // -inf where key 16 w + 4 g + r is not visible to row 16 cb + c (visb is
+  // 0xffff for a whole tile); the body is called once, after the masking,
+  // so its code is not repeated per case.  The first 64 list entries are
+  // held one per lane.
   const int vl0 = L < nvis ? s_vlist[L] : 0;
   auto entry = [&](int i) {
     return i < kWave ? __builtin_amdgcn_readlane(vl0, i) : __builtin_amdgcn_readfirstlane(s_vlist[i]);
@@ -533,25 +535,23 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
             for (int cb = 0; cb < 4; ++cb)
               for (int r = 0; r < 4; ++r) acc[cb][r] = clamp_score(acc[cb][r] * scale);
         }
+        uint32_t visb = 0xffffu;
         if (i >= nvis) {  // padding of the last group of U tiles: nothing visible
           for (int cb = 0; cb < 4; ++cb)
             for (int r = 0; r < 4; ++r) acc[cb][r] = -__builtin_inff();
-          body(uc, kb0, std::true_type{}, 0u, acc);
+          visb = 0u;
         } else if ((e >> 24) == 1) {  // wave-uniform
-          uint32_t visb = 0xffffu;
           for (int r = 0; r < 4; ++r) {
             const int key = kb0 + r;
             const int kp = key < NK ? kidx[key] : INT_MAX;
             for (int cb = 0; cb < 4; ++cb)
               if (!(key < NK && kp <= qpos[cb])) {
-                visb &= ~(1u << (4 * cb + r));
+                visb &= ~(1u << (15 - (4 * cb + r)));
                 acc[cb][r] = -__builtin_inff();
               }
           }
-          body(uc, kb0, std::true_type{}, visb, acc);
-        } else {
-          body(uc, kb0, std::false_type{}, 0xffffu, acc);
         }
+        body(uc, kb0, visb, acc);
       });
     }
   };
@@ -561,7 +561,7 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
   const float pinf = opaque_inf();
   for (int cb = 0; cb < 4; ++cb)
     for (int j = 0; j < 4 * R; ++j) cm[cb][j] = -__builtin_inff();
-  sweep(std::integral_constant<int, UR>{}, [&](auto uc, int, auto, uint32_t, f32x4 (&acc)[4]) {
+  sweep(std::integral_constant<int, UR>{}, [&](auto uc, int, uint32_t, f32x4 (&acc)[4]) {
     constexpr int j = decltype(uc)::value % R;
     for (int cb = 0; cb < 4; ++cb)
       for (int r = 0; r < 4; ++r) cm[cb][r + 4 * j] = vmax(cm[cb][r + 4 * j], acc[cb][r], pinf);
@@ -649,7 +649,7 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
     // one candidate per round (LDS atomic on the row's count), so the wave
     // runs as many rounds as its busiest lane has candidates (about two at
     // the headline shape) instead of visiting every slot.
-    auto collect = [&](int kb0, auto partial, uint32_t visb, f32x4 (&acc)[4], auto later) {
+    auto collect = [&](int kb0, uint32_t visb, f32x4 (&acc)[4], auto later) {
       // bit 15 - (4 cb + r) <- sign of v - fl: set where v < fl, so that
       // the complement marks !(v < fl) (NaN differences have a clear sign
       // bit)
@@ -657,8 +657,7 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
       for (int cb = 0; cb < 4; ++cb)
         for (int r = 0; r < 4; ++r)
           m = __builtin_amdgcn_alignbit(m, __float_as_uint(acc[cb][r] - fl[cb]), 31);
-      m = (~m | amask) & cmask;
-      if constexpr (decltype(partial)::value) m &= __builtin_bitreverse32(visb) >> 16;
+      m = (~m | amask) & cmask & visb;
       if (m != 0u) {
         for (int cb = 0; cb < 4; ++cb) *reinterpret_cast<f32x4*>(s_scr + ((4 * cb) ^ scr_sw)) = acc[cb];
       }
@@ -676,12 +675,12 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
       }
     };
     if (round == 0)
-      sweep(std::integral_constant<int, 2>{}, [&](auto, int kb0, auto partial, uint32_t visb, f32x4 (&acc)[4]) {
-        collect(kb0, partial, visb, acc, std::false_type{});
+      sweep(std::integral_constant<int, 2>{}, [&](auto, int kb0, uint32_t visb, f32x4 (&acc)[4]) {
+        collect(kb0, visb, acc, std::false_type{});
       });
     else
-      sweep(std::integral_constant<int, 2>{}, [&](auto, int kb0, auto partial, uint32_t visb, f32x4 (&acc)[4]) {
-        collect(kb0, partial, visb, acc, std::true_type{});
+      sweep(std::integral_constant<int, 2>{}, [&](auto, int kb0, uint32_t visb, f32x4 (&acc)[4]) {
+        collect(kb0, visb, acc, std::true_type{});
       });
     __syncthreads();
     max_round = round;
