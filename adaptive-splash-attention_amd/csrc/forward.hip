@@ -294,31 +294,43 @@ __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams
   }
   __syncthreads();
   int e[2] = {lb[0], lb[1]};  // list positions of the blocks' current tiles (their mask slots)
+  // One straight-line body for every tile: both blocks' halves always run.
+  // A tile outside block h's list (or skipped by its 32-row half) runs h's
+  // half with the clip bounds set to -0.0, which makes every weight of it
+  // 0: O and the row sums gain exact zeros (finite V), no mask is written
+  // for a tile not in the list, and an in-list tile skipped by its half
+  // writes the all-zero mask.  Branching per case instead made the
+  // compiler move the accumulators between register sets on every tile
+  // (66 register copies per tile, a third of the VALU overhead beyond the
+  // weights).  The cost is the idle half's products on tiles in only one
+  // of the two lists (one tile per pair in a causal pattern).
   for (int i = 0; cur != -1; ++i) {
     const int b = i & 1;
     const int kb = cur & 0x3fffffff;
-    bool in[2] = {(cur & (1 << 30)) != 0, cur < 0};
-    bool act[2];
-    for (int h = 0; h < 2; ++h) {
-      act[h] = in[h];  // wave-uniform
-      if constexpr (HALF) act[h] = in[h] && hvalid[h] && hrow[h][kb] != 0;
-    }
+    const bool in[2] = {(cur & (1 << 30)) != 0, cur < 0};
+    const bool whole_keys = kb * kBlock + kBlock <= NK;
+    const int kmax = kbnd[kb].y;
     f32x4 acc[2][4];
-    if (act[0] && act[1]) rows_x_frag2<D>(acc[0], acc[1], sm.K[b], qf[0], qf[1], lane);
-    else if (act[0]) rows_x_frag<D>(acc[0], sm.K[b], qf[0], lane);
-    else if (act[1]) rows_x_frag<D>(acc[1], sm.K[b], qf[1], lane);
-    // forward_kernel's weights, per block
-    auto weights = [&](int h, auto partial) {
-      uint32_t nm = 0;  // bit 4f + r <- u <= 0, highest bit first
-      for (int f = 3; f >= 0; --f)
-        for (int r = 3; r >= 0; --r) {
-          float v = clip[h](acc[h][f][r]);  // max(u, 0)
-          if constexpr (decltype(partial)::value)
-            v = sm.kid[b][16 * f + 4 * g + r] <= qpos[h] ? v : -0.0f;
-          acc[h][f][r] = v;
-          if constexpr (EMIT) nm = __builtin_amdgcn_alignbit(nm, __float_as_uint(v), 31);
-        }
-      if constexpr (EMIT) smask[size_t(e[h]) * 256] = uint16_t(~nm);
+    rows_x_frag2<D>(acc[0], acc[1], sm.K[b], qf[0], qf[1], lane);
+    for (int h = 0; h < 2; ++h) {
+      bool act = in[h];  // wave-uniform
+      if constexpr (HALF) act = act && hvalid[h] && hrow[h][kb] != 0;
+      SignedClip ch = clip[h];
+      if (!act) ch.lo = ch.hi = -0.0f;  // med3(x, -0, -0) = -0: no weight
+      // forward_kernel's weights: v = max(u, 0), then keys past the row's
+      // position set to -0.0 on tiles not wholly visible
+      for (int f = 0; f < 4; ++f)
+        for (int r = 0; r < 4; ++r) acc[h][f][r] = ch(acc[h][f][r]);
+      if (act && !(whole_keys && kmax <= qmin[h]))
+        for (int f = 0; f < 4; ++f)
+          for (int r = 0; r < 4; ++r)
+            acc[h][f][r] = sm.kid[b][16 * f + 4 * g + r] <= qpos[h] ? acc[h][f][r] : -0.0f;
+      if constexpr (EMIT) {
+        uint32_t nm = 0;  // bit 4f + r <- u <= 0, highest bit first
+        for (int f = 3; f >= 0; --f)
+          for (int r = 3; r >= 0; --r) nm = __builtin_amdgcn_alignbit(nm, __float_as_uint(acc[h][f][r]), 31);
+        if (in[h]) smask[size_t(e[h]) * 256] = uint16_t(~nm);
+      }
       for (int f = 0; f < 4; ++f)
         for (int r = 0; r < 4; ++r) {
           const float pv = pow_clipped<PC>(acc[h][f][r], a);
@@ -326,19 +338,8 @@ __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams
           else acc[h][f][r] = pv;
           rowsum[h] += pv;
         }
-    };
-    const bool whole_keys = kb * kBlock + kBlock <= NK;
-    for (int h = 0; h < 2; ++h) {
-      if (act[h]) {
-        if (whole_keys && kbnd[kb].y <= qmin[h]) weights(h, std::false_type{});
-        else weights(h, std::true_type{});
-      } else if constexpr (EMIT) {
-        if (in[h]) smask[size_t(e[h]) * 256] = 0;
-      }
     }
-    if (act[0] && act[1]) tile_t_x_acc2<D>(o[0], o[1], sm.V[b], acc[0], acc[1], lane);
-    else if (act[0]) tile_t_x_acc<D>(o[0], sm.V[b], acc[0], lane);
-    else if (act[1]) tile_t_x_acc<D>(o[1], sm.V[b], acc[1], lane);
+    tile_t_x_acc2<D>(o[0], o[1], sm.V[b], acc[0], acc[1], lane);
     for (int h = 0; h < 2; ++h) e[h] += in[h] ? 1 : 0;
     cur = nxt;
     if (cur != -1) {
