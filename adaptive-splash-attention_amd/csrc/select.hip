@@ -535,17 +535,18 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
             for (int cb = 0; cb < 4; ++cb)
               for (int r = 0; r < 4; ++r) acc[cb][r] = clamp_score(acc[cb][r] * scale);
         }
+        // The padding of the last group of U tiles (i >= nvis: no key
+        // visible, key limit INT_MIN) takes the partial tiles' path: a
+        // separate path that set acc to constants made the compiler copy
+        // acc between register sets on every whole tile.
         uint32_t visb = 0xffffu;
-        if (i >= nvis) {  // padding of the last group of U tiles: nothing visible
-          for (int cb = 0; cb < 4; ++cb)
-            for (int r = 0; r < 4; ++r) acc[cb][r] = -__builtin_inff();
-          visb = 0u;
-        } else if ((e >> 24) == 1) {  // wave-uniform
+        if (i >= nvis || (e >> 24) == 1) {  // wave-uniform
+          const int klim = i < nvis ? NK : INT_MIN;
           for (int r = 0; r < 4; ++r) {
             const int key = kb0 + r;
-            const int kp = key < NK ? kidx[key] : INT_MAX;
+            const int kp = key < klim ? kidx[key] : INT_MAX;
             for (int cb = 0; cb < 4; ++cb)
-              if (!(key < NK && kp <= qpos[cb])) {
+              if (!(key < klim && kp <= qpos[cb])) {
                 visb &= ~(1u << (15 - (4 * cb + r)));
                 acc[cb][r] = -__builtin_inff();
               }
