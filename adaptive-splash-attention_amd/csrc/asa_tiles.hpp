@@ -233,14 +233,20 @@ __device__ __forceinline__ void tile_t_x_acc(f32x4 (&o)[D / 16], const T* rm,
 // rows_x_frag for two B fragments at once: each A operand is read from LDS
 // once and feeds both products (the same operands and order per product as
 // rows_x_frag, so each result is bit-identical to it).
+// The products start from the accumulators c0, c1 (every block f), zero by
+// default.
 template <int D, typename T, typename std::enable_if<is_half<T>, int>::type = 0>
 __device__ __forceinline__ void rows_x_frag2(f32x4 (&acc0)[4], f32x4 (&acc1)[4], const T* rm,
                                              const RowFrag<T, D>& b0, const RowFrag<T, D>& b1,
-                                             int lane) {
+                                             int lane, const f32x4 c0 = f32x4{0.f, 0.f, 0.f, 0.f},
+                                             const f32x4 c1 = f32x4{0.f, 0.f, 0.f, 0.f}) {
   using V8 = typename Half<T>::v8;
   const int g = lane >> 4, c = lane & 15;
   const T* base = rm + c * Tile<T, D>::kRs + ((8 * g) ^ Tile<T, D>::sw(c));
-  for (int f = 0; f < 4; ++f) acc0[f] = acc1[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int f = 0; f < 4; ++f) {
+    acc0[f] = c0;
+    acc1[f] = c1;
+  }
   for (int s = 0; s < D / 32; ++s)
     for (int f = 0; f < 4; ++f) {
       const V8 a = *reinterpret_cast<const V8*>(base + 16 * f * Tile<T, D>::kRs + 32 * s);

@@ -185,10 +185,18 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
 // workgroup walks the union of the two blocks' key-block lists (merged on
 // the fly from the CSR).  Each K and V tile read from LDS then feeds two
 // fragments' products (rows_x_frag2, tile_t_x_acc2): half the LDS reads
-// per row of the one-block kernel, whose waves were half-bound by them.  A
-// tile in one block's list only runs that block's half.  Per block and
-// tile the arithmetic, its order and the masks written are those of
-// forward_kernel, so the results are bit-identical to it.
+// per row of the one-block kernel, whose waves were half-bound by them.
+//
+// The clip is folded into the products (launch_tde checks that it applies,
+// pair_fold_ok: an integer power class and c = (alpha - 1) scale in
+// [2^-8, 2^8]): the score products start from -tau / c instead of 0, so
+// that x = s - tau / c comes out of the MFMA and one v_med3 per score gives
+// v' = med3(x, lo / c, hi / c) = max(u, 0) / c, with SignedClip's sign-bit
+// rule.  The weights p' = v'^e are p / c^e, a per-launch constant that the
+// output's ratio cancels; the row sums are scaled back by c^e.  This saves
+// forward_kernel's fma per score (the kernel is VALU-bound); u is rounded
+// as c (s - tau / c) instead of once, an ulp-level difference from
+// forward_kernel.
 template <typename T, int D, int PC, bool EMIT, bool HALF>
 __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams p) {
   static_assert(is_half<T>, "16-bit inputs only");
@@ -216,7 +224,8 @@ __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams
   bool qok[2], hvalid[2];
   size_t row[2];
   RowFrag<T, D> qf[2];
-  SignedClip clip[2] = {SignedClip(am1, 0.0f, 0.0f, false), SignedClip(am1, 0.0f, 0.0f, false)};
+  const float cs = am1 * p.d.scale;  // c > 0 (pair_fold_ok)
+  float x0[2] = {0.0f, 0.0f}, lo[2] = {-0.0f, -0.0f}, hi[2] = {-0.0f, -0.0f};  // folded clip
   float pscale[2] = {1.0f, 1.0f}, rowsum[2] = {0.0f, 0.0f};
   const uint8_t* hrow[2] = {nullptr, nullptr};
   uint16_t* smask = nullptr;
@@ -229,14 +238,22 @@ __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams
     row[h] = size_t(bh) * NQ + (qok[h] ? q : 0);
     qf[h].load(static_cast<const T*>(p.q) + row[h] * D, qok[h], lane);
     qpos[h] = qok[h] ? p.q_idx[row[h]] : 0;
-    clip[h] = SignedClip(am1, p.d.scale, qok[h] ? p.taus[row[h]] : 0.0f, qok[h]);
+    if (qok[h]) {
+      // SignedClip's bounds, divided by c (rows that get no weight keep
+      // x0 = 0 and lo = hi = -0: v' = -0 for every score)
+      const float tau = p.taus[row[h]];
+      const float l = fmaf(-10.0f, am1, -tau), u = fmaf(10.0f, am1, -tau);
+      x0[h] = -tau / cs;
+      lo[h] = l > 0.0f ? l / cs : -0.0f;
+      hi[h] = u > 0.0f ? u / cs : -0.0f;
+    }
     if constexpr (std::is_same<T, h16>::value) {
       // fp16 P operands scaled by 2^-e, e the exponent of the row's
-      // largest weight (as in forward_kernel)
+      // largest weight p' (as in forward_kernel, for p)
       if (qok[h]) {
         const float s1 = p.top1[row[h]];
         const float u1 = fmaxf(fminf(fmaf(am1, s1, -p.taus[row[h]]), fmaf(10.0f, am1, -p.taus[row[h]])), 0.0f);
-        const float p1 = pow_clipped<PC>(u1, a);
+        const float p1 = pow_clipped<PC>(u1 / cs, a);
         int e = 0;
         (void)frexpf(p1, &e);
         pscale[h] = p1 > 0.0f ? (finite(p1) ? ldexpf(1.0f, -e) : 0.0f) : 1.0f;
@@ -311,16 +328,16 @@ __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams
     const bool whole_keys = kb * kBlock + kBlock <= NK;
     const int kmax = kbnd[kb].y;
     f32x4 acc[2][4];
-    rows_x_frag2<D>(acc[0], acc[1], sm.K[b], qf[0], qf[1], lane);
+    rows_x_frag2<D>(acc[0], acc[1], sm.K[b], qf[0], qf[1], lane, f32x4{x0[0], x0[0], x0[0], x0[0]},
+                    f32x4{x0[1], x0[1], x0[1], x0[1]});
     for (int h = 0; h < 2; ++h) {
       bool act = in[h];  // wave-uniform
       if constexpr (HALF) act = act && hvalid[h] && hrow[h][kb] != 0;
-      SignedClip ch = clip[h];
-      if (!act) ch.lo = ch.hi = -0.0f;  // med3(x, -0, -0) = -0: no weight
-      // forward_kernel's weights: v = max(u, 0), then keys past the row's
-      // position set to -0.0 on tiles not wholly visible
+      const float l = act ? lo[h] : -0.0f, u = act ? hi[h] : -0.0f;  // med3(x, -0, -0) = -0: no weight
+      // forward_kernel's weights, over c: v' = max(u, 0) / c, then keys past
+      // the row's position set to -0.0 on tiles not wholly visible
       for (int f = 0; f < 4; ++f)
-        for (int r = 0; r < 4; ++r) acc[h][f][r] = ch(acc[h][f][r]);
+        for (int r = 0; r < 4; ++r) acc[h][f][r] = __builtin_amdgcn_fmed3f(acc[h][f][r], l, u);
       if (act && !(whole_keys && kmax <= qmin[h]))
         for (int f = 0; f < 4; ++f)
           for (int r = 0; r < 4; ++r)
@@ -350,9 +367,10 @@ __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams
     __syncthreads();
   }
 
+  const float ce = pow_fast<PC>(cs, a);  // p = c^e p'
   for (int h = 0; h < 2; ++h) {
-    const float norm = sum_groups(rowsum[h]);
-    const float inv = 1.0f / ((norm + kEps) * pscale[h]);  // pscale 0: non-finite weights, output 0
+    const float norm = ce * sum_groups(rowsum[h]);
+    const float inv = ce / ((norm + kEps) * pscale[h]);  // pscale 0: non-finite weights, output 0
     if (qok[h]) {
       T* orow = static_cast<T*>(p.out) + row[h] * D;
       for (int db = 0; db < D / 16; ++db)
@@ -373,14 +391,23 @@ hipError_t launch_pair(const ForwardParams& p, hipStream_t s) {
     case kA15: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE2, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
     case kA20: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE1, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
     case kA125: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE4, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((forward_pair_kernel<T, D, kEGen, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
+    default: return hipErrorInvalidValue;  // excluded by pair_fold_ok
   }
   return hipGetLastError();
 }
 
+// forward_pair_kernel's folded clip applies: an integer power class (the
+// general power keeps an EPS floor on u) and c = (alpha - 1) scale in
+// [2^-8, 2^8], so that p / c^e is within 2^32 of p either way.
+inline bool pair_fold_ok(const ForwardParams& p) {
+  const float c = (p.d.alpha - 1.0f) * p.d.scale;
+  return alpha_class_of(p.d.alpha) != kAGen && c >= 0x1p-8f && c <= 0x1p8f;
+}
+
 template <typename T, int D, bool EMIT, bool HALF>
 hipError_t launch_tde(const ForwardParams& p, hipStream_t s) {
-  if constexpr (is_half<T> && D == 64) return launch_pair<T, D, EMIT, HALF>(p, s);
+  if constexpr (is_half<T> && D == 64)
+    if (pair_fold_ok(p)) return launch_pair<T, D, EMIT, HALF>(p, s);
   dim3 grid(p.d.nQB * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
     case kA15: hipLaunchKernelGGL((forward_kernel<T, D, kE2, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;

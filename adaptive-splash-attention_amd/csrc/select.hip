@@ -393,6 +393,15 @@ __host__ __device__ inline int select_round_bound(int NK, int k, int cap) {
 // Waves per SIMD the headline variant (bf16, d = 64, two classes per lane)
 // is held to: three blocks of its ~50 KB of LDS fit a CU, and 168 VGPRs
 // let three waves share a SIMD (one more VGPR would drop it to two).
+// Sweep 1's LDS ring (16-bit inputs): tiles in flight per wave, and its
+// bytes (four waves x tiles x 16 keys x D x 2 bytes).  It fits below
+// sel_layout's tkey for every k: the class-maxima exchange alone takes
+// 64 (64 R + 4) floats, and the value scratch 16 KiB after it.
+template <int D, int R>
+constexpr int ring_tiles() { return (D == 128 && R == 2) ? 3 : 4; }
+template <int D, int R>
+constexpr int ring_bytes() { return 4 * ring_tiles<D, R>() * 32 * D; }
+
 template <typename T, int D, int R>
 constexpr int select_waves_per_simd() { return sizeof(T) == 2 && D == 64 && R == 2 ? 3 : 1; }
 
@@ -491,6 +500,31 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
   auto entry = [&](int i) {
     return i < kWave ? __builtin_amdgcn_readlane(vl0, i) : __builtin_amdgcn_readfirstlane(s_vlist[i]);
   };
+  // Per tile, after its scores are formed: the visibility masking, then
+  // body(u, kb0, visb, acc).  The padding of the last group of U tiles
+  // (i >= nvis: no key visible, key limit INT_MIN) takes the partial
+  // tiles' path: a separate path that set acc to constants made the
+  // compiler copy acc between register sets on every whole tile.
+  auto finish = [&](auto uc, int i, int e, f32x4(&acc)[4], auto&& body) __attribute__((always_inline)) {
+    const int kb0 = (e & 0xffffff) * kBlock + 16 * w + 4 * g;  // the lane's first key
+    if constexpr (MODE == kExactScores)
+      for (int cb = 0; cb < 4; ++cb)
+        for (int r = 0; r < 4; ++r) acc[cb][r] = clamp_score(acc[cb][r] * scale);
+    uint32_t visb = 0xffffu;
+    if (i >= nvis || (e >> 24) == 1) {  // wave-uniform
+      const int klim = i < nvis ? NK : INT_MIN;
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + r;
+        const int kp = key < klim ? kidx[key] : INT_MAX;
+        for (int cb = 0; cb < 4; ++cb)
+          if (!(key < klim && kp <= qpos[cb])) {
+            visb &= ~(1u << (15 - (4 * cb + r)));
+            acc[cb][r] = -__builtin_inff();
+          }
+      }
+    }
+    body(uc, kb0, visb, acc);
+  };
   auto sweep = [&](auto u_tag, auto&& body) {
     constexpr int U = decltype(u_tag)::value;
     if (nvis == 0) return;  // block-uniform
@@ -515,10 +549,9 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
         constexpr int u = decltype(uc)::value;
         const int i = i0 + u;
         const int e = ent[u & 1];
-        const int kt = e & 0xffffff;
-        const int kb0 = kt * kBlock + 16 * w + 4 * g;  // the lane's first key
         f32x4 acc[4];
         if constexpr (MODE == kGivenScores) {
+          const int kb0 = (e & 0xffffff) * kBlock + 16 * w + 4 * g;
           for (int cb = 0; cb < 4; ++cb)
             for (int r = 0; r < 4; ++r) {
               const int key = kb0 + r;
@@ -531,30 +564,62 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
           kq[u & 1].product(acc, qf);
           ent[u & 1] = entry(i + 2 < nvis ? i + 2 : nvis - 1);
           fetch(kq[u & 1], ent[u & 1]);
-          if constexpr (MODE == kExactScores)
-            for (int cb = 0; cb < 4; ++cb)
-              for (int r = 0; r < 4; ++r) acc[cb][r] = clamp_score(acc[cb][r] * scale);
         }
-        // The padding of the last group of U tiles (i >= nvis: no key
-        // visible, key limit INT_MIN) takes the partial tiles' path: a
-        // separate path that set acc to constants made the compiler copy
-        // acc between register sets on every whole tile.
-        uint32_t visb = 0xffffu;
-        if (i >= nvis || (e >> 24) == 1) {  // wave-uniform
-          const int klim = i < nvis ? NK : INT_MIN;
-          for (int r = 0; r < 4; ++r) {
-            const int key = kb0 + r;
-            const int kp = key < klim ? kidx[key] : INT_MAX;
-            for (int cb = 0; cb < 4; ++cb)
-              if (!(key < klim && kp <= qpos[cb])) {
-                visb &= ~(1u << (15 - (4 * cb + r)));
-                acc[cb][r] = -__builtin_inff();
-              }
-          }
-        }
-        body(uc, kb0, visb, acc);
+        finish(uc, i, e, acc, body);
       });
     }
+  };
+  // Sweep 1 (16-bit inputs) reads its K quarters through a ring in LDS
+  // filled by global_load_lds (the loads in flight hold no VGPRs, so each
+  // wave keeps kRing tiles in flight instead of two).  The ring occupies
+  // the candidate lists' and value scratch's bytes, which sweep 1 leaves
+  // unused; each wave owns kRing slots of one wave quarter (16 keys x D,
+  // lane L's 16-byte chunk s at slot + 1024 s + 16 L, the order
+  // global_load_lds writes a wave's 64 chunks in).  The compiler does not
+  // order LDS reads after the DMA that fills them, so the waits are
+  // explicit: vmcnt before a slot is read (the (kRing - 1) younger tiles'
+  // loads may stay in flight), lgkmcnt(0) before a slot is refilled.
+  constexpr int kCh = D / 32;  // 16-byte chunks per lane and tile
+  constexpr int kSlot = kWave * 16 * kCh;  // bytes per wave and tile
+  constexpr int kRing = ring_tiles<D, R>();
+  constexpr bool kRingSweep = kTiles && is_half<T>;
+  auto sweep_ring = [&](auto u_tag, auto&& body) {
+    constexpr int U = decltype(u_tag)::value;
+    if (nvis == 0) return;  // block-uniform
+    unsigned char* ringw = smem + w * kRing * kSlot;  // this wave's slots
+    auto dma = [&](int slot, int e) __attribute__((always_inline)) {
+      const int key = (e & 0xffffff) * kBlock + kq0;
+      const T* src = Kb + size_t(key < NK ? key : 0) * D + 8 * g;
+      unsigned char* dst = ringw + slot * kSlot;
+      for (int s = 0; s < kCh; ++s)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + 32 * s),
+                                         (__attribute__((address_space(3))) void*)(dst + s * kWave * 16),
+                                         16, 0, 0);
+    };
+    // The Q fragments' loads are waited for here, by an s_waitcnt the
+    // compiler sees: otherwise its wait for them before the first product
+    // stays in the loop as vmcnt(0) on every tile (encoding: vmcnt 0,
+    // expcnt 7, lgkmcnt 15).
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    for (int j = 0; j < kRing; ++j) dma(j, entry(j < nvis ? j : nvis - 1));
+    int slot = 0;  // slot of tile i
+    for (int i0 = 0; i0 < nvis; i0 += U) {
+      static_for<0, U>([&](auto uc) {
+        const int i = i0 + decltype(uc)::value;
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kRing - 1) * kCh) : "memory");
+        KQuarter<T, D> kq;
+        using A = std::remove_reference_t<decltype(kq.a[0])>;
+        for (int s = 0; s < kCh; ++s)
+          kq.a[s] = *reinterpret_cast<const A*>(ringw + slot * kSlot + s * kWave * 16 + 16 * L);
+        f32x4 acc[4];
+        kq.product(acc, qf);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        dma(slot, entry(i + kRing < nvis ? i + kRing : nvis - 1));
+        slot = slot + 1 == kRing ? 0 : slot + 1;
+        finish(uc, i, entry(i < nvis ? i : nvis - 1), acc, body);
+      });
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   };
 
   // ---------------- sweep 1: class maxima ----------------
@@ -562,11 +627,17 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
   const float pinf = opaque_inf();
   for (int cb = 0; cb < 4; ++cb)
     for (int j = 0; j < 4 * R; ++j) cm[cb][j] = -__builtin_inff();
-  sweep(std::integral_constant<int, UR>{}, [&](auto uc, int, uint32_t, f32x4 (&acc)[4]) {
+  auto maxima = [&](auto uc, int, uint32_t, f32x4 (&acc)[4]) {
     constexpr int j = decltype(uc)::value % R;
     for (int cb = 0; cb < 4; ++cb)
       for (int r = 0; r < 4; ++r) cm[cb][r + 4 * j] = vmax(cm[cb][r + 4 * j], acc[cb][r], pinf);
-  });
+  };
+  if constexpr (kRingSweep) {
+    sweep_ring(std::integral_constant<int, UR>{}, maxima);
+    __syncthreads();  // every wave's ring reads are done before the exchange reuses the bytes
+  } else {
+    sweep(std::integral_constant<int, UR>{}, maxima);
+  }
 
   // Exchange: row 16 cb + c's 64 R class maxima, 4 R from each of its 16
   // lanes (4 waves x 4 lane groups), then wave w finds the floors of rows
@@ -937,6 +1008,7 @@ template <typename T, int D, int MODE, int R>
 hipError_t launch_one(const SelectParams& p, hipStream_t s) {
   const SelLayout l = sel_layout(p.d.k, p.cap, p.d.nKB);
   auto kern = select_kernel<T, D, MODE, R>;
+  if (is_half<T> && MODE != kGivenScores && ring_bytes<D, R>() > l.tkey) return hipErrorInvalidValue;
   if (l.total > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, l.total);
