@@ -288,8 +288,11 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
       vraw[u] = C::raw(Vb + size_t(key[u]) * D + sub * E);
     }
     for (int u = 0; u < kBatchQ; ++u) {
-      const float s = group_lanes_sum<LPR>(C::dot(qv, kraw[u]));
-      const float dp = group_lanes_sum<LPR>(C::dot(dO, vraw[u]));
+      float s = group_lanes_sum<LPR>(C::dot(qv, kraw[u]));
+      float dp = group_lanes_sum<LPR>(C::dot(dO, vraw[u]));
+      // complete here: sunk into the branch below, the last step's DPP
+      // move no longer fused into its add
+      asm volatile("" : "+v"(s), "+v"(dp));
       if (val[u]) {
         float kr[E];
         C::unpack(kraw[u], kr);
@@ -556,6 +559,9 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   const float alpha = p.d.alpha, am1 = alpha - 1.0f;
   const float a = 1.0f / am1, ew = (2.0f - alpha) / am1;
   const float cu = am1 * p.d.scale;  // ClippedU's c
+  // the score clamp [-10, 10] on the raw dot product (scale > 0); NaN dots
+  // give smin, as the clamp gives NaN -> -10
+  const float smax = 10.0f / p.d.scale, smin = -smax;
   const size_t rbase = size_t(bh) * NQ;
   const T* Qb = static_cast<const T*>(p.q) + rbase * D;
   const T* dOb = static_cast<const T*>(p.dout) + rbase * D;
@@ -657,6 +663,9 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
         }
         s = group_lanes_sum<LPR>(s);
         dp = group_lanes_sum<LPR>(dp);
+        // complete here: sunk into the branch below, the last step's DPP
+        // move no longer fused into its add
+        asm volatile("" : "+v"(s), "+v"(dp));
         // the record's words to every lane of each quad (DPP broadcasts)
         const RowRec rc{quad_bcast<0>(rw[u]), quad_bcast<1>(rw[u]), quad_bcast<2>(rw[u]),
                         quad_bcast<3>(rw[u])};
@@ -669,10 +678,11 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
             C::unpack(graw[u][c], x8);
             for (int x = 0; x < E; ++x) gr[c * E + x] = x8[x];
           }
-          // ClippedU of a valid row (the lists hold valid rows only)
-          const float lo = fmaxf(fmaf(-10.f, am1, rc.nt), 0.f);
-          const float hi = fmaxf(fmaf(10.f, am1, rc.nt), 0.f);
-          const float v = __builtin_amdgcn_fmed3f(fmaf(cu, s, rc.nt), lo, hi);
+          // max(u, 0) of a valid row (the lists hold valid rows only) with
+          // the score clamp on s itself: three instructions instead of
+          // ClippedU's bounds per pair (u differs from ClippedU's only for
+          // clamped scores, by the rounding of 10 / scale)
+          const float v = fmaxf(fmaf(cu, __builtin_amdgcn_fmed3f(s, smin, smax), rc.nt), 0.0f);
           const float pn = pow_clipped<PP>(v, a) * rc.invn;
           float wv = pow_clipped<PW>(v, ew);
           if constexpr (REF) wv = v > kEps ? wv : 0.0f;  // the reference's u > EPS
