@@ -53,8 +53,8 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "308c008b4d2c8441"
-HBM_TRAFFIC = {'bounds': 1110072, 'select': 141637409, 'tau': 34745398, 'refine': 109599604, 'compact': 2743465, 'forward': 297753286, 'bwd_dq_sparse': 240817863, 'bwd_dkdv_sparse': 288165908}
+HBM_TRAFFIC_SOURCES = "92644c62cec29345"
+HBM_TRAFFIC = {'bounds': 1110126, 'select': 145761295, 'tau': 34744896, 'refine': 109502944, 'compact': 2743455, 'forward': 314942197, 'bwd_dq_sparse': 240854008, 'bwd_dkdv_sparse': 288274033}
 
 
 def source_hash() -> str:
