@@ -62,6 +62,14 @@ CASES = [
     ("bf16_ragged_pairs", 2, 1, 197, 300, 64, 1.5, 16, 0.125, torch.bfloat16),
     ("fp16_odd_blocks", 1, 2, 130, 130, 64, 1.5, 8, 0.125, torch.float16),
     ("fp32_alpha_general", 1, 1, 128, 128, 64, 1.7, 8, 0.125, torch.float32),
+    # the paired forward folds (alpha - 1) scale into its clip for the
+    # integer power classes (p = v', v'^2, v'^4) when (alpha - 1) scale is in
+    # [2^-8, 2^8]; a general alpha or a scale outside that range runs the
+    # one-block forward at 16 bits and d = 64
+    ("fp16_d64_sparsemax", 1, 2, 192, 192, 64, 2.0, 16, 0.125, torch.float16),
+    ("bf16_d64_a125", 1, 2, 256, 256, 64, 1.25, 32, 0.125, torch.bfloat16),
+    ("bf16_d64_alpha_general", 1, 2, 256, 256, 64, 1.7, 16, 0.125, torch.bfloat16),
+    ("bf16_d64_small_scale", 1, 1, 128, 128, 64, 1.5, 8, 0.004, torch.bfloat16),
 ]
 
 
