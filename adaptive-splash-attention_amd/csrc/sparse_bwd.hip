@@ -130,6 +130,16 @@ template <> struct Chunk<float> {
   }
 };
 
+// 16 bytes at a byte offset from a wave-uniform base: the 32-bit offset
+// lets the load take the base from scalar registers (global_load's saddr
+// form), one VALU instruction per row address instead of the 64-bit
+// multiply-add of an element index.  Offsets stay within one head's rows
+// (NK or NQ rows of D elements: far below 2^32 bytes).
+template <typename T>
+__device__ __forceinline__ uint4 raw_at(const T* base, uint32_t byte_off) {
+  return *reinterpret_cast<const uint4*>(reinterpret_cast<const unsigned char*>(base) + byte_off);
+}
+
 // Sum over aligned groups of G lanes (G a power of two <= 32) by lane
 // exchanges: each step adds a lane's value and its partner's, so every lane
 // of a group gets a bit-identical sum.  After the steps within a quad
@@ -284,8 +294,9 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
       key[u] = val[u] ? lst[q + u] : 0;
     }
     for (int u = 0; u < kBatchQ; ++u) {
-      kraw[u] = C::raw(Kb + size_t(key[u]) * D + sub * E);
-      vraw[u] = C::raw(Vb + size_t(key[u]) * D + sub * E);
+      const uint32_t off = (uint32_t(key[u]) * D + sub * E) * uint32_t(sizeof(T));
+      kraw[u] = raw_at(Kb, off);
+      vraw[u] = raw_at(Vb, off);
     }
     for (int u = 0; u < kBatchQ; ++u) {
       float s = group_lanes_sum<LPR>(C::dot(qv, kraw[u]));
@@ -650,10 +661,12 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
       }
       for (int u = 0; u < kBatch; ++u) {
         for (int c = 0; c < NC; ++c) {
-          qraw[u][c] = C::raw(Qb + size_t(r[u]) * D + sub * EL + c * E);
-          graw[u][c] = C::raw(dOb + size_t(r[u]) * D + sub * EL + c * E);
+          const uint32_t off = (uint32_t(r[u]) * D + sub * EL + c * E) * uint32_t(sizeof(T));
+          qraw[u][c] = raw_at(Qb, off);
+          graw[u][c] = raw_at(dOb, off);
         }
-        rw[u] = reinterpret_cast<const float*>(rec + r[u])[sub & 3];
+        rw[u] = *reinterpret_cast<const float*>(reinterpret_cast<const unsigned char*>(rec) +
+                                                (uint32_t(r[u]) * uint32_t(sizeof(RowRec)) + 4u * (sub & 3)));
       }
       for (int u = 0; u < kBatch; ++u) {
         float s = 0.0f, dp = 0.0f;
