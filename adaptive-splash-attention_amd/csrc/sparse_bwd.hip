@@ -49,8 +49,13 @@ constexpr int kThreads = 256;
 constexpr int kRowList = 64;   // keys listed per row before a dQ phase B
 // rows listed per key before a dK/dV phase B (KPW keys per wave)
 template <int KPW> constexpr int key_list() { return KPW > 8 ? 96 : 128; }
-constexpr int kBatch = 2;      // dK/dV entries per lane group whose gathers are in flight together
-constexpr int kBatchQ = 3;     // dQ entries whose gathers are in flight together
+// Entries per lane group whose gathers are in flight together: dK/dV and
+// dQ.  Measured at the headline (alpha 1.5, bf16, d 64): dK/dV 2 -> 3 -> 4
+// gave 204 -> 195 -> 191 us, dQ 3 -> 4 -> 5 gave 144 -> 137 -> 135 us.  The
+// alpha 1.25 and general-alpha instantiations keep 2 and 3: at 4 and 5
+// their weights' extra registers spill.
+template <int AC> constexpr int batch_kv() { return AC == kA15 || AC == kA20 ? 4 : 2; }
+template <int AC> constexpr int batch_q() { return AC == kA15 || AC == kA20 ? 5 : 3; }
 constexpr int kChunk = 16;     // tiles whose masks are fetched together
 constexpr int kFlat = 1024;    // keys a dQ wave lists at once on its balanced path
 
@@ -178,6 +183,7 @@ __device__ __forceinline__ int groups_max(int v) {
 // ---------------------------------------------------------------------------
 template <typename T, int D, int AC, bool REF>
 __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p) {
+  constexpr int kBatchQ = batch_q<AC>();
   using C = Chunk<T>;
   constexpr int E = C::E;
   constexpr int LPR = D / E;          // lanes per row (16 bytes each)
@@ -510,6 +516,7 @@ template <typename T, int D> constexpr int keys_per_block() { return 4 * (kWave 
 
 template <typename T, int D, int AC, bool REF>
 __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams p) {
+  constexpr int kBatch = batch_kv<AC>();
   using C = Chunk<T>;
   constexpr int E = C::E;
   constexpr int NC = kKeyChunks;      // 16-byte chunks per lane
@@ -626,8 +633,9 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
     const int partner = s_rank[w][KPW - 1 - rank];
     const int pcnt = s_cnt[w][partner];
     const int cb = big ? cnt : pcnt, cs = big ? pcnt : cnt;
-    const int pcs = (cs + 1) & ~1;                         // the shorter list in whole batches
-    const int ob = min(cb, ((cb + pcs + 2) / 4) * 2);      // the longer list's head: even, about half
+    const int pcs = (cs + kBatch - 1) / kBatch * kBatch;  // the shorter list in whole batches
+    // the longer list's head: whole batches, about half of the pair's work
+    const int ob = min(cb, ((cb + pcs + kBatch) / (2 * kBatch)) * kBatch);
     const int hb = cb - ob;                                // its tail, summed by the shorter's group
     const int tail_at = big || hb == 0 ? INT_MAX : pcs;   // step where this group turns to the tail
     const int nmax = groups_max<LPR>(big ? ob : pcs + hb);
