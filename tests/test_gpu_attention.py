@@ -70,6 +70,9 @@ CASES = [
     ("bf16_d64_a125", 1, 2, 256, 256, 64, 1.25, 32, 0.125, torch.bfloat16),
     ("bf16_d64_alpha_general", 1, 2, 256, 256, 64, 1.7, 16, 0.125, torch.bfloat16),
     ("bf16_d64_small_scale", 1, 1, 128, 128, 64, 1.5, 8, 0.004, torch.bfloat16),
+    # 16-bit d = 128 with k <= 32: the score pass's LDS ring holds three
+    # tiles per wave there (four elsewhere)
+    ("bf16_d128_k16", 1, 2, 320, 320, 128, 1.5, 16, 128 ** -0.5, torch.bfloat16),
 ]
 
 
