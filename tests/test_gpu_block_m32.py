@@ -126,6 +126,31 @@ def test_attention_block_m32_matches_oracle(dev, case, mode, support):
         assert float((out64 - out).abs().max()) > 1e-2
 
 
+@pytest.mark.parametrize("mode", ["entmax", "reference"])
+def test_attention_block_m32_bf16_magnets(dev, mode):
+    """bf16 at d = 64 runs the paired forward; with 32-row masks a wave's
+    half drops the union tiles its mask row lacks (its clip bounds set to
+    -0 there).  The magnets make every pair of halves differ."""
+    print(f"[bm32] attention magnets bf16 {mode}", flush=True)
+    Q, K, V, dO, qi, ki = _magnets(2, 256, 64)
+    Q, K, V = (t.to(torch.bfloat16) for t in (Q, K, V))
+    alpha, scale, k = 1.5, 0.125, 2
+    q, kk, v, qd, kd = sa.ops.check_inputs(Q.to(dev), K.to(dev), V.to(dev), qi.to(dev),
+                                           ki.to(dev))
+    out, st = sa.ops.splash_forward(q, kk, v, qd, kd, alpha, k, scale, block_m=32)
+    grads = sa.ops.splash_backward(q, kk, v, qd, kd, out, dO.to(dev), st, alpha, k, scale, mode)
+    torch.cuda.synchronize()
+    m = orc.GRAD_ENTMAX if mode == "entmax" else orc.GRAD_REFERENCE
+    own, at, og = oracle_at_gpu_tau(np32(Q), np32(K), np32(V), np32(dO), qi.numpy(), ki.numpy(),
+                                    alpha, scale, k, st.taus.cpu().numpy(), m, block_m=32)
+    np.testing.assert_array_equal(st.mask.cpu().numpy(), own.mask)
+    assert_close("out", np32(out), at.out, 2e-2)
+    for name, g, w in zip(("dQ", "dK", "dV"), grads, og):
+        assert_close(name, np32(g), w, 2e-2)
+    out64, _ = sa.ops.splash_forward(q, kk, v, qd, kd, alpha, k, scale, with_support=False)
+    assert float((out64.float() - out.float()).abs().max()) > 1e-2
+
+
 def test_module_block_m32_bf16(dev):
     print("[bm32] module bf16 1x2x256x64 autograd", flush=True)
     Q, K, V, dO = make_inputs(1, 2, 256, 256, 64, seed=4, dtype=torch.bfloat16)
