@@ -142,6 +142,9 @@ size_t refine_lds_bytes(const Dims& d, int dtype, int lcap);
 // 0: none fit, every row sweeps; -1: not even the sweep stage fits).
 int refine_list_capacity(const Dims& d, int dtype, size_t max_lds);
 hipError_t launch_compact(const CompactParams& p, hipStream_t s);
+// launch_tau and launch_compact(cp) as one launch (the tau rows' blocks
+// first); for a mask that no pass changes between the two.
+hipError_t launch_tau_compact(const SelectParams& p, const CompactParams& cp, hipStream_t s);
 // 64-row mask from a 32-row one: mask[bh, qb, kb] = half[bh, 2 qb, kb] |
 // half[bh, 2 qb + 1, kb] (the second row when it exists).
 hipError_t launch_fold_halves(const uint8_t* half, uint8_t* mask, int BH, int NQ, int nQB,

@@ -286,24 +286,29 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
   hipError_t e = asa::launch_select(sp, sh.dtype, scores != nullptr, s);
   asa::profile_end(s);
   if (int rc = check_hip(e, "select kernel launch")) return rc;
-  asa::profile_begin("tau", s);
-  e = asa::launch_tau(sp, s);
-  asa::profile_end(s);
-  if (int rc = check_hip(e, "tau kernel launch")) return rc;
+  asa::CompactParams cp{sh.BH, sh.nQB, sh.nKB, c64.mask, c64.q_ptr, c64.q_list, c64.k_ptr,
+                        c64.k_list};
   if (sh.exact) {
+    asa::profile_begin("tau", s);
+    e = asa::launch_tau(sp, s);
+    asa::profile_end(s);
+    if (int rc = check_hip(e, "tau kernel launch")) return rc;
     // exact threshold over the whole row; adds the support's key blocks
     asa::profile_begin("refine", s);
     e = asa::launch_refine(sp, sh.dtype, s);
     asa::profile_end(s);
     if (int rc = check_hip(e, "refine kernel launch")) return rc;
+    asa::profile_begin("compact", s);
+    e = asa::launch_compact(cp, s);
+    asa::profile_end(s);
+    if (int rc = check_hip(e, "compact kernel launch")) return rc;
+  } else {
+    // the mask is final after the score pass: tau and the lists in one launch
+    asa::profile_begin("tau_compact", s);
+    e = asa::launch_tau_compact(sp, cp, s);
+    asa::profile_end(s);
+    if (int rc = check_hip(e, "tau/compact kernel launch")) return rc;
   }
-
-  asa::CompactParams cp{sh.BH, sh.nQB, sh.nKB, c64.mask, c64.q_ptr, c64.q_list, c64.k_ptr,
-                        c64.k_list};
-  asa::profile_begin("compact", s);
-  e = asa::launch_compact(cp, s);
-  asa::profile_end(s);
-  if (int rc = check_hip(e, "compact kernel launch")) return rc;
   if (sh.bm == 32) {
     asa::CompactParams cm{sh.BH, sh.nQBm, sh.nKB, st->mask, st->q_ptr, st->q_list, st->k_ptr,
                           st->k_list};

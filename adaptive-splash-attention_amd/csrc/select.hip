@@ -43,6 +43,7 @@
 #include <climits>
 #include <type_traits>
 
+#include "asa_compact.hpp"
 #include "asa_device.hpp"
 #include "asa_launch.hpp"
 #include "asa_stage.hpp"
@@ -988,9 +989,9 @@ __global__ __launch_bounds__(kThreads) void bounds_kernel(SelectParams p) {
 // tau of every row from its sorted top-k values (one thread per row):
 // tkv[e * rows + row], e < k.
 template <int AC, int KMAX>
-__global__ __launch_bounds__(kThreads) void tau_kernel(SelectParams p) {
+__device__ __forceinline__ void tau_row(const SelectParams& p, int blk) {
   const size_t rows = size_t(p.d.BH) * p.d.NQ;
-  const size_t r = size_t(blockIdx.x) * kThreads + threadIdx.x;
+  const size_t r = size_t(blk) * kThreads + threadIdx.x;
   if (r >= rows) return;
   const int k = p.d.k;
   const float* v = p.tkv + r;
@@ -1001,6 +1002,25 @@ __global__ __launch_bounds__(kThreads) void tau_kernel(SelectParams p) {
     p.taus[r] = entmax_tau<AC, KMAX>([&](int j) { return reg[j]; }, k, p.d.alpha);
   } else {
     p.taus[r] = entmax_tau<AC, 0>([&](int j) { return v[size_t(j) * rows]; }, k, p.d.alpha);
+  }
+}
+
+
+template <int AC, int KMAX>
+__global__ __launch_bounds__(kThreads) void tau_kernel(SelectParams p) {
+  tau_row<AC, KMAX>(p, blockIdx.x);
+}
+
+// tau_kernel's blocks, then compact_kernel's (both read only what the
+// score pass wrote): one launch, the compaction running beside the tau
+// rows instead of after them.
+template <int AC, int KMAX>
+__global__ __launch_bounds__(kThreads) void tau_compact_kernel(SelectParams p, CompactParams cp, int ntau) {
+  if (int(blockIdx.x) < ntau) {  // block-uniform
+    tau_row<AC, KMAX>(p, blockIdx.x);
+  } else {
+    extern __shared__ int sm[];
+    compact_detail::compact_block(cp, sm, int(blockIdx.x) - ntau);
   }
 }
 
@@ -1062,6 +1082,33 @@ hipError_t launch_tau(const SelectParams& p, hipStream_t s) {
     default:
       if (reg) hipLaunchKernelGGL((tau_kernel<kAGen, 32>), grid, dim3(kThreads), 0, s, p);
       else hipLaunchKernelGGL((tau_kernel<kAGen, 0>), grid, dim3(kThreads), 0, s, p);
+      break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_tau_compact(const SelectParams& p, const CompactParams& cp, hipStream_t s) {
+  const size_t rows = size_t(p.d.BH) * p.d.NQ;
+  const int ntau = int((rows + kThreads - 1) / kThreads);
+  const dim3 grid(unsigned(ntau + 2 * cp.BH));
+  const size_t lds = compact_detail::compact_lds_bytes(cp);
+  const bool reg = p.d.k <= 32;  // the row's values fit in registers
+  switch (alpha_class_of(p.d.alpha)) {
+    case kA15:
+      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kA15, 32>), grid, dim3(kThreads), lds, s, p, cp, ntau);
+      else hipLaunchKernelGGL((tau_compact_kernel<kA15, 0>), grid, dim3(kThreads), lds, s, p, cp, ntau);
+      break;
+    case kA20:
+      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kA20, 32>), grid, dim3(kThreads), lds, s, p, cp, ntau);
+      else hipLaunchKernelGGL((tau_compact_kernel<kA20, 0>), grid, dim3(kThreads), lds, s, p, cp, ntau);
+      break;
+    case kA125:
+      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kA125, 32>), grid, dim3(kThreads), lds, s, p, cp, ntau);
+      else hipLaunchKernelGGL((tau_compact_kernel<kA125, 0>), grid, dim3(kThreads), lds, s, p, cp, ntau);
+      break;
+    default:
+      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kAGen, 32>), grid, dim3(kThreads), lds, s, p, cp, ntau);
+      else hipLaunchKernelGGL((tau_compact_kernel<kAGen, 0>), grid, dim3(kThreads), lds, s, p, cp, ntau);
       break;
   }
   return hipGetLastError();

@@ -134,6 +134,9 @@ def kernel_models(B, H, N, d, nnzb, nQB, nKB, k_keep, nsup):
                        bytes=rows * d * ELEM + vis_blocks * tile + rows * k_keep * 4),
         "bounds": dict(bound="hbm", flops=0.0, bytes=BH * N * 4 + BH * nKB * 8),
         "compact": dict(bound="hbm", flops=0.0, bytes=2 * BH * nQB * nKB + csr),
+        # tau and compact in one launch (reference tau mode)
+        "tau_compact": dict(bound="hbm", flops=0.0,
+                            bytes=rows * k_keep * 4 + rows * 4 + 2 * BH * nQB * nKB + csr),
         # the forward's tile bytes are mostly L2-served (its algorithmic byte
         # rate exceeds the HBM peak); its MFMA work is the bound
         "forward": dict(bound="mfma", flops=4.0 * 64 * 64 * d * nnzb,
