@@ -53,8 +53,8 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "259c886bb1fd33fc"
-HBM_TRAFFIC = {'bounds': 1110028, 'select': 145084697, 'tau': 34745367, 'refine': 111252895, 'compact': 2743464, 'forward': 314759480, 'bwd_dq_sparse': 240768230, 'bwd_dkdv_sparse': 287903291}
+HBM_TRAFFIC_SOURCES = "bfeec5c4df6492ca"
+HBM_TRAFFIC = {'bounds': 1110082, 'select': 139729729, 'tau': 34744923, 'tau_compact': 37481537, 'refine': 109657927, 'compact': 2744251, 'forward': 314952705, 'bwd_dq_sparse': 240829579, 'bwd_dkdv_sparse': 288023243}
 
 
 def source_hash() -> str:
