@@ -1,5 +1,6 @@
 // Score pass: scores, exact per-row top-k and block mask (tau follows in
-// tau_kernel, from the sorted top-k values this pass writes).
+// tau_kernel, from the sorted top-k values this pass writes, or in
+// tau_compact_kernel, which builds the CSR lists in the same launch).
 //
 // Reference: build_mask_kernel + insert_topk + entmax_threshold
 // (adasplashattention.cu:35-217), one thread per query that scans every key
@@ -7,8 +8,9 @@
 // 64-row query block of one (batch, head).  During the sweeps the waves
 // split the keys, not the rows: wave w loads keys 16w..16w+15 of each
 // visible key tile straight from L2 into MFMA operand registers (KQuarter,
-// two tiles in flight, no LDS stage and no barrier per tile) and scores
-// them against all 64 rows.  The top-k is found in two sweeps over the
+// two tiles in flight, no barrier per tile; with 16-bit inputs sweep 1
+// reads them through a per-wave LDS ring filled by global_load_lds) and
+// scores them against all 64 rows.  The top-k is found in two sweeps over the
 // visible key blocks instead of by insertion:
 //
 //   sweep 1  every score updates one of 64*R running "class maxima" of its
