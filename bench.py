@@ -53,8 +53,8 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "bfeec5c4df6492ca"
-HBM_TRAFFIC = {'bounds': 1110082, 'select': 139729729, 'tau': 34744923, 'tau_compact': 37481537, 'refine': 109657927, 'compact': 2744251, 'forward': 314952705, 'bwd_dq_sparse': 240829579, 'bwd_dkdv_sparse': 288023243}
+HBM_TRAFFIC_SOURCES = "574b0fc7b9b4c1ab"
+HBM_TRAFFIC = {'bounds': 1110170, 'select': 142820673, 'tau': 34745088, 'tau_compact': 37484285, 'refine': 109670764, 'compact': 2744252, 'forward': 314953218, 'bwd_dq_sparse': 240769369, 'bwd_dkdv_sparse': 287893960}
 
 
 def source_hash() -> str:
