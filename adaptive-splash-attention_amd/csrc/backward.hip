@@ -398,9 +398,10 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dkdv_ke
     T* dv = static_cast<T*>(p.dv) + krow * D;
     for (int db = 0; db < D / 16; ++db)
       for (int r = 0; r < 4; ++r) {
+        // NaN -> 0; an overflowed sum stays +-inf (reference atomics, cu:684-697)
         float vk = scale * ak[db][r], vv = av[db][r];
-        if (!finite(vk)) vk = 0.0f;
-        if (!finite(vv)) vv = 0.0f;
+        if (__builtin_isnan(vk)) vk = 0.0f;
+        if (__builtin_isnan(vv)) vv = 0.0f;
         Elem<T>::store(dk + 16 * db + 4 * g + r, vk);
         Elem<T>::store(dv + 16 * db + 4 * g + r, vv);
       }

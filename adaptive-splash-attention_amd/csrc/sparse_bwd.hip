@@ -865,9 +865,11 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
 
   if (jok) {
     for (int x = 0; x < EL; ++x) {
+      // NaN -> 0; a sum that overflowed stays +-inf, as the reference's
+      // atomic sums do (its host fix-up clamps them, cu:684-697)
       const float vk = p.d.scale * dk[x];
-      dk[x] = finite(vk) ? vk : 0.0f;
-      dv[x] = finite(dv[x]) ? dv[x] : 0.0f;
+      dk[x] = __builtin_isnan(vk) ? 0.0f : vk;
+      dv[x] = __builtin_isnan(dv[x]) ? 0.0f : dv[x];
     }
     for (int c = 0; c < NC; ++c) {
       float k8[E], v8[E];

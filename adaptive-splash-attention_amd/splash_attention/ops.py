@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import warnings
 from dataclasses import dataclass
 
 import torch
@@ -102,6 +103,28 @@ class SplashState:
             for n, t in zip(cls.SUPPORT, ts[7:]):
                 setattr(st, n, t)
         return st
+
+
+def fix_nonfinite(t: torch.Tensor, name: str) -> torch.Tensor:
+    """The reference's host fix-up of a result (adasplashattention.cu:599-606
+    for the output, :684-697 for dQ, dK, dV): NaN elements become 0, and if
+    any element is infinite the whole tensor is clamped to [-100, 100]; each
+    step warns.  Synchronises with the device (two reductions read back), as
+    the reference's ``.item()`` calls do.
+
+    The kernels already zero non-finite outputs and dQ elements, as the
+    reference's kernels do (:335-337, :529-531); a dK or dV sum that
+    overflows stays +-inf, as the reference's atomic sums do, and is what
+    this clamp acts on.
+    """
+    if bool(torch.isnan(t).any()):
+        warnings.warn(f"NaN values detected in {name}, setting to zero", RuntimeWarning,
+                      stacklevel=3)
+        t = t.masked_fill(torch.isnan(t), 0.0)
+    if bool(torch.isinf(t).any()):
+        warnings.warn(f"Inf values detected in {name}, clamping", RuntimeWarning, stacklevel=3)
+        t = torch.clamp(t, -100.0, 100.0)
+    return t
 
 
 def clamp_alpha(alpha: float) -> float:

@@ -187,40 +187,49 @@ def roofline_of(model, ms):
     return r
 
 
+def dense_entmax_fwd_bwd(Q, K, V, dO, alpha, scale, iters=40):
+    """Dense exact alpha-entmax attention fwd+bwd in PyTorch on whatever
+    device the tensors are on (fp32 math, materialised [BH, NQ, NK] scores
+    clamped to [-10, 10] as the reference does, causal by position, tau by
+    `iters` bisection steps on [max - 1, max] of (alpha-1) * scores, exact
+    entmax Jacobian gradient).  Returns (O, dQ, dK, dV)."""
+    import torch
+
+    q, k, v, go = (t.float() for t in (Q, K, V, dO))
+    kt = k.transpose(-1, -2).contiguous()
+    S = torch.matmul(q, kt).mul_(scale).clamp_(-10.0, 10.0)
+    NQ, NK = S.shape[-2:]
+    causal = torch.ones(NQ, NK, device=S.device, dtype=torch.bool).tril_(NK - NQ)
+    z = S.mul_(alpha - 1.0).masked_fill_(~causal, -float("inf"))
+    a = 1.0 / (alpha - 1.0)
+    hi = z.amax(-1, keepdim=True)
+    lo = hi - 1.0
+    for _ in range(iters):
+        mid = 0.5 * (lo + hi)
+        f = (z - mid).clamp_(min=0).pow_(a).sum(-1, keepdim=True) - 1.0
+        pos = f > 0
+        lo = torch.where(pos, mid, lo)
+        hi = torch.where(pos, hi, mid)
+    P = (z - 0.5 * (lo + hi)).clamp_(min=0).pow_(a)
+    P = P / P.sum(-1, keepdim=True)
+    O = torch.matmul(P, v)
+    dP = torch.matmul(go, v.transpose(-1, -2).contiguous())
+    g = torch.where(P > 0, P.pow(2.0 - alpha), torch.zeros_like(P))
+    shift = (g * dP).sum(-1, keepdim=True) / g.sum(-1, keepdim=True)
+    dS = g * (dP - shift)
+    dQ = torch.matmul(dS, k) * scale
+    dK = torch.matmul(dS.transpose(-1, -2).contiguous(), q) * scale
+    dV = torch.matmul(P.transpose(-1, -2).contiguous(), go)
+    return O, dQ, dK, dV
+
+
 def dense_gpu_baseline(Q, K, V, dO, alpha, scale, iters=40, runs=5):
-    """Dense exact alpha-entmax attention fwd+bwd in PyTorch on the GPU (fp32
-    math, materialised [BH, N, N] scores, tau by bisection, exact entmax
-    Jacobian); returns (median, min) ms per fwd+bwd over `runs` runs after
-    one warm-up, and the run count."""
+    """dense_entmax_fwd_bwd on the GPU; returns (median, min) ms per fwd+bwd
+    over `runs` runs after one warm-up, and the run count."""
     import torch
 
     def run():
-        q, k, v, go = (t.float() for t in (Q, K, V, dO))
-        kt = k.transpose(-1, -2).contiguous()
-        S = torch.matmul(q, kt).mul_(scale).clamp_(-10.0, 10.0)
-        N = S.shape[-1]
-        causal = torch.ones(N, N, device=S.device, dtype=torch.bool).tril_()
-        z = S.mul_(alpha - 1.0).masked_fill_(~causal, -float("inf"))
-        a = 1.0 / (alpha - 1.0)
-        hi = z.amax(-1, keepdim=True)
-        lo = hi - 1.0
-        for _ in range(iters):
-            mid = 0.5 * (lo + hi)
-            f = (z - mid).clamp_(min=0).pow_(a).sum(-1, keepdim=True) - 1.0
-            pos = f > 0
-            lo = torch.where(pos, mid, lo)
-            hi = torch.where(pos, hi, mid)
-        P = (z - 0.5 * (lo + hi)).clamp_(min=0).pow_(a)
-        P = P / P.sum(-1, keepdim=True)
-        O = torch.matmul(P, v)
-        dP = torch.matmul(go, v.transpose(-1, -2).contiguous())
-        g = torch.where(P > 0, P.pow(2.0 - alpha), torch.zeros_like(P))
-        shift = (g * dP).sum(-1, keepdim=True) / g.sum(-1, keepdim=True)
-        dS = g * (dP - shift)
-        dQ = torch.matmul(dS, k) * scale
-        dK = torch.matmul(dS.transpose(-1, -2).contiguous(), q) * scale
-        dV = torch.matmul(P.transpose(-1, -2).contiguous(), go)
-        return O, dQ, dK, dV
+        return dense_entmax_fwd_bwd(Q, K, V, dO, alpha, scale, iters)
 
     run()
     torch.cuda.synchronize()
@@ -231,6 +240,40 @@ def dense_gpu_baseline(Q, K, V, dO, alpha, scale, iters=40, runs=5):
         torch.cuda.synchronize()
         times.append((time.perf_counter() - t0) * 1e3)
     return statistics.median(times), min(times), runs
+
+
+def dense_cpu_baseline(warmup=3, trials=10):
+    """The primary CPU baseline of the build's plan: dense exact alpha-entmax
+    attention fwd+bwd in PyTorch (dense_entmax_fwd_bwd) on the host CPU at
+    BASELINE configs[0] (c1) and configs[1] (c2), fp32, Q/K/V ~ N(0,1)
+    (seed 0) and dO ~ N(0,1) (seed 1), with every core of the host and with
+    one thread; median and min of `trials` runs after `warmup` warm-ups
+    each.  The reference itself has no CPU path (adasplashattention.cu:543)."""
+    import torch
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    prev = torch.get_num_threads()
+    res = {"threads": threads, "host": host_cpu(), "kind": "dense PyTorch",
+           "what": "dense exact alpha-entmax fwd+bwd in PyTorch on the host CPU, fp32, "
+                   "[BH, N, N] scores, 40 bisection steps, exact entmax Jacobian; median "
+                   f"of {trials} runs after {warmup} warm-ups"}
+    try:
+        for name, (B, H, N) in {"c1": (1, 2, 256), "c2": (2, 8, 1024)}.items():
+            g = torch.Generator().manual_seed(0)
+            Q, K, V = (torch.randn(B, H, N, 64, generator=g) for _ in range(3))
+            dO = torch.randn(B, H, N, 64, generator=torch.Generator().manual_seed(1))
+            fn = lambda: dense_entmax_fwd_bwd(Q, K, V, dO, 1.5, 0.125)
+            entry = {"shape": f"B={B} H={H} N={N} d=64 fp32 alpha=1.5 causal, fwd+bwd"}
+            for label, n in (("all_cores", threads), ("one_thread", 1)):
+                torch.set_num_threads(n)
+                med, mn = _time(fn, warmup, trials)
+                entry[label] = {"ms": round(med * 1e3, 3), "min_ms": round(mn * 1e3, 3),
+                                "threads": n,
+                                "tflops": round(effective_flops(B, H, N, 64) / med / 1e12, 6)}
+            res[name] = entry
+    finally:
+        torch.set_num_threads(prev)
+    return res
 
 
 def _oracle_run(heads, N, d, k, alpha, scale, seed=0):
@@ -279,6 +322,8 @@ def cpu_baseline(heads=16, warmup=3, trials=10):
                      f"N={N} d={d} k={k}, {threads} OpenMP threads, median of {trials} trials "
                      f"after {warmup} warm-ups: {med:.3f} s (min {mn:.3f} s)",
            "ms_per_step_scaled": round(med * 1e3 * 64 / heads, 1),
+           "scaled": f"value and ms_per_step_scaled scale the {heads}-slice sample to the "
+                     f"64 slices of the headline step (x{64 / heads:g})",
            "host": host_cpu()}
     # one thread, one slice (the OpenMP loops are over slices)
     from oracle import oracle as orc
@@ -297,6 +342,7 @@ def cpu_baseline(heads=16, warmup=3, trials=10):
         cfgs[name] = {"ms": round(mc * 1e3, 3), "min_ms": round(mnc * 1e3, 3),
                       "shape": f"BH={BH} N={Nc} d=64 fp32 k={kc} alpha=1.5 causal, fwd+bwd"}
     out["configs"] = cfgs
+    out["dense_pytorch"] = dense_cpu_baseline(warmup, trials)
     return out
 
 

@@ -397,7 +397,8 @@ void asao_forward(const real *Q, const real *K, const real *V, const int32_t *qi
  * Backward for given taus and query-major CSR.  dQ, dK, dV are written
  * (zeroed first).  mode 0: entmax-Jacobian gradient; mode 1: the
  * gradient of the reference kernel (:343-535).  Non-finite contributions
- * are dropped and non-finite results set to zero, as the reference does.
+ * are dropped and non-finite dQ set to zero, as the reference does; dK and
+ * dV keep an overflowed (+-inf) sum and zero NaN.
  */
 void asao_backward(const real *Q, const real *K, const real *V, const int32_t *qidx,
                    const int32_t *kidx, const real *dO, int BH, int NQ, int NK, int d,
@@ -506,10 +507,13 @@ void asao_backward(const real *Q, const real *K, const real *V, const int32_t *q
             for (int j = 0; j < NK; ++j) {
                 const long kj = (long)bh * NK + j;
                 for (int t = 0; t < d; ++t) {
+                    /* a sum beyond the float range is +-inf, as the
+                     * reference's fp32 atomic sums give (:477, :518); its
+                     * host fix-up (:684-697) then clamps it */
                     real gkv = (real)dk_acc[(size_t)j * d + t];
                     real gvv = (real)dv_acc[(size_t)j * d + t];
-                    dK[kj * d + t] = rfinite(gkv) ? gkv : (real)0;
-                    dV[kj * d + t] = rfinite(gvv) ? gvv : (real)0;
+                    dK[kj * d + t] = isnan(gkv) ? (real)0 : gkv;
+                    dV[kj * d + t] = isnan(gvv) ? (real)0 : gvv;
                 }
             }
         }

@@ -218,6 +218,22 @@ def backward(Q, K, V, Q_idx, K_idx, dO, alpha: float, sm_scale: float, taus, q_p
     return dQ, dK, dV
 
 
+def host_fixup(x: np.ndarray) -> tuple[np.ndarray, bool, bool]:
+    """The reference's host fix-up of one result tensor
+    (source/adasplashattention.cu:599-606 for Out, :684-697 for dQ, dK, dV):
+    NaN elements become 0 (``masked_fill_``); then, if any element is
+    infinite, the whole tensor is clamped to [-100, 100] (``torch::clamp``).
+    Returns (fixed array, had NaN, had Inf)."""
+    x = np.array(x, copy=True)
+    nan = bool(np.isnan(x).any())
+    if nan:
+        x[np.isnan(x)] = 0
+    inf = bool(np.isinf(x).any())
+    if inf:
+        x = np.clip(x, -100.0, 100.0)
+    return x, nan, inf
+
+
 def set_num_threads(n: int) -> int:
     """Set the OpenMP thread count of both back ends; returns the previous
     count of the f32 one."""

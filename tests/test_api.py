@@ -113,3 +113,50 @@ def test_kernel_layout_pads(d, dk, dtype):
     assert back.shape == Q.shape and back.dtype == dtype
     back.sum().backward()
     assert torch.equal(Q.grad, torch.full_like(Q, 2))
+
+
+def test_reference_order_defaults_are_the_compiled_references():
+    """forward/backward default to the compiled reference's K_KEEP = 8 and
+    BLOCK_M = 32 (adasplashattention.cu:8-9, :17-19) and apply its host
+    fix-up (:599-606, :684-697) unless told not to."""
+    import inspect
+
+    for fn in (sa.forward, sa.backward):
+        sig = inspect.signature(fn).parameters
+        assert sig["k_keep"].default == 8
+        assert sig["block_m"].default == 32
+        assert sig["fix_nonfinite"].default is True
+    assert inspect.signature(sa.backward).parameters["grad_mode"].default == "reference"
+
+
+def test_host_fixup_follows_the_reference():
+    """ops.fix_nonfinite on host tensors against the oracle's restatement of
+    cu:599-606 / :684-697 and hand-written cases: NaN -> 0 with a warning;
+    any inf clamps the whole tensor to [-100, 100] with a warning; finite
+    tensors pass unchanged and silently."""
+    import warnings
+
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    fin = torch.tensor([1.0, -250.0, 3.0])
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert torch.equal(ops.fix_nonfinite(fin, "dK"), fin)   # no inf: no clamp
+    nan = torch.tensor([float("nan"), -250.0, 3.0])
+    with pytest.warns(RuntimeWarning, match="NaN values detected in dQ, setting to zero"):
+        got = ops.fix_nonfinite(nan, "dQ")
+    assert got.tolist() == [0.0, -250.0, 3.0]
+    inf = torch.tensor([float("inf"), -250.0, 3.0, float("nan"), -float("inf")])
+    with pytest.warns(RuntimeWarning) as rec:
+        got = ops.fix_nonfinite(inf, "dV")
+    msgs = [str(r.message) for r in rec]
+    assert msgs == ["NaN values detected in dV, setting to zero",
+                    "Inf values detected in dV, clamping"]
+    assert got.tolist() == [100.0, -100.0, 3.0, 0.0, -100.0]
+    for x in (fin, nan, inf):
+        want, _, _ = orc.host_fixup(x.numpy())
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")
+            np.testing.assert_array_equal(ops.fix_nonfinite(x, "out").numpy(), want)

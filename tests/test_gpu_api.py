@@ -33,22 +33,88 @@ def test_module_autograd_matches_oracle(dev):
     assert_close("dV", np32(v.grad), gv, 1e-5)
 
 
-def test_reference_style_entry_points(dev):
+def _magnets(BH, N, d, seed=3):
+    """Half h of the queries (32 rows) has its top-2 keys in key block h % 4
+    (every key visible), so the two 32-row halves of each 64-row block
+    select different key blocks: 32-row and 64-row mask blocks then give
+    outputs that differ by O(1)."""
+    rng = np.random.default_rng(seed)
+    Q = rng.normal(size=(BH, N, d)) * 0.1
+    K = rng.normal(size=(BH, N, d)) * 0.1
+    V = rng.normal(size=(BH, N, d))
+    dO = rng.normal(size=(BH, N, d))
+    for h in range(N // 32):
+        Q[:, 32 * h:32 * h + 32, h] += 1.0
+        K[:, 64 * (h % 4) + h, h] = 5.0
+        K[:, 64 * (h % 4) + 8 + h, h] = 4.0
+    t = [torch.from_numpy(x.astype(np.float32)).reshape(1, BH, N, d) for x in (Q, K, V, dO)]
+    qi = torch.full((BH, N), N - 1, dtype=torch.int32)
+    return (*t, qi, causal_idx(BH, N))
+
+
+@pytest.mark.parametrize("case", ["c1", "magnets"])
+def test_reference_style_entry_points(dev, case):
     """sa.forward / sa.backward take the reference's argument order
-    (adasplashattention.cu:537-541, :611-616) and return its gradient."""
-    print("[api] reference-style forward/backward", flush=True)
-    B, H, N, d = 1, 2, 192, 64
-    Q, K, V, dO = make_inputs(B, H, N, N, d, seed=4)
-    idx = causal_idx(B * H, N)
-    out = sa.forward(Q.to(dev), K.to(dev), V.to(dev), idx.to(dev), idx.to(dev), 0.125, 1.5)
-    dQ, dK, dV = sa.backward(Q.to(dev), K.to(dev), V.to(dev), idx.to(dev), idx.to(dev), 0.125,
-                             1.5, dO.to(dev))
-    fw, (gq, gk, gv) = orc.attention(np32(Q), np32(K), np32(V), idx.numpy(), idx.numpy(),
-                                     np32(dO), 1.5, 0.125, 8, mode=orc.GRAD_REFERENCE)
+    (adasplashattention.cu:537-541, :611-616), default to its compiled
+    BLOCK_M = 32 (:8-9), and return its gradient.  On the "magnets" inputs
+    a 64-row default would be off by O(1) (checked against the oracle)."""
+    print(f"[api] reference-style forward/backward {case}", flush=True)
+    if case == "c1":
+        B, H, N, d = 1, 2, 192, 64
+        Q, K, V, dO = make_inputs(B, H, N, N, d, seed=4)
+        qi = ki = causal_idx(B * H, N)
+        kw, k = {}, 8          # the reference's compiled K_KEEP
+    else:
+        Q, K, V, dO, qi, ki = _magnets(2, 256, 64)
+        kw, k = {"k_keep": 2}, 2
+    args = (Q.to(dev), K.to(dev), V.to(dev), qi.to(dev), ki.to(dev), 0.125, 1.5)
+    out = sa.forward(*args, **kw)
+    dQ, dK, dV = sa.backward(*args, dO.to(dev), **kw)
+    fw, (gq, gk, gv) = orc.attention(np32(Q), np32(K), np32(V), qi.numpy(), ki.numpy(),
+                                     np32(dO), 1.5, 0.125, k, mode=orc.GRAD_REFERENCE,
+                                     block_m=32)
     assert_close("out", np32(out), fw.out, 1e-5)
     assert_close("dQ", np32(dQ), gq, 1e-5)
     assert_close("dK", np32(dK), gk, 1e-5)
     assert_close("dV", np32(dV), gv, 1e-5)
+    if case == "magnets":
+        fw64 = orc.forward(np32(Q), np32(K), np32(V), qi.numpy(), ki.numpy(), 1.5, 0.125, k,
+                           block_m=64)
+        assert float(np.abs(fw64.out - fw.out).max()) > 1e-2
+
+
+def test_reference_host_fixup_clamps_overflowed_dv(dev):
+    """The reference's host fix-up (adasplashattention.cu:684-697): a dV sum
+    that overflows (fp32 atomics there, fp32 registers here) is +inf, and
+    any inf clamps the whole tensor to [-100, 100] with a warning.  Rows
+    0-3 see only key 0 (weight 1 each), and dO's column 0 is 3e38, so
+    dV[key 0, 0] = 4 * 3e38 overflows; V is scaled by 1e-6 so that
+    dp = dO . v stays finite and dQ, dK are ordinary (large) numbers."""
+    print("[api] host fix-up: overflowing dV", flush=True)
+    B, H, N, d = 1, 1, 128, 64
+    Q, K, V, dO = make_inputs(B, H, N, N, d, seed=11)
+    V = V * 1e-6
+    dO[..., 0] = 3e38
+    qi = causal_idx(1, N)
+    qi[:, :4] = 0
+    ki = causal_idx(1, N)
+    args = (Q.to(dev), K.to(dev), V.to(dev), qi.to(dev), ki.to(dev), 0.125, 1.5)
+    with pytest.warns(RuntimeWarning, match="Inf values detected in dV, clamping"):
+        dQ, dK, dV = sa.backward(*args, dO.to(dev))
+    assert float(dV.abs().max()) <= 100.0 and torch.isfinite(dV).all()
+    fw, (gq, gk, gv) = orc.attention(np32(Q), np32(K), np32(V), qi.numpy(), ki.numpy(),
+                                     np32(dO), 1.5, 0.125, 8, mode=orc.GRAD_REFERENCE,
+                                     block_m=32)
+    assert np.isinf(gv).any()          # the oracle's sum overflows too
+    want, nan, inf = orc.host_fixup(gv)
+    assert inf and not nan
+    assert_close("dV (fixed up)", np32(dV), want, 1e-5)
+    assert_close("dQ", np32(dQ), gq, 1e-5)
+    assert_close("dK", np32(dK), gk, 1e-5)
+    # opting out returns the raw sums: the overflowed element is +inf
+    raw = sa.backward(*args, dO.to(dev), fix_nonfinite=False)[2]
+    assert bool(torch.isinf(raw).any())
+    assert torch.equal(torch.clamp(raw, -100, 100), dV)
 
 
 def test_reference_style_default_scale_uses_callers_head_dim(dev):
@@ -67,7 +133,7 @@ def test_reference_style_default_scale_uses_callers_head_dim(dev):
     for x, y in zip(ga, gb):
         assert torch.equal(x, y)
     fw, _ = orc.attention(np32(Q), np32(K), np32(V), idx.cpu().numpy(), idx.cpu().numpy(),
-                          np32(dO), 1.5, d ** -0.5, 8, mode=orc.GRAD_REFERENCE)
+                          np32(dO), 1.5, d ** -0.5, 8, mode=orc.GRAD_REFERENCE, block_m=32)
     assert_close("out", np32(a), fw.out, 1e-5)
 
 
@@ -127,7 +193,8 @@ def test_nan_scores_follow_reference_clamp(dev):
     idx = causal_idx(1, N)
     out = sa.forward(Q.to(dev), K.to(dev), V.to(dev), idx.to(dev), idx.to(dev), 0.125, 1.5)
     assert torch.isfinite(out).all()
-    fw = orc.forward(np32(Q), np32(K), np32(V), idx.numpy(), idx.numpy(), 1.5, 0.125, 8)
+    fw = orc.forward(np32(Q), np32(K), np32(V), idx.numpy(), idx.numpy(), 1.5, 0.125, 8,
+                     block_m=32)
     assert_close("out", np32(out), fw.out, 1e-5)
 
 

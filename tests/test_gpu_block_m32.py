@@ -126,14 +126,21 @@ def test_attention_block_m32_matches_oracle(dev, case, mode, support):
         assert float((out64 - out).abs().max()) > 1e-2
 
 
+TOL16 = {torch.bfloat16: 2e-2, torch.float16: 4e-3}
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("mode", ["entmax", "reference"])
-def test_attention_block_m32_bf16_magnets(dev, mode):
-    """bf16 at d = 64 runs the paired forward; with 32-row masks a wave's
-    half drops the union tiles its mask row lacks (its clip bounds set to
-    -0 there).  The magnets make every pair of halves differ."""
-    print(f"[bm32] attention magnets bf16 {mode}", flush=True)
-    Q, K, V, dO, qi, ki = _magnets(2, 256, 64)
-    Q, K, V = (t.to(torch.bfloat16) for t in (Q, K, V))
+def test_attention_block_m32_16bit_magnets(dev, mode, dtype, d):
+    """16-bit inputs: at d = 64 the paired forward (bf16, and fp16 with its
+    P scaling), at d = 128 the one-block forward; with 32-row masks a
+    wave's half drops the union tiles its mask row lacks (its clip bounds
+    set to -0 there).  The magnets make every pair of halves differ."""
+    print(f"[bm32] attention magnets {dtype} d={d} {mode}", flush=True)
+    Q, K, V, dO, qi, ki = _magnets(2, 256, d)
+    Q, K, V = (t.to(dtype) for t in (Q, K, V))
+    tol = TOL16[dtype]
     alpha, scale, k = 1.5, 0.125, 2
     q, kk, v, qd, kd = sa.ops.check_inputs(Q.to(dev), K.to(dev), V.to(dev), qi.to(dev),
                                            ki.to(dev))
@@ -144,9 +151,9 @@ def test_attention_block_m32_bf16_magnets(dev, mode):
     own, at, og = oracle_at_gpu_tau(np32(Q), np32(K), np32(V), np32(dO), qi.numpy(), ki.numpy(),
                                     alpha, scale, k, st.taus.cpu().numpy(), m, block_m=32)
     np.testing.assert_array_equal(st.mask.cpu().numpy(), own.mask)
-    assert_close("out", np32(out), at.out, 2e-2)
+    assert_close("out", np32(out), at.out, tol)
     for name, g, w in zip(("dQ", "dK", "dV"), grads, og):
-        assert_close(name, np32(g), w, 2e-2)
+        assert_close(name, np32(g), w, tol)
     out64, _ = sa.ops.splash_forward(q, kk, v, qd, kd, alpha, k, scale, with_support=False)
     assert float((out64.float() - out.float()).abs().max()) > 1e-2
 

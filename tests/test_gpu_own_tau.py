@@ -10,8 +10,9 @@ recurrence one step apart on a few rows.  So:
     max-norm;
   - every key outside the supports of the rows that do not match: dK and
     dV within 1e-5 (a key's gradient sums over the rows that weight it);
-  - the rows that do not match are counted, and their tau difference and
-    output / dQ errors printed.
+  - the rows that do not match are counted and bounded: at most 2 (c1) or
+    16 (c2) of them, tau within 1e-4, and their out / dQ, and the dK / dV
+    of the keys they weight, within 1e-4.
 Block masks are compared exactly.  Both gradient modes.
 """
 import numpy as np
@@ -89,13 +90,24 @@ def test_parity_at_oracle_tau(dev, cfg, mode):
     clean = ~tainted
     assert float(e_dk[clean].max()) <= 1e-5, f"dK {float(e_dk[clean].max()):.2e}"
     assert float(e_dv[clean].max()) <= 1e-5, f"dV {float(e_dv[clean].max()):.2e}"
+    dtau = float(np.abs(gt - ot).max())
     msg = (f"[own tau] {cfg} {mode}: {nbad} of {match.size} rows with tau off by > 1e-6 "
-           f"(max |dtau| {float(np.abs(gt - ot).max()):.2e}); {int(tainted.sum())} of "
+           f"(max |dtau| {dtau:.2e}); {int(tainted.sum())} of "
            f"{tainted.size} keys in their supports")
     if nbad:
         msg += (f"; on those rows out err {float(e_out[~match].max()):.2e}, "
-                f"dQ err {float(e_dq[~match].max()):.2e}")
+                f"dQ err {float(e_dq[~match].max()):.2e}; on those keys dK err "
+                f"{float(e_dk[tainted].max()):.2e}, dV err {float(e_dv[tainted].max()):.2e}")
     print(msg, flush=True)
-    # the non-matching rows are the recurrence's discontinuity, not a drift
-    assert nbad <= max(2, match.size // 200)
-    assert float(np.abs(gt - ot).max()) <= 1e-3
+    # The non-matching rows are the recurrence's one-step discontinuity, not
+    # a drift: few of them (observed 0 at c1, 7 at c2), tau one small Halley
+    # step apart (observed 3.05e-5), and their outputs and gradients within
+    # 1e-4 (observed 2.1e-5 out, 3.7e-5 dQ).  A regression that made the
+    # discontinuity several times more common or larger fails here.
+    assert nbad <= {"c1": 2, "c2": 16}[cfg], f"{nbad} rows off the oracle's tau"
+    assert dtau <= 1e-4, f"max |dtau| {dtau:.2e}"
+    if nbad:
+        assert float(e_out[~match].max()) <= 1e-4, f"out on tau-mismatched rows"
+        assert float(e_dq[~match].max()) <= 1e-4, f"dQ on tau-mismatched rows"
+        assert float(e_dk[tainted].max()) <= 1e-4, f"dK on their support keys"
+        assert float(e_dv[tainted].max()) <= 1e-4, f"dV on their support keys"

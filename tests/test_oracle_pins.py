@@ -440,3 +440,30 @@ def test_key_block_grads_match_oracle_backward(mode, alpha, causal, block_m):
                                     block_m=block_m)
         np.testing.assert_allclose(dK, gk[bh][rows], rtol=1e-9, atol=1e-12 * np.abs(gk).max())
         np.testing.assert_allclose(dV, gv[bh][rows], rtol=1e-9, atol=1e-12 * np.abs(gv).max())
+
+
+def test_overflowed_key_sum_is_inf_and_host_fixup_clamps():
+    """dV of a key is the sum over the rows that weight it of P * dO
+    (cu:473-479).  Two rows that see only key 0 weight it with P = 1 (one
+    visible key: p / (p + EPS) rounds to 1); with dO[:, 0] = 3e38 its sum
+    6e38 is beyond the float range: +inf, as the reference's fp32 atomic
+    sum gives; dQ and dK stay finite.  The host fix-up
+    (cu:684-697) then clamps the whole dV to [-100, 100]."""
+    d = 64
+    rng = np.random.default_rng(0)
+    Q = rng.normal(size=(1, 2, d)).astype(np.float32)
+    K = rng.normal(size=(1, 1, d)).astype(np.float32)
+    V = rng.normal(size=(1, 1, d)).astype(np.float32)
+    dO = rng.normal(size=(1, 2, d)).astype(np.float32)
+    dO[:, :, 0] = 3e38
+    qi = np.zeros((1, 2), np.int32)
+    ki = np.zeros((1, 1), np.int32)
+    for mode in (orc.GRAD_ENTMAX, orc.GRAD_REFERENCE):
+        _, (dQ, dK, dV) = orc.attention(Q, K, V, qi, ki, dO, 1.5, 0.125, 8, mode=mode)
+        assert dV[0, 0, 0] == np.inf
+        np.testing.assert_allclose(dV[0, 0, 1:], dO[0, 0, 1:] + dO[0, 1, 1:], rtol=1e-6)
+        assert np.isfinite(dK).all() and np.isfinite(dQ).all()
+        fixed, nan, inf = orc.host_fixup(dV)
+        assert inf and not nan
+        assert fixed[0, 0, 0] == 100.0
+        np.testing.assert_array_equal(fixed[0, 0, 1:], np.clip(dV[0, 0, 1:], -100, 100))

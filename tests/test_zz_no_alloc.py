@@ -58,3 +58,52 @@ def test_noalloc_rejects_problems_above_its_workspace(dev):
     rc = lib.asa_forward_noalloc(p, None, None, None, None, None, None, None, None)
     assert rc == _lib.ASA_ERR_UNSUPPORTED
     assert "asa_forward_noalloc holds" in lib.asa_last_error().decode()
+
+
+def test_noalloc_forward_replays_in_a_hip_graph(dev):
+    """The stated use of asa_forward_noalloc: capture it in a HIP graph
+    (torch.cuda.CUDAGraph) after a first call outside capture (which looks
+    up the array's address), then replay it three times, each on new inputs
+    copied into the captured buffers and with eager work between replays;
+    every replay equals an eager asa_forward call on the same inputs bit for
+    bit.  The forward records no hipMemsetAsync (its first kernel clears
+    what must start at zero)."""
+    from splash_attention import ops
+
+    B, H, N, d, k, alpha, scale = 1, 4, 512, 64, 16, 1.5, 0.125
+    print(f"[noalloc] graph capture B={B} H={H} N={N} d={d} bf16 k={k}", flush=True)
+    Q, K, V, _ = (t.to(dev) for t in make_inputs(B, H, N, N, d, seed=5, dtype=torch.bfloat16))
+    idx = causal_idx(B * H, N).to(dev)
+    sQ, sK, sV = Q.clone(), K.clone(), V.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ops.splash_forward(sQ, sK, sV, idx, idx, alpha, k, scale, with_topk=True, noalloc=True)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gout, gst = ops.splash_forward(sQ, sK, sV, idx, idx, alpha, k, scale, with_topk=True,
+                                       noalloc=True)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        nQ, nK, nV, _ = make_inputs(B, H, N, N, d, seed=40 + rep, dtype=torch.bfloat16)
+        sQ.copy_(nQ)
+        sK.copy_(nK)
+        sV.copy_(nV)
+        graph.replay()
+        torch.cuda.synchronize()
+        want_out, want = ops.splash_forward(sQ, sK, sV, idx, idx, alpha, k, scale,
+                                            with_topk=True)
+        torch.cuda.synchronize()
+        assert torch.equal(gout.view(torch.int16), want_out.view(torch.int16)), f"replay {rep}"
+        for name in ("taus", "norms", "mask", "q_ptr", "q_list", "k_ptr", "k_list",
+                     "topk_idx", "topk_val", "status"):
+            a, b = getattr(gst, name), getattr(want, name)
+            if a.dtype.is_floating_point:
+                a, b = a.view(torch.int32), b.view(torch.int32)
+            assert torch.equal(a, b), f"replay {rep}: {name}"
+        for bh in range(B * H):
+            n = int(want.q_ptr[bh, -1])
+            assert torch.equal(gst.sup_mask[bh, :n], want.sup_mask[bh, :n]), f"sup_mask {bh}"
+    del graph
