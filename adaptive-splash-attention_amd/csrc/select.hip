@@ -317,7 +317,11 @@ template <typename T, int D> struct KQuarter16 {
   V8 a[D / 32];
   // Keys >= NK read key 0 instead: they lie in partially visible tiles,
   // where the visibility test discards their scores, so no zeroing (and no
-  // wait for the load where it is issued) is needed.
+  // wait for the load where it is issued) is needed.  (This register path
+  // loads 16 half rows per instruction, a third of the L2 rate of whole-row
+  // loads; a whole-row load with the operands rebuilt by two DPP row
+  // rotations per register measured the same sweep time, which the
+  // candidate appends, not the loads, set.)
   __device__ __forceinline__ void load(const T* Kb, int key, int NK, int g) {
     const T* src = Kb + size_t(key < NK ? key : 0) * D + 8 * g;
     for (int s = 0; s < D / 32; ++s) a[s] = *reinterpret_cast<const V8*>(src + 32 * s);
@@ -547,13 +551,13 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
       fetch(kq[1], ent[1]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    for (int i0 = 0; i0 < nvis; i0 += U) {
-      static_for<0, U>([&](auto uc) {
-        constexpr int u = decltype(uc)::value;
-        const int i = i0 + u;
-        const int e = ent[u & 1];
-        f32x4 acc[4];
-        if constexpr (MODE == kGivenScores) {
+    if constexpr (MODE == kGivenScores) {
+      for (int i0 = 0; i0 < nvis; i0 += U) {
+        static_for<0, U>([&](auto uc) {
+          constexpr int u = decltype(uc)::value;
+          const int i = i0 + u;
+          const int e = ent[u & 1];
+          f32x4 acc[4];
           const int kb0 = (e & 0xffffff) * kBlock + 16 * w + 4 * g;
           for (int cb = 0; cb < 4; ++cb)
             for (int r = 0; r < 4; ++r) {
@@ -563,41 +567,75 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
                                : 0.0f;
             }
           ent[u & 1] = entry(i + 2 < nvis ? i + 2 : nvis - 1);
-        } else {
-          kq[u & 1].product(acc, qf);
-          ent[u & 1] = entry(i + 2 < nvis ? i + 2 : nvis - 1);
-          fetch(kq[u & 1], ent[u & 1]);
-        }
-        finish(uc, i, e, acc, body);
-      });
+          finish(uc, i, e, acc, body);
+        });
+      }
+    } else {
+      // Software-pipelined by one tile: the products of tile i + 1 are
+      // issued before tile i's scores are used, so the matrix unit works
+      // under tile i's filter and candidate appends (the appends wait on
+      // LDS).  accs[i & 1] holds tile i's scores; kq[j & 1] holds tile j's
+      // operands, fetched two steps before its products.  The last step's
+      // products (tile nvis, a repeat of the list's last tile) are unused.
+      f32x4 accs[2][4];
+      kq[0].product(accs[0], qf);
+      int ecur = ent[0];
+      ent[0] = entry(2 < nvis ? 2 : nvis - 1);
+      fetch(kq[0], ent[0]);
+      for (int i0 = 0; i0 < nvis; i0 += U) {
+        static_for<0, U>([&](auto uc) {
+          constexpr int u = decltype(uc)::value;
+          const int i = i0 + u;
+          const int enext = ent[(u + 1) & 1];
+          kq[(u + 1) & 1].product(accs[(u + 1) & 1], qf);
+          ent[(u + 1) & 1] = entry(i + 3 < nvis ? i + 3 : nvis - 1);
+          fetch(kq[(u + 1) & 1], ent[(u + 1) & 1]);
+          finish(uc, i, ecur, accs[u & 1], body);
+          ecur = enext;
+        });
+      }
     }
   };
   // Sweep 1 (16-bit inputs) reads its K quarters through a ring in LDS
   // filled by global_load_lds (the loads in flight hold no VGPRs, so each
   // wave keeps kRing tiles in flight instead of two).  The ring occupies
   // the candidate lists' and value scratch's bytes, which sweep 1 leaves
-  // unused; each wave owns kRing slots of one wave quarter (16 keys x D,
-  // lane L's 16-byte chunk s at slot + 1024 s + 16 L, the order
-  // global_load_lds writes a wave's 64 chunks in).  The compiler does not
-  // order LDS reads after the DMA that fills them, so the waits are
-  // explicit: vmcnt before a slot is read (the (kRing - 1) younger tiles'
-  // loads may stay in flight), lgkmcnt(0) before a slot is refilled.
-  constexpr int kCh = D / 32;  // 16-byte chunks per lane and tile
+  // unused; each wave owns kRing slots of one wave quarter (16 keys x D
+  // bytes of 2-byte elements, row-major).  The quarter's rows are
+  // contiguous in memory, and each DMA instruction reads whole rows (8 rows
+  // of 128 bytes at D = 64, 4 of 256 at D = 128): a load of 16 half rows,
+  // the MFMA operand layout, streams from L2 at about a third of the rate
+  // (measured at the headline shape: 8.5 against 28 TB/s).  global_load_lds
+  // puts lane L's 16 bytes at the instruction's base + 16 L, so lane L
+  // fetches the chunk that belongs at that place: row r's chunk x is stored
+  // at chunk x ^ sw(r), which makes the operand reads (16 rows at one chunk
+  // per 16 lanes) fall in distinct banks.  The compiler does not order LDS
+  // reads after the DMA that fills them, so the waits are explicit: vmcnt
+  // before a slot is read (the (kRing - 1) younger tiles' loads may stay in
+  // flight), lgkmcnt(0) before a slot is refilled.
+  constexpr int kCh = D / 32;              // DMA instructions (and MFMA k steps) per quarter
   constexpr int kSlot = kWave * 16 * kCh;  // bytes per wave and tile
+  constexpr int kCpr = D / 8;              // 16-byte chunks per row
+  constexpr int kRpi = kWave / kCpr;       // rows per DMA instruction
+  auto qsw = [](int r) { return D == 64 ? (r >> 1) & 7 : r & 15; };
   constexpr int kRing = ring_tiles<D, R>();
   constexpr bool kRingSweep = kTiles && is_half<T>;
   auto sweep_ring = [&](auto u_tag, auto&& body) {
     constexpr int U = decltype(u_tag)::value;
     if (nvis == 0) return;  // block-uniform
     unsigned char* ringw = smem + w * kRing * kSlot;  // this wave's slots
+    // lane L of instruction j: quarter row r = kRpi j + L / kCpr, stored
+    // chunk L % kCpr, fetched chunk (L % kCpr) ^ sw(r)
     auto dma = [&](int slot, int e) __attribute__((always_inline)) {
-      const int key = (e & 0xffffff) * kBlock + kq0;
-      const T* src = Kb + size_t(key < NK ? key : 0) * D + 8 * g;
+      const int kq = (e & 0xffffff) * kBlock + 16 * w;  // the quarter's first key
       unsigned char* dst = ringw + slot * kSlot;
-      for (int s = 0; s < kCh; ++s)
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + 32 * s),
-                                         (__attribute__((address_space(3))) void*)(dst + s * kWave * 16),
+      for (int j = 0; j < kCh; ++j) {
+        const int r = kRpi * j + L / kCpr, key = kq + r;
+        const T* src = Kb + size_t(key < NK ? key : 0) * D + 8 * ((L % kCpr) ^ qsw(r));
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                         (__attribute__((address_space(3))) void*)(dst + j * kWave * 16),
                                          16, 0, 0);
+      }
     };
     // The Q fragments' loads are waited for here, by an s_waitcnt the
     // compiler sees: otherwise its wait for them before the first product
@@ -612,8 +650,10 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kRing - 1) * kCh) : "memory");
         KQuarter<T, D> kq;
         using A = std::remove_reference_t<decltype(kq.a[0])>;
+        // operand s of lane (c, g): quarter row c, chunk 4 s + g
         for (int s = 0; s < kCh; ++s)
-          kq.a[s] = *reinterpret_cast<const A*>(ringw + slot * kSlot + s * kWave * 16 + 16 * L);
+          kq.a[s] = *reinterpret_cast<const A*>(ringw + slot * kSlot + c * (16 * kCpr) +
+                                                16 * ((4 * s + g) ^ qsw(c)));
         f32x4 acc[4];
         kq.product(acc, qf);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -723,7 +763,10 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
     // candidates then park their 16 values in their LDS scratch and append
     // one candidate per round (LDS atomic on the row's count), so the wave
     // runs as many rounds as its busiest lane has candidates (about two at
-    // the headline shape) instead of visiting every slot.
+    // the headline shape) instead of visiting every slot.  (Storing every
+    // candidate straight from its register instead, one atomic per row and
+    // 16 predicated stores, measured 1.5 times slower: the predicated
+    // stores cost more VALU than the LDS round trips they remove.)
     auto collect = [&](int kb0, uint32_t visb, f32x4 (&acc)[4], auto later) {
       // bit 15 - (4 cb + r) <- sign of v - fl: set where v < fl, so that
       // the complement marks !(v < fl) (NaN differences have a clear sign
