@@ -53,8 +53,8 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "574b0fc7b9b4c1ab"
-HBM_TRAFFIC = {'bounds': 1110170, 'select': 142820673, 'tau': 34745088, 'tau_compact': 37484285, 'refine': 109670764, 'compact': 2744252, 'forward': 314953218, 'bwd_dq_sparse': 240769369, 'bwd_dkdv_sparse': 287893960}
+HBM_TRAFFIC_SOURCES = "5e5aa603a6d546ee"
+HBM_TRAFFIC = {'bounds': 1110153, 'select': 138301030, 'tau': 34745447, 'tau_compact': 37483839, 'refine': 109730098, 'compact': 2744259, 'forward': 314870810, 'bwd_dq_sparse': 240781333, 'bwd_dkdv_sparse': 287896791}
 
 
 def source_hash() -> str:
