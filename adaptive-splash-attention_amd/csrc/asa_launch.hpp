@@ -10,12 +10,47 @@ namespace asa {
 enum ElemType : int { kElemF32 = 0, kElemBF16 = 1, kElemF16 = 2 };
 inline int elem_bytes(int dtype) { return dtype == kElemF32 ? 4 : 2; }
 
-// Problem constants shared by every kernel.
+// Problem constants shared by every kernel.  D is the head dimension the
+// kernels compute at (64 or 128, compile-time in each kernel); hd <= D is
+// the tensors' own head dimension (a multiple of one 16-byte chunk: 8
+// elements for 16-bit types, 4 for fp32).  Columns hd .. D - 1 are never
+// read or written: loads of them give zeros, so every dot product is the
+// hd-dimensional one, and stores skip them.
 struct Dims {
-  int BH, NQ, NK, D, k, nQB, nKB;
+  int BH, H, NQ, NK, D, hd, k, nQB, nKB;
   float alpha;  // already clamped to [1.05, 3]
   float scale;
 };
+
+// Where the rows of a [B, H, N, hd] operand are: element strides of batch,
+// head and row (the head dimension is contiguous).  Every stride is a
+// multiple of a 16-byte chunk's elements, so that every chunk the kernels
+// load is 16-byte aligned, and the offsets of a head's rows from its first
+// fit 32 bits (checked by the C ABI).
+struct Lay {
+  int64_t sb, sh, sn;
+};
+// Offset (elements) of head bh = b * H + h's first row.
+__host__ __device__ inline size_t head_at(const Lay& l, int bh, int H) {
+  return size_t(bh / H) * size_t(l.sb) + size_t(bh % H) * size_t(l.sh);
+}
+// The contiguous layout of a [B, H, N, hd] tensor.
+__host__ __device__ inline Lay contiguous_lay(int H, int N, int hd) {
+  return Lay{int64_t(H) * N * hd, int64_t(N) * hd, hd};
+}
+// Whether an operand is a contiguous [B, H, N, D] tensor (then its row n
+// of head bh is at (bh N + n) D: the kernels' compile-time-stride case).
+__host__ __device__ inline bool lay_dense(const Lay& l, int H, int N, int D) {
+  const Lay c = contiguous_lay(H, N, D);
+  return l.sb == c.sb && l.sh == c.sh && l.sn == c.sn;
+}
+// Row n of head bh of an operand: at (bh N + n) D when DENSE (a contiguous
+// [B, H, N, D] tensor), else from its strides.
+template <bool DENSE, int D, typename T>
+__host__ __device__ inline T* row_at(T* base, const Lay& l, int bh, int H, int N, int n) {
+  if constexpr (DENSE) return base + (size_t(bh) * N + n) * D;
+  else return base + head_at(l, bh, H) + size_t(n) * size_t(l.sn);
+}
 
 // Support masks written by the forward and read by the backward: for the
 // tile at the head's q_list position e (query block qb, key block kb), bit
@@ -39,6 +74,7 @@ struct SelectParams {
   Dims d;
   const void* q;          // MFMA path
   const void* k;
+  Lay lq, lk;
   const float* scores;    // scores path: [BH, NQ, NK]
   const int32_t* q_idx;
   const int32_t* k_idx;
@@ -74,6 +110,7 @@ struct ForwardParams {
   const void* q;
   const void* k;
   const void* v;
+  Lay lq, lk, lv, lo;  // lo: out
   const int32_t* q_idx;
   const int32_t* k_idx;
   const float* taus;
@@ -118,6 +155,7 @@ struct BackwardParams {
   void* dq;
   void* dk;
   void* dv;
+  Lay lq, lk, lv, lo, ldo, ldq, ldk, ldv;  // lo: out, ldo: dout
   SupportMasks sup;  // mask == nullptr: dense passes
   RowRec* rowrec;    // workspace [BH * NQ] (support-mask passes)
   int32_t* posmap;   // workspace [BH, nQB * nKB] (support-mask dK/dV pass)

@@ -20,6 +20,8 @@
 
 namespace asa {
 
+enum StageRows : int { kRowsAny = 0, kRowsDense = 1, kRowsStrided = 2 };
+
 template <typename T, int D, int NT = 256>
 struct Stager {
   static constexpr int kEpc = 16 / int(sizeof(T));   // elements per 16-byte chunk
@@ -27,26 +29,48 @@ struct Stager {
   static constexpr int kQuads = (kBlock / 4) * kCpr; // quads per tile
   static constexpr int kPer = 2 * kQuads / NT;       // quads per thread
   static_assert(2 * kQuads % NT == 0, "quads must divide evenly");
+  static_assert(kQuads % 64 == 0, "a wave's quads must lie in one tile");
   static constexpr int kRs = Tile<T, D>::kRs;
 
   uint4 r[kPer][4];
 
-  // Rows [row0, row0 + 64) of src0 / src1 ([*, D] row-major); rows >= nrows
-  // read as zero.  A tile wholly inside loads its quad's four rows from one
-  // address (the row steps become immediate offsets), without tests.
-  __device__ __forceinline__ void load(const T* src0, const T* src1, int row0, int nrows, int t) {
+  // Rows [row0, row0 + 64) of src0 / src1, their rows sn0 / sn1 elements
+  // apart; rows >= nrows and columns >= hd read as zero.  A tile wholly
+  // inside rows of exactly D elements (sn = hd = D) loads its quad's four
+  // rows from one address (the row steps become immediate offsets),
+  // without tests.  ROWS: kRowsAny tests for that case at run time;
+  // kRowsDense (the caller guarantees sn0 = sn1 = hd = D) and
+  // kRowsStrided compile one case in, which keeps the other's registers
+  // out of a kernel that is short of them.
+  template <int ROWS = kRowsAny>
+  __device__ __forceinline__ void load(const T* src0, size_t sn0, const T* src1, size_t sn1,
+                                       int row0, int nrows, int hd, int t) {
     const bool whole = row0 + kBlock <= nrows;  // block-uniform
+    const bool dense = ROWS == kRowsDense ||
+                       (ROWS == kRowsAny && sn0 == D && sn1 == D && hd == D);  // uniform
     for (int i = 0; i < kPer; ++i) {
       const int qi = t + i * NT;
       const int job = qi / kQuads, q = qi % kQuads;
       const int rq = q / kCpr, cc = q % kCpr;
-      const T* src = (job == 0 ? src0 : src1) + size_t(row0 + 4 * rq) * D + cc * kEpc;
-      if (whole) {
+      if (whole && dense) {
+        const T* src = (job == 0 ? src0 : src1) + size_t(row0 + 4 * rq) * D + cc * kEpc;
         for (int j = 0; j < 4; ++j) r[i][j] = *reinterpret_cast<const uint4*>(src + j * D);
       } else {
+        // the tile's rows from a wave-uniform base (kQuads is a multiple of
+        // the wave: one tile per wave and i) at 32-bit byte offsets (a
+        // head's rows lie within 2^31 bytes of its first), so that the
+        // strided path holds no 64-bit addresses
+        const int jw = __builtin_amdgcn_readfirstlane(job);
+        const size_t sn = jw == 0 ? sn0 : sn1;
+        const unsigned char* base =
+            reinterpret_cast<const unsigned char*>((jw == 0 ? src0 : src1) + size_t(row0) * sn);
+        const uint32_t snb = uint32_t(sn) * uint32_t(sizeof(T));
+        const uint32_t off = uint32_t(4 * rq) * snb + uint32_t(cc * kEpc) * uint32_t(sizeof(T));
+        const bool col = cc * kEpc < hd;
         for (int j = 0; j < 4; ++j)
-          r[i][j] = row0 + 4 * rq + j < nrows ? *reinterpret_cast<const uint4*>(src + j * D)
-                                              : uint4{0u, 0u, 0u, 0u};
+          r[i][j] = col && row0 + 4 * rq + j < nrows
+                        ? *reinterpret_cast<const uint4*>(base + (off + uint32_t(j) * snb))
+                        : uint4{0u, 0u, 0u, 0u};
       }
     }
   }
@@ -61,37 +85,6 @@ struct Stager {
       // the chunk swizzle depends on row bits 2-3: constant over the quad
       T* d = dst + 4 * rq * kRs + ((cc * kEpc) ^ Tile<T, D>::sw(4 * rq));
       for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(d + j * kRs) = r[i][j];
-    }
-  }
-};
-
-// K tile of 64 keys in LDS, in the attention passes' tile layout (padded
-// row stride, swizzled 16-byte chunks: Tile<T, D>), filled by all NT
-// threads in 16-byte chunks (consecutive threads, consecutive chunks of a
-// row: coalesced global reads).  The scores are formed by rows_x_frag, the
-// attention passes' score product with the same operands and accumulation
-// order, so every pass sees bit-identical scores.
-template <typename T, int D, int NT = 256> struct KStage {
-  static constexpr int kRs = Tile<T, D>::kRs;                   // elements per LDS row
-  static constexpr int kRowChunks = D * int(sizeof(T)) / 16;    // 16-byte chunks per row
-  static constexpr int kPerThread = kBlock * kRowChunks / NT;
-  static_assert(kBlock * kRowChunks % NT == 0, "tile chunks must divide the block");
-  uint4 r[kPerThread];
-  // rows >= NK read as zero (such keys are never visible)
-  __device__ __forceinline__ void load(const T* Kb, int kbase, int NK, int t) {
-    for (int j = 0; j < kPerThread; ++j) {
-      const int ch = t + j * NT, row = ch / kRowChunks;
-      const int col = (ch % kRowChunks) * (16 / int(sizeof(T)));
-      r[j] = kbase + row < NK
-                 ? *reinterpret_cast<const uint4*>(Kb + size_t(kbase + row) * D + col)
-                 : uint4{0u, 0u, 0u, 0u};
-    }
-  }
-  __device__ __forceinline__ void store(T* buf, int t) const {
-    for (int j = 0; j < kPerThread; ++j) {
-      const int ch = t + j * NT, row = ch / kRowChunks;
-      const int col = (ch % kRowChunks) * (16 / int(sizeof(T)));
-      *reinterpret_cast<uint4*>(buf + row * kRs + (col ^ Tile<T, D>::sw(row))) = r[j];
     }
   }
 };

@@ -47,26 +47,26 @@ template <int D> struct Tile<float, D> {
 };
 
 // B-operand fragment of one row per lane (lane column c16 <- `row`),
-// covering the whole head dimension.
+// covering the whole head dimension; columns >= hd read as zero.
 template <typename T, int D> struct RowFrag;
 // 16-bit formats (bf16, fp16)
 template <typename T, int D> struct RowFrag16 {
   using V8 = typename Half<T>::v8;
   V8 v[D / 32];
-  __device__ void load(const T* row, bool ok, int lane) {
+  __device__ void load(const T* row, bool ok, int lane, int hd = D) {
     const int g = lane >> 4;
     for (int s = 0; s < D / 32; ++s)
-      v[s] = ok ? *reinterpret_cast<const V8*>(row + 32 * s + 8 * g) : V8{};
+      v[s] = ok && 32 * s + 8 * g < hd ? *reinterpret_cast<const V8*>(row + 32 * s + 8 * g) : V8{};
   }
 };
 template <int D> struct RowFrag<u16, D> : RowFrag16<u16, D> {};
 template <int D> struct RowFrag<h16, D> : RowFrag16<h16, D> {};
 template <int D> struct RowFrag<float, D> {
   f32x4 v[D / 16];
-  __device__ void load(const float* row, bool ok, int lane) {
+  __device__ void load(const float* row, bool ok, int lane, int hd = D) {
     const int g = lane >> 4;
     for (int j = 0; j < D / 16; ++j)
-      v[j] = ok ? *reinterpret_cast<const f32x4*>(row + 16 * j + 4 * g) : f32x4{};
+      v[j] = ok && 16 * j + 4 * g < hd ? *reinterpret_cast<const f32x4*>(row + 16 * j + 4 * g) : f32x4{};
   }
 };
 
@@ -101,20 +101,21 @@ __device__ __forceinline__ void rows_x_frag(f32x4 (&acc)[4], const float* rm,
 }
 
 // rows_x_frag with the tile read straight from global memory: `rows` points
-// at the tile's first row of a [*, D] row-major tensor, rows >= nrows read as
-// zero.  The same operands in the same MFMA order as the LDS versions above
+// at the tile's first row, rows `sn` elements apart; rows >= nrows and
+// columns >= hd read as zero.  The same operands in the same MFMA order as the LDS versions above
 // (the LDS tile holds the same values; its swizzle only moves them), so the
 // results are bit-identical.
 template <int D, typename T, typename std::enable_if<is_half<T>, int>::type = 0>
 __device__ __forceinline__ void rows_x_frag_global(f32x4 (&acc)[4], const T* rows, int nrows,
-                                                   const RowFrag<T, D>& b, int lane) {
+                                                   size_t sn, int hd, const RowFrag<T, D>& b,
+                                                   int lane) {
   using V8 = typename Half<T>::v8;
   const int g = lane >> 4, c = lane & 15;
   V8 a[D / 32][4];
   for (int s = 0; s < D / 32; ++s)
     for (int f = 0; f < 4; ++f)
-      a[s][f] = 16 * f + c < nrows
-                    ? *reinterpret_cast<const V8*>(rows + (16 * f + c) * D + 32 * s + 8 * g)
+      a[s][f] = 16 * f + c < nrows && 32 * s + 8 * g < hd
+                    ? *reinterpret_cast<const V8*>(rows + (16 * f + c) * sn + 32 * s + 8 * g)
                     : V8{};
   for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < D / 32; ++s)
@@ -122,14 +123,15 @@ __device__ __forceinline__ void rows_x_frag_global(f32x4 (&acc)[4], const T* row
 }
 template <int D>
 __device__ __forceinline__ void rows_x_frag_global(f32x4 (&acc)[4], const float* rows, int nrows,
-                                                   const RowFrag<float, D>& b, int lane) {
+                                                   size_t sn, int hd, const RowFrag<float, D>& b,
+                                                   int lane) {
   const int g = lane >> 4, c = lane & 15;
   for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < D / 16; ++j) {
     f32x4 a[4];
     for (int f = 0; f < 4; ++f)
-      a[f] = 16 * f + c < nrows
-                 ? *reinterpret_cast<const f32x4*>(rows + (16 * f + c) * D + 16 * j + 4 * g)
+      a[f] = 16 * f + c < nrows && 16 * j + 4 * g < hd
+                 ? *reinterpret_cast<const f32x4*>(rows + (16 * f + c) * sn + 16 * j + 4 * g)
                  : f32x4{};
     for (int f = 0; f < 4; ++f)
       for (int r = 0; r < 4; ++r) acc[f] = mfma(a[f][r], b.v[j][r], acc[f]);
@@ -143,12 +145,12 @@ template <typename T, int D> struct KFrags;
 template <typename T, int D> struct KFrags16 {
   using V8 = typename Half<T>::v8;
   V8 a[D / 32][4];
-  __device__ __forceinline__ void load(const T* rows, int nrows, int lane) {
+  __device__ __forceinline__ void load(const T* rows, int nrows, size_t sn, int hd, int lane) {
     const int g = lane >> 4, c = lane & 15;
     for (int s = 0; s < D / 32; ++s)
       for (int f = 0; f < 4; ++f)
-        a[s][f] = 16 * f + c < nrows
-                      ? *reinterpret_cast<const V8*>(rows + (16 * f + c) * D + 32 * s + 8 * g)
+        a[s][f] = 16 * f + c < nrows && 32 * s + 8 * g < hd
+                      ? *reinterpret_cast<const V8*>(rows + (16 * f + c) * sn + 32 * s + 8 * g)
                       : V8{};
   }
   __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<T, D>& b) const {
@@ -161,14 +163,17 @@ template <int D> struct KFrags<u16, D> : KFrags16<u16, D> {};
 template <int D> struct KFrags<h16, D> : KFrags16<h16, D> {};
 template <int D> struct KFrags<float, D> {
   const float* rows;
-  int nrows, lane;
-  __device__ __forceinline__ void load(const float* r, int n, int l) {
+  size_t sn;
+  int nrows, hd, lane;
+  __device__ __forceinline__ void load(const float* r, int n, size_t s, int h, int l) {
     rows = r;
     nrows = n;
+    sn = s;
+    hd = h;
     lane = l;
   }
   __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<float, D>& b) const {
-    rows_x_frag_global<D>(acc, rows, nrows, b, lane);
+    rows_x_frag_global<D>(acc, rows, nrows, sn, hd, b, lane);
   }
 };
 

@@ -57,10 +57,11 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(BackwardParams p) {
   const size_t rows = size_t(p.d.BH) * p.d.NQ;
   const size_t r = size_t(blockIdx.x) * kThreads + threadIdx.x;
   if (r >= rows) return;
-  const T* o = static_cast<const T*>(p.out) + r * D;
-  const T* go = static_cast<const T*>(p.dout) + r * D;
+  const int bh = int(r / p.d.NQ), n = int(r % p.d.NQ);
+  const T* o = static_cast<const T*>(p.out) + head_at(p.lo, bh, p.d.H) + size_t(n) * p.lo.sn;
+  const T* go = static_cast<const T*>(p.dout) + head_at(p.ldo, bh, p.d.H) + size_t(n) * p.ldo.sn;
   float acc = 0.0f;
-  for (int t = 0; t < D; ++t) acc += Elem<T>::load(o + t) * Elem<T>::load(go + t);
+  for (int t = 0; t < p.d.hd; ++t) acc += Elem<T>::load(o + t) * Elem<T>::load(go + t);
   float* shift = p.delta;
   float* cfac = p.delta + rows;
   shift[r] = acc;
@@ -98,14 +99,16 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
   const bool qok = q < NQ;
   const size_t rows = size_t(p.d.BH) * NQ;
   const size_t row = size_t(bh) * NQ + (qok ? q : 0);
+  const int H = p.d.H, hd = p.d.hd;
 
-  const T* Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
-  const T* Vb = static_cast<const T*>(p.v) + size_t(bh) * NK * D;
+  const T* Kb = static_cast<const T*>(p.k) + head_at(p.lk, bh, H);
+  const T* Vb = static_cast<const T*>(p.v) + head_at(p.lv, bh, H);
   const int32_t* kidx = p.k_idx + size_t(bh) * NK;
 
   RowFrag<T, D> qf, df;
-  qf.load(static_cast<const T*>(p.q) + row * D, qok, lane);
-  df.load(static_cast<const T*>(p.dout) + row * D, qok, lane);
+  qf.load(static_cast<const T*>(p.q) + head_at(p.lq, bh, H) + size_t(qok ? q : 0) * p.lq.sn, qok, lane, hd);
+  df.load(static_cast<const T*>(p.dout) + head_at(p.ldo, bh, H) + size_t(qok ? q : 0) * p.ldo.sn, qok, lane,
+          hd);
   const int qpos = qok ? p.q_idx[row] : 0;
   const float alpha = p.d.alpha;
   const float am1 = alpha - 1.0f;
@@ -147,7 +150,7 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
   PosStager ps;
   auto fetch = [&](int e) {
     const int kbase = ql[e] * kBlock;
-    st.load(Kb, Vb, kbase, NK, t);
+    st.template load<kRowsStrided>(Kb, p.lk.sn, Vb, p.lv.sn, kbase, NK, hd, t);
     ps.load(kidx, kbase, NK, INT32_MAX, t);
   };
   auto put = [&](int b) {
@@ -213,15 +216,16 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dq_kern
     }
   }
   if (qok) {
-    T* out = static_cast<T*>(p.dq) + row * D;
+    T* out = static_cast<T*>(p.dq) + head_at(p.ldq, bh, H) + size_t(q) * p.ldq.sn;
     const float cs = (REF || kOpScaled) ? scale : scale * cfac;
     for (int db = 0; db < D / 16; ++db)
-      for (int r = 0; r < 4; ++r) {
-        const float acc = REF ? a1[db][r] : (a1[db][r] - shift * a2[db][r]);
-        float v = cs * acc;
-        if (!finite(v)) v = 0.0f;
-        Elem<T>::store(out + 16 * db + 4 * g + r, v);
-      }
+      if (16 * db + 4 * g < hd)
+        for (int r = 0; r < 4; ++r) {
+          const float acc = REF ? a1[db][r] : (a1[db][r] - shift * a2[db][r]);
+          float v = cs * acc;
+          if (!finite(v)) v = 0.0f;
+          Elem<T>::store(out + 16 * db + 4 * g + r, v);
+        }
   }
 }
 
@@ -289,14 +293,15 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dkdv_ke
   const bool jok = j < NK;
   const size_t krow = size_t(bh) * NK + (jok ? j : 0);
   const size_t rows = size_t(p.d.BH) * NQ;
+  const int H = p.d.H, hd = p.d.hd;
 
-  const T* Qb = static_cast<const T*>(p.q) + size_t(bh) * NQ * D;
-  const T* dOb = static_cast<const T*>(p.dout) + size_t(bh) * NQ * D;
+  const T* Qb = static_cast<const T*>(p.q) + head_at(p.lq, bh, H);
+  const T* dOb = static_cast<const T*>(p.dout) + head_at(p.ldo, bh, H);
   const int32_t* qidx = p.q_idx + size_t(bh) * NQ;
 
   RowFrag<T, D> kf, vf;
-  kf.load(static_cast<const T*>(p.k) + krow * D, jok, lane);
-  vf.load(static_cast<const T*>(p.v) + krow * D, jok, lane);
+  kf.load(static_cast<const T*>(p.k) + head_at(p.lk, bh, H) + size_t(jok ? j : 0) * p.lk.sn, jok, lane, hd);
+  vf.load(static_cast<const T*>(p.v) + head_at(p.lv, bh, H) + size_t(jok ? j : 0) * p.lv.sn, jok, lane, hd);
   const int kpos = jok ? p.k_idx[krow] : 0;
   const float alpha = p.d.alpha;
   const float am1 = alpha - 1.0f;
@@ -322,7 +327,7 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dkdv_ke
   QConstStager qs;
   auto fetch = [&](int e) {
     const int qbase = kl[e] * kBlock;
-    st.load(Qb, dOb, qbase, NQ, t);
+    st.template load<kRowsStrided>(Qb, p.lq.sn, dOb, p.ldo.sn, qbase, NQ, hd, t);
     ps.load(qidx, qbase, NQ, INT32_MAX, t);
     qs.load(p, rows, bh, qbase, kb, NQ, am1, t);
   };
@@ -394,17 +399,18 @@ __global__ __launch_bounds__(kThreads, (dq_waves_per_simd<T, D>())) void dkdv_ke
   }
 
   if (jok) {
-    T* dk = static_cast<T*>(p.dk) + krow * D;
-    T* dv = static_cast<T*>(p.dv) + krow * D;
+    T* dk = static_cast<T*>(p.dk) + head_at(p.ldk, bh, H) + size_t(j) * p.ldk.sn;
+    T* dv = static_cast<T*>(p.dv) + head_at(p.ldv, bh, H) + size_t(j) * p.ldv.sn;
     for (int db = 0; db < D / 16; ++db)
-      for (int r = 0; r < 4; ++r) {
-        // NaN -> 0; an overflowed sum stays +-inf (reference atomics, cu:684-697)
-        float vk = scale * ak[db][r], vv = av[db][r];
-        if (__builtin_isnan(vk)) vk = 0.0f;
-        if (__builtin_isnan(vv)) vv = 0.0f;
-        Elem<T>::store(dk + 16 * db + 4 * g + r, vk);
-        Elem<T>::store(dv + 16 * db + 4 * g + r, vv);
-      }
+      if (16 * db + 4 * g < hd)
+        for (int r = 0; r < 4; ++r) {
+          // NaN -> 0; an overflowed sum stays +-inf (reference atomics, cu:684-697)
+          float vk = scale * ak[db][r], vv = av[db][r];
+          if (__builtin_isnan(vk)) vk = 0.0f;
+          if (__builtin_isnan(vv)) vv = 0.0f;
+          Elem<T>::store(dk + 16 * db + 4 * g + r, vk);
+          Elem<T>::store(dv + 16 * db + 4 * g + r, vv);
+        }
   }
 }
 

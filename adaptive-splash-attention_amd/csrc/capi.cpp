@@ -12,6 +12,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -48,7 +49,9 @@ int check_hip(hipError_t e, const char* what) {
 }
 
 struct Shape {
-  int BH, NQ, NK, D, k;
+  int BH, H, NQ, NK, D, k;
+  int hd;   // the tensors' head dimension (D: the kernels' compute width)
+  asa::Lay lq, lk, lv, ldo;  // input strides (validated)
   int nQB;  // 64-row query blocks (the kernels' tiles)
   int nKB;
   int bm;   // block_m: 64, or 32 (the reference's BLOCK_M)
@@ -57,6 +60,18 @@ struct Shape {
   bool exact;  // ASA_TAU_EXACT
   float alpha, scale;
 };
+
+// Strides of a contiguous [batch, heads, n, hd] tensor.
+asa::Lay contiguous(int heads, int n, int hd) { return asa::contiguous_lay(heads, n, hd); }
+
+// 16-byte alignment of every tensor pointer (the kernels' 16-byte loads
+// and stores).
+int check_aligned(std::initializer_list<const void*> ptrs) {
+  for (const void* q : ptrs)
+    if (reinterpret_cast<uintptr_t>(q) % 16)
+      return fail(ASA_ERR_INVALID_ARGUMENT, "tensor pointer %p is not 16-byte aligned", q);
+  return ASA_OK;
+}
 
 int validate(const asa_problem* p, Shape* sh) {
   if (!p) return fail(ASA_ERR_INVALID_ARGUMENT, "problem descriptor is NULL");
@@ -69,8 +84,8 @@ int validate(const asa_problem* p, Shape* sh) {
     return fail(ASA_ERR_INVALID_ARGUMENT, "nk (%d) must be below 2^28", p->nk);
   if (p->head_dim > 128)
     return fail(ASA_ERR_INVALID_ARGUMENT, "Head dimension too large (%d > 128)", p->head_dim);
-  if (p->head_dim != 64 && p->head_dim != 128)
-    return fail(ASA_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", p->head_dim);
+  if (p->head_dim < 1)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "head_dim %d must be >= 1", p->head_dim);
   if (p->k_keep < 1 || p->k_keep > 128)
     return fail(ASA_ERR_INVALID_ARGUMENT, "k_keep %d out of range [1, 128]", p->k_keep);
   if ((p->block_m != 64 && p->block_m != 32) || p->block_n != 64)
@@ -83,6 +98,11 @@ int validate(const asa_problem* p, Shape* sh) {
     return fail(ASA_ERR_INVALID_ARGUMENT, "unknown dtype %d", p->dtype);
   if (p->tau_mode != ASA_TAU_REFERENCE && p->tau_mode != ASA_TAU_EXACT)
     return fail(ASA_ERR_INVALID_ARGUMENT, "unknown tau_mode %d", p->tau_mode);
+  // 16-byte chunks: the kernels' unit of every load and store
+  const int epc = p->dtype == ASA_DTYPE_F32 ? 4 : 8;
+  if (p->head_dim % epc)
+    return fail(ASA_ERR_UNSUPPORTED, "head_dim %d must be a multiple of %d for this dtype",
+                p->head_dim, epc);
   if (!std::isfinite(p->alpha)) return fail(ASA_ERR_INVALID_ARGUMENT, "alpha is not finite");
   if (!std::isfinite(p->sm_scale)) return fail(ASA_ERR_INVALID_ARGUMENT, "sm_scale is not finite");
   const long long bh = (long long)p->batch * p->heads;
@@ -92,9 +112,41 @@ int validate(const asa_problem* p, Shape* sh) {
       bh * (long long)p->nq > (1LL << 40) || bh * (long long)p->nk > (1LL << 40))
     return fail(ASA_ERR_INVALID_ARGUMENT, "problem too large");
   sh->BH = int(bh);
+  sh->H = p->heads;
   sh->NQ = p->nq;
   sh->NK = p->nk;
-  sh->D = p->head_dim;
+  sh->hd = p->head_dim;
+  sh->D = p->head_dim <= 64 ? 64 : 128;
+  const int64_t ebytes = p->dtype == ASA_DTYPE_F32 ? 4 : 2;
+  struct {
+    const int64_t* st;
+    int n;
+    asa::Lay* lay;
+    const char* name;
+  } ops[] = {{p->q_strides, p->nq, &sh->lq, "q"},
+             {p->k_strides, p->nk, &sh->lk, "k"},
+             {p->v_strides, p->nk, &sh->lv, "v"},
+             {p->dout_strides, p->nq, &sh->ldo, "dout"}};
+  for (auto& o : ops) {
+    if (o.st[0] == 0 && o.st[1] == 0 && o.st[2] == 0) {
+      *o.lay = contiguous(p->heads, o.n, p->head_dim);
+      continue;
+    }
+    for (int i = 0; i < 3; ++i)
+      if (o.st[i] < 0 || o.st[i] % epc)
+        return fail(ASA_ERR_INVALID_ARGUMENT,
+                    "%s_strides[%d] = %lld must be >= 0 and a multiple of %d elements", o.name, i,
+                    (long long)o.st[i], epc);
+    // a head's rows within 2^31 bytes of its first (32-bit row offsets)
+    if (((int64_t(o.n) - 1) * o.st[2] + p->head_dim) * ebytes >= (int64_t(1) << 31))
+      return fail(ASA_ERR_UNSUPPORTED, "%s row stride %lld spans 2^31 bytes or more per head",
+                  o.name, (long long)o.st[2]);
+    // a dimension of size 1 takes its contiguous stride (its stride is
+    // never used), so that a contiguous tensor compares equal to one
+    const asa::Lay c = contiguous(p->heads, o.n, p->head_dim);
+    *o.lay = asa::Lay{p->batch == 1 ? c.sb : o.st[0], p->heads == 1 ? c.sh : o.st[1],
+                      o.n == 1 ? c.sn : o.st[2]};
+  }
   sh->k = p->k_keep;
   sh->nQB = int(nqb);
   sh->nKB = int(nkb);
@@ -109,7 +161,7 @@ int validate(const asa_problem* p, Shape* sh) {
 }
 
 asa::Dims dims_of(const Shape& s) {
-  return asa::Dims{s.BH, s.NQ, s.NK, s.D, s.k, s.nQB, s.nKB, s.alpha, s.scale};
+  return asa::Dims{s.BH, s.H, s.NQ, s.NK, s.D, s.hd, s.k, s.nQB, s.nKB, s.alpha, s.scale};
 }
 
 // Bytes of the sorted top-k values at the start of the forward workspace,
@@ -269,6 +321,8 @@ int run_select(const Shape& sh, const void* q, const void* k, const float* score
   }
   sp.q = q;
   sp.k = k;
+  sp.lq = sh.lq;
+  sp.lk = sh.lk;
   sp.scores = scores;
   sp.q_idx = q_idx;
   sp.k_idx = k_idx;
@@ -389,6 +443,10 @@ int forward_impl(const Shape& sh, const void* q, const void* k, const void* v,
   fp.q = q;
   fp.k = k;
   fp.v = v;
+  fp.lq = sh.lq;
+  fp.lk = sh.lk;
+  fp.lv = sh.lv;
+  fp.lo = contiguous(sh.H, sh.NQ, sh.hd);
   fp.q_idx = q_idx;
   fp.k_idx = k_idx;
   fp.taus = st->taus;
@@ -445,6 +503,7 @@ int asa_forward(const asa_problem* p, const void* q, const void* k, const void* 
   if (int rc = validate(p, &sh)) return rc;
   if (!q || !k || !v || !q_idx || !k_idx || !out)
     return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
+  if (int rc = check_aligned({q, k, v, out})) return rc;
   if (int rc = check_state(st, true)) return rc;
   if (!workspace) return fail(ASA_ERR_INVALID_ARGUMENT, "workspace is NULL");
   return forward_impl(sh, q, k, v, q_idx, k_idx, out, st, workspace, stream);
@@ -464,6 +523,7 @@ int asa_forward_noalloc(const asa_problem* p, const void* q, const void* k, cons
                 z.workspace, kScratchBytes);
   if (!q || !k || !v || !q_idx || !k_idx || !out)
     return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
+  if (int rc = check_aligned({q, k, v, out})) return rc;
   if (int rc = check_state(st, true)) return rc;
   void* ws = nullptr;
   if (int rc = scratch_address(&ws)) return rc;
@@ -482,6 +542,7 @@ int asa_backward(const asa_problem* p, int32_t grad_mode, const void* q, const v
     return fail(ASA_ERR_INVALID_ARGUMENT, "a tensor argument is NULL");
   if (grad_mode == ASA_GRAD_REFERENCE && !out)
     return fail(ASA_ERR_INVALID_ARGUMENT, "reference-gradient mode needs the forward output");
+  if (int rc = check_aligned({q, k, v, out, dout, dq, dk, dv})) return rc;
   if (!workspace) return fail(ASA_ERR_INVALID_ARGUMENT, "workspace is NULL");
   if (int rc = check_state(st, true)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -494,6 +555,14 @@ int asa_backward(const asa_problem* p, int32_t grad_mode, const void* q, const v
   bp.v = v;
   bp.out = out;
   bp.dout = dout;
+  bp.lq = sh.lq;
+  bp.lk = sh.lk;
+  bp.lv = sh.lv;
+  bp.ldo = sh.ldo;
+  bp.lo = contiguous(sh.H, sh.NQ, sh.hd);
+  bp.ldq = contiguous(sh.H, sh.NQ, sh.hd);
+  bp.ldk = contiguous(sh.H, sh.NK, sh.hd);
+  bp.ldv = contiguous(sh.H, sh.NK, sh.hd);
   bp.q_idx = q_idx;
   bp.k_idx = k_idx;
   bp.taus = st->taus;

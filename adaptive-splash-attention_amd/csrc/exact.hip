@@ -259,13 +259,15 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
     const float pz1 = pk ? s_z1[prow] : 0.0f;
     hi = pz1;  // f over the whole row is -1 there; lo keeps f >= 0
     if (pk && g == 0) s_ptau[slot] = tau;
-    {  // the packed rows' Q, 16 bytes per thread and step
+    {  // the packed rows' Q, 16 bytes per thread and step (columns >= hd: zero)
       constexpr int kEpc = 16 / int(sizeof(T)), kCpr = D / kEpc;
-      const T* Qh = static_cast<const T*>(p.q) + (size_t(bh) * NQ + qb * kBlock) * D;
+      const T* Qh = static_cast<const T*>(p.q) + head_at(p.lq, bh, p.d.H) + size_t(qb * kBlock) * p.lq.sn;
       for (int i = t; i < nneed * kCpr; i += kThreads) {
         const int sl = i / kCpr, cc = i % kCpr;
         *reinterpret_cast<uint4*>(s_q + sl * D + cc * kEpc) =
-            *reinterpret_cast<const uint4*>(Qh + size_t(s_rows[sl]) * D + cc * kEpc);
+            cc * kEpc < p.d.hd
+                ? *reinterpret_cast<const uint4*>(Qh + size_t(s_rows[sl]) * p.lq.sn + cc * kEpc)
+                : uint4{0u, 0u, 0u, 0u};
       }
     }
 
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
     // multiplies its K fragments by all packed row groups (below).  Partial
     // sums meet in LDS in a fixed order.
     const int ngroups = (nneed + 15) >> 4;
-    const T* Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
+    const T* Kb = static_cast<const T*>(p.k) + head_at(p.lk, bh, p.d.H);
     const int32_t* kidx = p.k_idx + size_t(bh) * NK;
     const int nbw = (nKB + 31) >> 5;
     bool done = !pk;
@@ -308,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(SelectParams p) {
         const int kb = ent & 0xffffff, kbase = kb * kBlock;
         const bool full = (ent >> 24) == 2;
         KFrags<T, D> kf;
-        kf.load(Kb + size_t(kbase) * D, NK - kbase, lane);
+        kf.load(Kb + size_t(kbase) * p.lk.sn, NK - kbase, size_t(p.lk.sn), p.d.hd, lane);
         float vany = 0.0f;  // > 0: some row of the wave has u > 0 in the tile
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg) {

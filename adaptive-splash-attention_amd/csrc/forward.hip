@@ -46,13 +46,15 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   const int q = qb * kBlock + 16 * w + c16;  // this lane's query row
   const bool qok = q < NQ;
   const size_t row = size_t(bh) * NQ + (qok ? q : 0);
+  const int H = p.d.H, hd = p.d.hd;
 
-  const T* Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
-  const T* Vb = static_cast<const T*>(p.v) + size_t(bh) * NK * D;
+  const T* Kb = static_cast<const T*>(p.k) + head_at(p.lk, bh, H);
+  const T* Vb = static_cast<const T*>(p.v) + head_at(p.lv, bh, H);
   const int32_t* kidx = p.k_idx + size_t(bh) * NK;
 
   RowFrag<T, D> qf;
-  qf.load(static_cast<const T*>(p.q) + row * D, qok, lane);
+  qf.load(static_cast<const T*>(p.q) + head_at(p.lq, bh, H) + size_t(qok ? q : 0) * p.lq.sn, qok,
+          lane, hd);
   const int qpos = qok ? p.q_idx[row] : 0;
   const float am1 = p.d.alpha - 1.0f;
   const float a = 1.0f / am1;
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   PosStager ps;
   auto fetch = [&](int e) {
     const int kbase = ql[e] * kBlock;
-    st.load(Kb, Vb, kbase, NK, t);
+    st.template load<kRowsStrided>(Kb, p.lk.sn, Vb, p.lv.sn, kbase, NK, hd, t);
     ps.load(kidx, kbase, NK, INT32_MAX, t);
   };
   auto put = [&](int b) {
@@ -169,13 +171,14 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
   const float norm = sum_groups(rowsum);
   const float inv = 1.0f / ((norm + kEps) * pscale);  // pscale 0: non-finite weights, output 0
   if (qok) {
-    T* orow = static_cast<T*>(p.out) + row * D;
+    T* orow = static_cast<T*>(p.out) + head_at(p.lo, bh, H) + size_t(q) * p.lo.sn;
     for (int db = 0; db < D / 16; ++db)
-      for (int r = 0; r < 4; ++r) {
-        float v = o[db][r] * inv;
-        if (!finite(v)) v = 0.0f;
-        Elem<T>::store(orow + 16 * db + 4 * g + r, v);
-      }
+      if (16 * db + 4 * g < hd)
+        for (int r = 0; r < 4; ++r) {
+          float v = o[db][r] * inv;
+          if (!finite(v)) v = 0.0f;
+          Elem<T>::store(orow + 16 * db + 4 * g + r, v);
+        }
     if (g == 0) p.norms[row] = norm;
   }
 }
@@ -197,7 +200,9 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
 // forward_kernel's fma per score (the kernel is VALU-bound); u is rounded
 // as c (s - tau / c) instead of once, an ulp-level difference from
 // forward_kernel.
-template <typename T, int D, int PC, bool EMIT, bool HALF>
+// DENSE: Q, K, V and Out contiguous [B, H, N, D] (hd = D), compile-time
+// strides; else any strides and hd.
+template <typename T, int D, int PC, bool EMIT, bool HALF, bool DENSE>
 __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams p) {
   static_assert(is_half<T>, "16-bit inputs only");
   __shared__ FwdSmem<T, D> sm;
@@ -209,9 +214,10 @@ __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams
   int brank, bh;
   xcd_rank_order(blockIdx.x, nP, p.d.BH, brank, bh);
   const int qp2 = nP - 1 - brank;  // heaviest first
+  const int H = p.d.H, hd = DENSE ? D : p.d.hd;
 
-  const T* Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
-  const T* Vb = static_cast<const T*>(p.v) + size_t(bh) * NK * D;
+  const T* Kb = row_at<DENSE, D>(static_cast<const T*>(p.k), p.lk, bh, H, NK, 0);
+  const T* Vb = row_at<DENSE, D>(static_cast<const T*>(p.v), p.lv, bh, H, NK, 0);
   const int32_t* kidx = p.k_idx + size_t(bh) * NK;
   const int2* kbnd = p.kbounds + size_t(bh) * nKB;
   const float am1 = p.d.alpha - 1.0f;
@@ -236,7 +242,8 @@ __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams
     const int q = qb[h] * kBlock + 16 * w + c16;
     qok[h] = bok && q < NQ;
     row[h] = size_t(bh) * NQ + (qok[h] ? q : 0);
-    qf[h].load(static_cast<const T*>(p.q) + row[h] * D, qok[h], lane);
+    qf[h].load(row_at<DENSE, D>(static_cast<const T*>(p.q), p.lq, bh, H, NQ, qok[h] ? q : 0), qok[h],
+               lane, hd);
     qpos[h] = qok[h] ? p.q_idx[row[h]] : 0;
     if (qok[h]) {
       // SignedClip's bounds, divided by c (rows that get no weight keep
@@ -295,7 +302,7 @@ __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams
   PosStager ps;
   auto fetch = [&](int ent) {
     const int kbase = (ent & 0x3fffffff) * kBlock;
-    st.load(Kb, Vb, kbase, NK, t);
+    st.template load<DENSE ? kRowsDense : kRowsStrided>(Kb, p.lk.sn, Vb, p.lv.sn, kbase, NK, hd, t);
     ps.load(kidx, kbase, NK, INT32_MAX, t);
   };
   auto put = [&](int b) {
@@ -372,28 +379,41 @@ __global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams
     const float norm = ce * sum_groups(rowsum[h]);
     const float inv = ce / ((norm + kEps) * pscale[h]);  // pscale 0: non-finite weights, output 0
     if (qok[h]) {
-      T* orow = static_cast<T*>(p.out) + row[h] * D;
+      T* orow = row_at<DENSE, D>(static_cast<T*>(p.out), p.lo, bh, H, NQ, int(row[h] - size_t(bh) * NQ));
       for (int db = 0; db < D / 16; ++db)
-        for (int r = 0; r < 4; ++r) {
-          float v = o[h][db][r] * inv;
-          if (!finite(v)) v = 0.0f;
-          Elem<T>::store(orow + 16 * db + 4 * g + r, v);
-        }
+        if (DENSE || 16 * db + 4 * g < hd)
+          for (int r = 0; r < 4; ++r) {
+            float v = o[h][db][r] * inv;
+            if (!finite(v)) v = 0.0f;
+            Elem<T>::store(orow + 16 * db + 4 * g + r, v);
+          }
       if (g == 0) p.norms[row[h]] = norm;
     }
   }
 }
 
-template <typename T, int D, bool EMIT, bool HALF>
-hipError_t launch_pair(const ForwardParams& p, hipStream_t s) {
+template <typename T, int D, bool EMIT, bool HALF, bool DENSE>
+hipError_t launch_pair_rows(const ForwardParams& p, hipStream_t s) {
   dim3 grid(((p.d.nQB + 1) / 2) * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
-    case kA15: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE2, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
-    case kA20: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE1, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
-    case kA125: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE4, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;
+    case kA15: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE2, EMIT, HALF, DENSE>), grid, dim3(kThreads), 0, s, p); break;
+    case kA20: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE1, EMIT, HALF, DENSE>), grid, dim3(kThreads), 0, s, p); break;
+    case kA125: hipLaunchKernelGGL((forward_pair_kernel<T, D, kE4, EMIT, HALF, DENSE>), grid, dim3(kThreads), 0, s, p); break;
     default: return hipErrorInvalidValue;  // excluded by pair_fold_ok
   }
   return hipGetLastError();
+}
+// Q, K, V and Out contiguous [B, H, N, D] (hd = D).
+inline bool fwd_dense(const ForwardParams& p) {
+  const int H = p.d.H, D = p.d.D;
+  return p.d.hd == D && lay_dense(p.lq, H, p.d.NQ, D) && lay_dense(p.lk, H, p.d.NK, D) &&
+         lay_dense(p.lv, H, p.d.NK, D) && lay_dense(p.lo, H, p.d.NQ, D);
+}
+
+template <typename T, int D, bool EMIT, bool HALF>
+hipError_t launch_pair(const ForwardParams& p, hipStream_t s) {
+  if (fwd_dense(p)) return launch_pair_rows<T, D, EMIT, HALF, true>(p, s);
+  return launch_pair_rows<T, D, EMIT, HALF, false>(p, s);
 }
 
 // forward_pair_kernel's folded clip applies: an integer power class (the

@@ -322,9 +322,20 @@ template <typename T, int D> struct KQuarter16 {
   // loads; a whole-row load with the operands rebuilt by two DPP row
   // rotations per register measured the same sweep time, which the
   // candidate appends, not the loads, set.)
-  __device__ __forceinline__ void load(const T* Kb, int key, int NK, int g) {
-    const T* src = Kb + size_t(key < NK ? key : 0) * D + 8 * g;
-    for (int s = 0; s < D / 32; ++s) a[s] = *reinterpret_cast<const V8*>(src + 32 * s);
+  // GENERAL: rows snb bytes apart (32-bit offsets from the head's first
+  // row, which the C ABI bounds below 2^31), columns >= hd read as zero;
+  // else rows of exactly D elements, hd = D.
+  template <bool GENERAL>
+  __device__ __forceinline__ void load(const T* Kb, int key, int NK, uint32_t snb, int hd, int g) {
+    const int kk = key < NK ? key : 0;
+    if constexpr (GENERAL) {
+      const unsigned char* src = reinterpret_cast<const unsigned char*>(Kb) + (uint32_t(kk) * snb + 16u * g);
+      for (int s = 0; s < D / 32; ++s)
+        a[s] = 32 * s + 8 * g < hd ? *reinterpret_cast<const V8*>(src + 64 * s) : V8{};
+    } else {
+      const T* src = Kb + size_t(kk) * D + 8 * g;
+      for (int s = 0; s < D / 32; ++s) a[s] = *reinterpret_cast<const V8*>(src + 32 * s);
+    }
   }
   __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<T, D> (&qf)[4]) const {
     for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -336,9 +347,17 @@ template <int D> struct KQuarter<u16, D> : KQuarter16<u16, D> {};
 template <int D> struct KQuarter<h16, D> : KQuarter16<h16, D> {};
 template <int D> struct KQuarter<float, D> {
   f32x4 a[D / 16];
-  __device__ __forceinline__ void load(const float* Kb, int key, int NK, int g) {
-    const float* src = Kb + size_t(key < NK ? key : 0) * D + 4 * g;
-    for (int j = 0; j < D / 16; ++j) a[j] = *reinterpret_cast<const f32x4*>(src + 16 * j);
+  template <bool GENERAL>
+  __device__ __forceinline__ void load(const float* Kb, int key, int NK, uint32_t snb, int hd, int g) {
+    const int kk = key < NK ? key : 0;
+    if constexpr (GENERAL) {
+      const unsigned char* src = reinterpret_cast<const unsigned char*>(Kb) + (uint32_t(kk) * snb + 16u * g);
+      for (int j = 0; j < D / 16; ++j)
+        a[j] = 16 * j + 4 * g < hd ? *reinterpret_cast<const f32x4*>(src + 64 * j) : f32x4{};
+    } else {
+      const float* src = Kb + size_t(kk) * D + 4 * g;
+      for (int j = 0; j < D / 16; ++j) a[j] = *reinterpret_cast<const f32x4*>(src + 16 * j);
+    }
   }
   __device__ __forceinline__ void product(f32x4 (&acc)[4], const RowFrag<float, D> (&qf)[4]) const {
     for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -412,7 +431,11 @@ constexpr int ring_bytes() { return 4 * ring_tiles<D, R>() * 32 * D; }
 template <typename T, int D, int R>
 constexpr int select_waves_per_simd() { return sizeof(T) == 2 && D == 64 && R == 2 ? 3 : 1; }
 
-template <typename T, int D, int MODE, int R>
+// WIDE: K rows of exactly D elements (hd = D, row stride D): compile-time
+// addressing, no column tests, and with 16-bit inputs sweep 1 reads K
+// through the LDS ring (whose loads read whole rows).  Else any row stride
+// and hd.
+template <typename T, int D, int MODE, int R, bool WIDE>
 __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void select_kernel(SelectParams p) {
   constexpr bool kExact = MODE != kRawDots;
   constexpr bool kTiles = MODE != kGivenScores;
@@ -489,10 +512,12 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
   RowFrag<T, D> qf[4];  // Q^T operands: row 16 cb + c in column c of the products
   const T* Kb = nullptr;
   if constexpr (kTiles) {
+    const T* Qh = static_cast<const T*>(p.q) + head_at(p.lq, bh, p.d.H);
     for (int cb = 0; cb < 4; ++cb)
-      qf[cb].load(static_cast<const T*>(p.q) + (grow0 + 16 * cb + c) * D, rowok[cb], L);
-    Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
+      qf[cb].load(Qh + size_t(rowok[cb] ? q0 + 16 * cb + c : 0) * p.lq.sn, rowok[cb], L, p.d.hd);
+    Kb = static_cast<const T*>(p.k) + head_at(p.lk, bh, p.d.H);
   }
+  const uint32_t ksnb = uint32_t(p.lk.sn) * uint32_t(sizeof(T));  // K row stride, bytes (GENERAL loads)
   const int kq0 = 16 * w + c;  // the lane's A-operand key within a tile
 
   // One pass over the visible key blocks: body(u, kt, visb, acc) for each,
@@ -537,7 +562,7 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
     if (nvis == 0) return;  // block-uniform
     KQuarter<T, D> kq[2];
     auto fetch = [&](KQuarter<T, D>& f, int e) {
-      f.load(Kb, (e & 0xffffff) * kBlock + kq0, NK, g);
+      f.template load<!WIDE>(Kb, (e & 0xffffff) * kBlock + kq0, NK, ksnb, p.d.hd, g);
     };
     // The loads are unconditional (past the end of the list they repeat its
     // last tile), so the number in flight is the same on every path and the
@@ -619,7 +644,7 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
   constexpr int kRpi = kWave / kCpr;       // rows per DMA instruction
   auto qsw = [](int r) { return D == 64 ? (r >> 1) & 7 : r & 15; };
   constexpr int kRing = ring_tiles<D, R>();
-  constexpr bool kRingSweep = kTiles && is_half<T>;
+  constexpr bool kRingSweep = kTiles && is_half<T> && WIDE;
   auto sweep_ring = [&](auto u_tag, auto&& body) {
     constexpr int U = decltype(u_tag)::value;
     if (nvis == 0) return;  // block-uniform
@@ -1069,11 +1094,12 @@ __global__ __launch_bounds__(kThreads) void tau_compact_kernel(SelectParams p, C
   }
 }
 
-template <typename T, int D, int MODE, int R>
+template <typename T, int D, int MODE, int R, bool WIDE>
 hipError_t launch_one(const SelectParams& p, hipStream_t s) {
   const SelLayout l = sel_layout(p.d.k, p.cap, p.d.nKB);
-  auto kern = select_kernel<T, D, MODE, R>;
-  if (is_half<T> && MODE != kGivenScores && ring_bytes<D, R>() > l.tkey) return hipErrorInvalidValue;
+  auto kern = select_kernel<T, D, MODE, R, WIDE>;
+  if (WIDE && is_half<T> && MODE != kGivenScores && ring_bytes<D, R>() > l.tkey)
+    return hipErrorInvalidValue;
   if (l.total > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, l.total);
@@ -1083,12 +1109,22 @@ hipError_t launch_one(const SelectParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The WIDE variant (K rows of D elements) for the 16-bit MFMA sweeps with
+// raw dots (the usual scale > 0); the others take the general loads (and
+// sweep 1 on the register path).
+template <typename T, int D, int MODE, int R>
+hipError_t launch_ring(const SelectParams& p, hipStream_t s) {
+  if constexpr (is_half<T> && MODE == kRawDots)
+    if (p.d.hd == D && p.lk.sn == D) return launch_one<T, D, MODE, R, true>(p, s);
+  return launch_one<T, D, MODE, R, false>(p, s);
+}
+
 // Class sets per (row, position): more sets tighten the sweep-2 floor; the
 // larger k, the more candidates a loose floor admits.
 template <typename T, int D, int MODE>
 hipError_t launch_r(const SelectParams& p, hipStream_t s) {
-  if (classes_per_lane(p.d.k) == 2) return launch_one<T, D, MODE, 2>(p, s);
-  return launch_one<T, D, MODE, 4>(p, s);
+  if (classes_per_lane(p.d.k) == 2) return launch_ring<T, D, MODE, 2>(p, s);
+  return launch_ring<T, D, MODE, 4>(p, s);
 }
 
 template <typename T, int D>

@@ -181,7 +181,7 @@ __device__ __forceinline__ int groups_max(int v) {
 // ---------------------------------------------------------------------------
 // dQ
 // ---------------------------------------------------------------------------
-template <typename T, int D, int AC, bool REF>
+template <typename T, int D, int AC, bool REF, bool FULL>
 __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p) {
   constexpr int kBatchQ = batch_q<AC>();
   using C = Chunk<T>;
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
   __shared__ int s_list[4][RPR][kRowList];   // chunked path
   __shared__ uint64_t s_mw[4][kChunk][16];   // mask words of a chunk of tiles: [tile][row]
   __shared__ int s_kb[4][kChunk];            // first key of each tile
-  const int NQ = p.d.NQ, NK = p.d.NK, nQB = p.d.nQB, nKB = p.d.nKB;
+  const int NQ = p.d.NQ, nQB = p.d.nQB, nKB = p.d.nKB;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   // head by head (xcd_task): the pass's work per block hardly depends on
   // the query block, and two heads' K/V rows at a time stay in the L2
@@ -210,12 +210,23 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
   const int task = xcd_task(blockIdx.x, nQB * p.d.BH);
   const int qb = nQB - 1 - task % nQB, bh = task / nQB;
   const int sub = lane % LPR, grp = lane / LPR;
+  // The lane's 16 bytes of a row: inside the head dimension (colok), or a
+  // lane past hd, which gathers the row's first chunk instead (an address
+  // inside the row) and drops its partial dot products; its own sums are
+  // never stored.  FULL: hd = D and rows of D elements (compile-time
+  // strides).
+  const bool colok = FULL || sub * E < p.d.hd;
+  const uint32_t lcol = uint32_t(colok ? sub * E : 0) * uint32_t(sizeof(T));  // bytes
+  const uint32_t ksb = uint32_t(FULL ? D : p.lk.sn) * uint32_t(sizeof(T));   // row strides, bytes
+  const uint32_t vsb = uint32_t(FULL ? D : p.lv.sn) * uint32_t(sizeof(T));
 
   const float alpha = p.d.alpha, am1 = alpha - 1.0f, ew = (2.0f - alpha) / am1;
   const float scale = p.d.scale;
   const size_t rows = size_t(p.d.BH) * NQ;
-  const T* Kb = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
-  const T* Vb = static_cast<const T*>(p.v) + size_t(bh) * NK * D;
+  const T* Kb = static_cast<const T*>(p.k) + head_at(p.lk, bh, p.d.H);
+  const T* Vb = static_cast<const T*>(p.v) + head_at(p.lv, bh, p.d.H);
+  const T* Qh = static_cast<const T*>(p.q) + head_at(p.lq, bh, p.d.H);
+  const T* dOh = static_cast<const T*>(p.dout) + head_at(p.ldo, bh, p.d.H);
   const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
   const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
   const int e0 = qp[qb], e1 = qp[qb + 1];
@@ -272,10 +283,9 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
     const int qrow = qb * kBlock + 16 * w + r;
     nqv = uint4{0u, 0u, 0u, 0u};
     ndO = uint4{0u, 0u, 0u, 0u};
-    if (qrow < NQ) {
-      const size_t rw = size_t(bh) * NQ + qrow;
-      nqv = C::raw(static_cast<const T*>(p.q) + rw * D + sub * E);
-      ndO = C::raw(static_cast<const T*>(p.dout) + rw * D + sub * E);
+    if (qrow < NQ && colok) {
+      nqv = C::raw(Qh + size_t(qrow) * (FULL ? D : p.lq.sn) + sub * E);
+      ndO = C::raw(dOh + size_t(qrow) * (FULL ? D : p.ldo.sn) + sub * E);
     }
   };
   auto start_row = [&](int r) {  // after prefetch(r)
@@ -300,13 +310,17 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
       key[u] = val[u] ? lst[q + u] : 0;
     }
     for (int u = 0; u < kBatchQ; ++u) {
-      const uint32_t off = (uint32_t(key[u]) * D + sub * E) * uint32_t(sizeof(T));
-      kraw[u] = raw_at(Kb, off);
-      vraw[u] = raw_at(Vb, off);
+      kraw[u] = raw_at(Kb, uint32_t(key[u]) * ksb + lcol);
+      vraw[u] = raw_at(Vb, uint32_t(key[u]) * vsb + lcol);
     }
     for (int u = 0; u < kBatchQ; ++u) {
-      float s = group_lanes_sum<LPR>(C::dot(qv, kraw[u]));
-      float dp = group_lanes_sum<LPR>(C::dot(dO, vraw[u]));
+      float ps = C::dot(qv, kraw[u]), pd = C::dot(dO, vraw[u]);
+      if constexpr (!FULL) {
+        ps = colok ? ps : 0.0f;
+        pd = colok ? pd : 0.0f;
+      }
+      float s = group_lanes_sum<LPR>(ps);
+      float dp = group_lanes_sum<LPR>(pd);
       // complete here: sunk into the branch below, the last step's DPP
       // move no longer fused into its add
       asm volatile("" : "+v"(s), "+v"(dp));
@@ -344,7 +358,10 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
       const float v = cs * fmaf(-shift, a2[x], a1[x]);
       o[x] = finite(v) ? v : 0.0f;
     }
-    C::store(static_cast<T*>(p.dq) + row * D + sub * E, o);
+    if (colok)
+      C::store(static_cast<T*>(p.dq) + head_at(p.ldq, bh, p.d.H) +
+                   size_t(qb * kBlock + 16 * w + rr) * (FULL ? D : p.ldq.sn) + sub * E,
+               o);
     if (sub == 0)
       p.rowrec[row] = RowRec{clip.nt, 1.0f / (norm + kEps), cfac, -cfac * shift};
   };
@@ -514,7 +531,7 @@ constexpr int kKeyChunks = 1;
 template <typename T, int D> constexpr int key_lanes() { return D / (kKeyChunks * Chunk<T>::E); }
 template <typename T, int D> constexpr int keys_per_block() { return 4 * (kWave / key_lanes<T, D>()); }
 
-template <typename T, int D, int AC, bool REF>
+template <typename T, int D, int AC, bool REF, bool FULL>
 __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams p) {
   constexpr int kBatch = batch_kv<AC>();
   using C = Chunk<T>;
@@ -572,7 +589,6 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   const int jb = slice * KPB + w * KPW;  // first key (within the block) of this wave
   const int j = kb * kBlock + jb + grp;  // this group's key
   const bool jok = j < NK;
-  const size_t krow = size_t(bh) * NK + (jok ? j : 0);
 
   const float alpha = p.d.alpha, am1 = alpha - 1.0f;
   const float a = 1.0f / am1, ew = (2.0f - alpha) / am1;
@@ -581,37 +597,49 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
   // give smin, as the clamp gives NaN -> -10
   const float smax = 10.0f / p.d.scale, smin = -smax;
   const size_t rbase = size_t(bh) * NQ;
-  const T* Qb = static_cast<const T*>(p.q) + rbase * D;
-  const T* dOb = static_cast<const T*>(p.dout) + rbase * D;
+  const int H = p.d.H;
+  const T* Qb = static_cast<const T*>(p.q) + head_at(p.lq, bh, H);
+  const T* dOb = static_cast<const T*>(p.dout) + head_at(p.ldo, bh, H);
+  // Chunk c of the lane's rows: inside the head dimension (colok[c]), or
+  // past hd, where the lane gathers the row's first chunk instead (an
+  // address inside the row) and drops that chunk's partial dot products;
+  // its sums there are never stored.  FULL: hd = D, rows of D elements.
+  bool colok[NC];
+  uint32_t lcol[NC];  // bytes
+  for (int c = 0; c < NC; ++c) {
+    colok[c] = FULL || sub * EL + c * E < p.d.hd;
+    lcol[c] = uint32_t(colok[c] ? sub * EL + c * E : 0) * uint32_t(sizeof(T));
+  }
+  const uint32_t qsb = uint32_t(FULL ? D : p.lq.sn) * uint32_t(sizeof(T));  // row strides, bytes
+  const uint32_t gsb = uint32_t(FULL ? D : p.ldo.sn) * uint32_t(sizeof(T));
+  const size_t ksn = FULL ? size_t(D) : size_t(p.lk.sn), vsn = FULL ? size_t(D) : size_t(p.lv.sn);
   const RowRec* rec = p.rowrec + rbase;
-  const int32_t* qp = p.q_ptr + size_t(bh) * (nQB + 1);
-  const int32_t* ql = p.q_list + size_t(bh) * nQB * nKB;
   const int32_t* kp = p.k_ptr + size_t(bh) * (nKB + 1);
   const int32_t* kl = p.k_list + size_t(bh) * nKB * nQB;
   const uint16_t* hmask = p.sup.mask + size_t(bh) * nQB * nKB * 256;
 
   uint4 kv[NC], vv[NC];  // raw 16-byte chunks of the key's rows
+  const T* const Kh = static_cast<const T*>(p.k) + head_at(p.lk, bh, H);
+  const T* const Vh = static_cast<const T*>(p.v) + head_at(p.lv, bh, H);
   for (int c = 0; c < NC; ++c) {
     kv[c] = uint4{0u, 0u, 0u, 0u};
     vv[c] = uint4{0u, 0u, 0u, 0u};
-    if (jok) {
-      kv[c] = C::raw(static_cast<const T*>(p.k) + krow * D + sub * EL + c * E);
-      vv[c] = C::raw(static_cast<const T*>(p.v) + krow * D + sub * EL + c * E);
+    if (jok && colok[c]) {
+      kv[c] = C::raw(Kh + size_t(j) * ksn + sub * EL + c * E);
+      vv[c] = C::raw(Vh + size_t(j) * vsn + sub * EL + c * E);
     }
   }
   float dk[EL], dv[EL];
   for (int x = 0; x < EL; ++x) dk[x] = dv[x] = 0.0f;
 
   const int* mylist = s_lists + (w * KPW + grp) * kKeyList;
-  // chunk c of row `key` (jb + key of the block) of K or V, zero past NK
-  // (returned by value: arrays passed by reference here kept the
-  // accumulators out of registers)
-  const T* const Kh = static_cast<const T*>(p.k) + size_t(bh) * NK * D;
-  const T* const Vh = static_cast<const T*>(p.v) + size_t(bh) * NK * D;
-  auto key_chunk = [&](const T* base, int key, int c) -> uint4 {
+  // chunk c of row `key` (jb + key of the block) of K or V (rows sn
+  // elements apart), zero past NK and past hd (returned by value: arrays
+  // passed by reference here kept the accumulators out of registers)
+  auto key_chunk = [&](const T* base, size_t sn, int key, int c) -> uint4 {
     const int jj = kb * kBlock + jb + key;
-    if (jj >= NK) return uint4{0u, 0u, 0u, 0u};
-    return C::raw(base + size_t(jj) * D + sub * EL + c * E);
+    if (jj >= NK || !colok[c]) return uint4{0u, 0u, 0u, 0u};
+    return C::raw(base + size_t(jj) * sn + sub * EL + c * E);
   };
   // phase B: the wave's KPW key lists, kBatch entries at a time in every
   // lane group.  The keys pair up by list length (longest with shortest,
@@ -651,8 +679,8 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
         }
         for (int x = 0; x < EL; ++x) dk[x] = dv[x] = 0.0f;
         for (int c = 0; c < NC; ++c) {
-          kv[c] = key_chunk(Kh, partner, c);
-          vv[c] = key_chunk(Vh, partner, c);
+          kv[c] = key_chunk(Kh, ksn, partner, c);
+          vv[c] = key_chunk(Vh, vsn, partner, c);
         }
         lst = s_lists + (w * KPW + partner) * kKeyList;
         off = pcs - ob;
@@ -669,9 +697,8 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
       }
       for (int u = 0; u < kBatch; ++u) {
         for (int c = 0; c < NC; ++c) {
-          const uint32_t off = (uint32_t(r[u]) * D + sub * EL + c * E) * uint32_t(sizeof(T));
-          qraw[u][c] = raw_at(Qb, off);
-          graw[u][c] = raw_at(dOb, off);
+          qraw[u][c] = raw_at(Qb, uint32_t(r[u]) * qsb + lcol[c]);
+          graw[u][c] = raw_at(dOb, uint32_t(r[u]) * gsb + lcol[c]);
         }
         rw[u] = *reinterpret_cast<const float*>(reinterpret_cast<const unsigned char*>(rec) +
                                                 (uint32_t(r[u]) * uint32_t(sizeof(RowRec)) + 4u * (sub & 3)));
@@ -679,8 +706,10 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
       for (int u = 0; u < kBatch; ++u) {
         float s = 0.0f, dp = 0.0f;
         for (int c = 0; c < NC; ++c) {
-          s = C::dot(qraw[u][c], kv[c], s);
-          dp = C::dot(graw[u][c], vv[c], dp);
+          if (FULL || colok[c]) {
+            s = C::dot(qraw[u][c], kv[c], s);
+            dp = C::dot(graw[u][c], vv[c], dp);
+          }
         }
         s = group_lanes_sum<LPR>(s);
         dp = group_lanes_sum<LPR>(dp);
@@ -735,8 +764,8 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
         dv[x] = b4.x; dv[x + 1] = b4.y; dv[x + 2] = b4.z; dv[x + 3] = b4.w;
       }
       for (int c = 0; c < NC; ++c) {
-        kv[c] = key_chunk(Kh, grp, c);
-        vv[c] = key_chunk(Vh, grp, c);
+        kv[c] = key_chunk(Kh, ksn, grp, c);
+        vv[c] = key_chunk(Vh, vsn, grp, c);
       }
     }
     if (big && hb > 0) {  // the longer list's group: add its tail's sums
@@ -877,21 +906,39 @@ __global__ __launch_bounds__(kThreads, 4) void dkdv_sparse_kernel(BackwardParams
         k8[x] = dk[c * E + x];
         v8[x] = dv[c * E + x];
       }
-      C::store(static_cast<T*>(p.dk) + krow * D + sub * EL + c * E, k8);
-      C::store(static_cast<T*>(p.dv) + krow * D + sub * EL + c * E, v8);
+      if (colok[c]) {
+        C::store(static_cast<T*>(p.dk) + head_at(p.ldk, bh, H) + size_t(j) * (FULL ? D : p.ldk.sn) +
+                     sub * EL + c * E,
+                 k8);
+        C::store(static_cast<T*>(p.dv) + head_at(p.ldv, bh, H) + size_t(j) * (FULL ? D : p.ldv.sn) +
+                     sub * EL + c * E,
+                 v8);
+      }
     }
   }
+}
+
+// Rows of exactly D elements in every operand (hd = D): the kernels'
+// compile-time-stride variant.
+inline bool rows_dense(const BackwardParams& p) {
+  const int64_t D = p.d.D;
+  return p.d.hd == D && p.lq.sn == D && p.lk.sn == D && p.lv.sn == D && p.ldo.sn == D &&
+         p.ldq.sn == D && p.ldk.sn == D && p.ldv.sn == D;
 }
 
 template <typename T, int D, bool REF, bool DKDV>
 hipError_t launch_sparse_m(const BackwardParams& p, hipStream_t s) {
   const dim3 grid(DKDV ? p.d.nKB * (kBlock / keys_per_block<T, D>()) * p.d.BH : p.d.nQB * p.d.BH);
+  const bool full = rows_dense(p);
   auto go = [&](auto ac) {
     constexpr int AC = decltype(ac)::value;
-    if constexpr (DKDV)
-      hipLaunchKernelGGL((dkdv_sparse_kernel<T, D, AC, REF>), grid, dim3(kThreads), 0, s, p);
-    else
-      hipLaunchKernelGGL((dq_sparse_kernel<T, D, AC, REF>), grid, dim3(kThreads), 0, s, p);
+    if constexpr (DKDV) {
+      if (full) hipLaunchKernelGGL((dkdv_sparse_kernel<T, D, AC, REF, true>), grid, dim3(kThreads), 0, s, p);
+      else hipLaunchKernelGGL((dkdv_sparse_kernel<T, D, AC, REF, false>), grid, dim3(kThreads), 0, s, p);
+    } else {
+      if (full) hipLaunchKernelGGL((dq_sparse_kernel<T, D, AC, REF, true>), grid, dim3(kThreads), 0, s, p);
+      else hipLaunchKernelGGL((dq_sparse_kernel<T, D, AC, REF, false>), grid, dim3(kThreads), 0, s, p);
+    }
   };
   switch (alpha_class_of(p.d.alpha)) {
     case kA15: go(std::integral_constant<int, kA15>{}); break;

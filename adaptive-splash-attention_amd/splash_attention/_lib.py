@@ -12,7 +12,7 @@ import threading
 
 from . import _build
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 ASA_OK = 0
 ASA_ERR_INVALID_ARGUMENT = 1
@@ -63,6 +63,11 @@ class Problem(ctypes.Structure):
         ("sm_scale", ctypes.c_float),
         ("dtype", ctypes.c_int32),
         ("tau_mode", ctypes.c_int32),
+        # element strides {batch, head, row}; zeros: contiguous
+        ("q_strides", ctypes.c_int64 * 3),
+        ("k_strides", ctypes.c_int64 * 3),
+        ("v_strides", ctypes.c_int64 * 3),
+        ("dout_strides", ctypes.c_int64 * 3),
     ]
 
 

@@ -36,7 +36,8 @@ def forward_op(Q: Tensor, K: Tensor, V: Tensor, Q_idx: Optional[Tensor], K_idx: 
                ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """out, taus, norms, mask, q_ptr, q_list, k_ptr, k_list and the support
     masks sup_mask (grad_mode is recorded for the backward only).  out is in
-    the kernels' layout (ops.to_kernel_layout: head dimension 64 or 128)."""
+    the kernels' layout (ops.to_kernel_layout: the head dimension a whole
+    number of 16-byte chunks), contiguous."""
     q, k, v, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     out, st = ops.splash_forward(q, k, v, qi, ki, alpha, k_keep, sm_scale, with_support=True,
                                  tau_mode=tau_mode, block_m=block_m)
@@ -54,7 +55,7 @@ def _forward_fake(Q, K, V, Q_idx, K_idx, alpha, k_keep, sm_scale, grad_mode,
     f32 = dict(dtype=torch.float32, device=Q.device)
     i32 = dict(dtype=torch.int32, device=Q.device)
     odt = Q.dtype
-    return (torch.empty((B, H, NQ, ops.kernel_head_dim(d)), dtype=odt, device=Q.device),
+    return (torch.empty((B, H, NQ, ops.kernel_head_dim(d, Q.dtype)), dtype=odt, device=Q.device),
             torch.empty((BH, NQ), **f32), torch.empty((BH, NQ), **f32),
             torch.empty((BH, nQB, nKB), dtype=torch.uint8, device=Q.device),
             torch.empty((BH, nQB + 1), **i32), torch.empty((BH, nQB * nKB), **i32),
@@ -93,8 +94,8 @@ def _setup_context(ctx, inputs, output):
 def _backward(ctx, dout, *unused_state_grads):
     Q, K, V, Q_idx, K_idx, out, *state = ctx.saved_tensors
     alpha, k_keep, sm_scale, grad_mode = ctx.params
-    dQ, dK, dV = backward_op(Q, K, V, Q_idx, K_idx, out, dout.contiguous(), *state, alpha, k_keep,
-                             sm_scale, grad_mode)
+    dQ, dK, dV = backward_op(Q, K, V, Q_idx, K_idx, out, dout, *state, alpha, k_keep, sm_scale,
+                             grad_mode)
     return dQ, dK, dV, None, None, None, None, None, None, None, None
 
 

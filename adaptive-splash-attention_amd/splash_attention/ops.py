@@ -22,7 +22,6 @@ BLOCK_MS = (64, 32)      # supported block_m values
 BLOCK_N = 64
 MAX_HEAD_DIM = 128
 MAX_K_KEEP = 128
-KERNEL_HEAD_DIMS = (64, 128)
 
 # dtypes the kernels compute in
 _DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16,
@@ -199,8 +198,10 @@ def check_shapes(Q, K, V, k_keep=None):
 
 
 def check_inputs(Q, K, V, Q_idx=None, K_idx=None):
-    """Validate and normalise (Q, K, V, Q_idx, K_idx); returns contiguous
-    tensors in the kernels' layout (see to_kernel_layout)."""
+    """Validate and normalise (Q, K, V, Q_idx, K_idx).  Q, K, V come back as
+    the kernels read them (kernel_operand): the caller's tensors themselves,
+    views included, unless their head dimension needs padding or their
+    layout cannot be read in place."""
     check_shapes(Q, K, V)
     B, H, NQ, _ = Q.shape
     NK = K.shape[2]
@@ -208,26 +209,34 @@ def check_inputs(Q, K, V, Q_idx=None, K_idx=None):
     qi = _index(Q_idx, BH, NQ, B, H, Q.device, "Q_idx")
     ki = _index(K_idx, BH, NK, B, H, Q.device, "K_idx")
     Q, K, V = to_kernel_layout(Q, K, V)
-    return _aligned(Q), _aligned(K), _aligned(V), qi, ki
+    return kernel_operand(Q), kernel_operand(K), kernel_operand(V), qi, ki
 
 
-def kernel_head_dim(d: int) -> int:
-    """The kernel head dimension a head dimension d <= 128 runs at."""
-    return KERNEL_HEAD_DIMS[0] if d <= KERNEL_HEAD_DIMS[0] else KERNEL_HEAD_DIMS[1]
+def chunk_elems(dtype: torch.dtype) -> int:
+    """Elements of a 16-byte chunk, the kernels' unit of every load and store."""
+    return 4 if dtype == torch.float32 else 8
+
+
+def kernel_head_dim(d: int, dtype: torch.dtype) -> int:
+    """The head dimension the kernels take for a caller's d <= 128: d itself
+    when it is a whole number of 16-byte chunks, else d rounded up to one."""
+    e = chunk_elems(dtype)
+    return -(-d // e) * e
 
 
 def to_kernel_layout(*ts):
     """Tensors [..., d] as the kernels take them: the head dimension
-    zero-padded to 64 or 128.
+    zero-padded to a whole number of 16-byte chunks (kernel_head_dim; no
+    change for d a multiple of 8, or of 4 in fp32).
 
     The reference accepts any d <= 128 (adasplashattention.cu:542); the
-    kernels are built for d = 64 and 128.  Zero columns add exact zeros to
-    every dot product, so scores, weights and tau are those of the unpadded
-    problem, and the padded columns of the outputs and of dQ, dK, dV are
-    zero.  The padding is a differentiable torch op: gradients reach the
-    caller's tensors through it.
+    kernels read any d that is a whole number of 16-byte chunks, in place.
+    Zero columns add exact zeros to every dot product, so scores, weights
+    and tau are those of the unpadded problem, and the padded columns of
+    the outputs and of dQ, dK, dV are zero.  The padding is a
+    differentiable torch op: gradients reach the caller's tensors through it.
     """
-    dk = kernel_head_dim(ts[0].size(-1))
+    dk = kernel_head_dim(ts[0].size(-1), ts[0].dtype)
     out = []
     for t in ts:
         if t.size(-1) != dk:
@@ -245,12 +254,51 @@ def from_kernel_layout(t: torch.Tensor, d: int, dtype: torch.dtype) -> torch.Ten
     return t
 
 
-def _aligned(t: torch.Tensor) -> torch.Tensor:
-    """Contiguous with a 16-byte aligned base (the kernels load 16-byte vectors)."""
+def strides_of(t: torch.Tensor) -> tuple:
+    """Element strides {batch, head, row} of a [B, H, N, d] operand, as the
+    C ABI takes them (a dimension of size 1 gets stride 0)."""
+    return tuple(st if n > 1 else 0 for n, st in zip(t.shape[:3], t.stride()[:3]))
+
+
+def readable_in_place(t: torch.Tensor) -> bool:
+    """Whether the kernels can read a [B, H, N, d] operand where it is (the
+    C ABI's stride rules, asa_problem.q_strides): contiguous head dimension,
+    16-byte aligned start, non-negative batch, head and row strides that are
+    whole 16-byte chunks, and a head's rows within 2^31 bytes of its first."""
+    e = chunk_elems(t.dtype)
+    if t.size(-1) > 1 and t.stride(-1) != 1:
+        return False
+    if t.data_ptr() % 16:
+        return False
+    st = strides_of(t)
+    if any(x < 0 or x % e for x in st):
+        return False
+    return ((t.size(2) - 1) * st[2] + t.size(-1)) * t.element_size() < 2 ** 31
+
+
+def kernel_operand(t: torch.Tensor) -> torch.Tensor:
+    """t itself if readable_in_place, else a contiguous, 16-byte aligned copy."""
+    if readable_in_place(t):
+        return t
     t = t.contiguous()
     if t.data_ptr() % 16:
         t = t.clone()
     return t
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous with a 16-byte aligned base (the C ABI's Out, dQ, dK, dV)."""
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _set_strides(p: _lib.Problem, **ts) -> None:
+    for name, t in ts.items():
+        arr = getattr(p, name + "_strides")
+        for i, x in enumerate(strides_of(t)):
+            arr[i] = x
 
 
 def check_tau_mode(tau_mode: str) -> int:
@@ -334,8 +382,9 @@ def splash_forward(Q, K, V, Q_idx, K_idx, alpha: float, k_keep: int, sm_scale=No
     B, H, NQ, d = Q.shape
     p = make_problem(B, H, NQ, K.shape[2], d, Q.dtype, alpha, k_keep, sm_scale, tau_mode,
                      block_m)
+    _set_strides(p, q=Q, k=K, v=V)
     st = alloc_state(p, Q.device, with_topk, with_support)
-    out = torch.empty_like(Q)
+    out = torch.empty(Q.shape, dtype=Q.dtype, device=Q.device)
     cst = st.c_struct()
     if noalloc:
         with torch.cuda.device(Q.device):
@@ -353,15 +402,16 @@ def splash_forward(Q, K, V, Q_idx, K_idx, alpha: float, k_keep: int, sm_scale=No
     return out, st
 
 
-def _as_kernel_operand(t: torch.Tensor, Q: torch.Tensor, name: str) -> torch.Tensor:
+def _as_kernel_operand(t: torch.Tensor, Q: torch.Tensor, name: str, contiguous: bool = False):
     """A [B, H, NQ, d'] operand of the backward (dOut, Out) in the layout of
-    the kernel-layout Q: padded to Q's head dimension, in Q's dtype."""
+    the kernel-layout Q: padded to Q's head dimension, in Q's dtype, read in
+    place where the C ABI allows (dOut) or contiguous (Out)."""
     dq = Q.size(-1)
     if (t.dim() != 4 or tuple(t.shape[:3]) != tuple(Q.shape[:3]) or t.size(-1) > dq
-            or kernel_head_dim(t.size(-1)) != dq):
+            or kernel_head_dim(t.size(-1), Q.dtype) != dq):
         raise ValueError(f"{name} shape {tuple(t.shape)} must equal Q shape {tuple(Q.shape)}")
-    (t,) = to_kernel_layout(t)
-    return _aligned(t.to(Q.dtype))
+    (t,) = to_kernel_layout(t.to(Q.dtype))
+    return _aligned(t) if contiguous else kernel_operand(t)
 
 
 def splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st: SplashState, alpha: float,
@@ -375,11 +425,12 @@ def splash_backward(Q, K, V, Q_idx, K_idx, out, dout, st: SplashState, alpha: fl
                      block_m=block_m_of(st, NQ))
     dout = _as_kernel_operand(dout, Q, "dOut")
     if out is not None:
-        out = _as_kernel_operand(out, Q, "Out")
+        out = _as_kernel_operand(out, Q, "Out", contiguous=True)
+    _set_strides(p, q=Q, k=K, v=V, dout=dout)
     ws = workspace(p, Q.device)
-    dQ = torch.empty_like(Q)
-    dK = torch.empty_like(K)
-    dV = torch.empty_like(V)
+    dQ = torch.empty(Q.shape, dtype=Q.dtype, device=Q.device)
+    dK = torch.empty(K.shape, dtype=K.dtype, device=K.device)
+    dV = torch.empty(V.shape, dtype=V.dtype, device=V.device)
     cst = st.c_struct()
     with torch.cuda.device(Q.device):
         rc = lib.asa_backward(ctypes.byref(p), GRAD_MODES[grad_mode], Q.data_ptr(), K.data_ptr(),

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define ASA_ABI_VERSION 6
+#define ASA_ABI_VERSION 7
 
 typedef enum asa_status {
   ASA_OK = 0,
@@ -82,7 +82,10 @@ typedef enum asa_grad_mode {
 } asa_grad_mode;
 
 /* Problem descriptor.  Q, Out, dOut, dQ: [batch, heads, nq, head_dim];
- * K, V, dK, dV: [batch, heads, nk, head_dim]; all contiguous, row-major.
+ * K, V, dK, dV: [batch, heads, nk, head_dim], row-major with the head
+ * dimension contiguous.  Out, dQ, dK and dV are contiguous; Q, K, V and
+ * dOut may have any batch, head and row strides (q_strides ... below).
+ * Every tensor pointer is 16-byte aligned.
  * Q_idx: [batch*heads, nq], K_idx: [batch*heads, nk], int32 positions.
  * Reference argument list: forward_splash(Q, K, V, Q_idx, K_idx, sm_scale,
  * alpha) (adasplashattention.cu:537-541).                                 */
@@ -91,7 +94,10 @@ typedef struct asa_problem {
   int32_t heads;
   int32_t nq;
   int32_t nk;
-  int32_t head_dim; /* 64 or 128 (reference limit: <= 128, :542)         */
+  int32_t head_dim; /* <= 128 (reference limit, :542), a multiple of 8
+                     * for bf16 / fp16 and of 4 for fp32 (one 16-byte
+                     * chunk); the kernels compute at 64 (head_dim <= 64)
+                     * or 128 and never touch the columns past head_dim */
   int32_t k_keep;   /* 1..128 (reference: compile-time 8, :17-19)        */
   int32_t block_m;  /* query rows per mask block: 64, or 32 (the
                      * reference's BLOCK_M, :8-9; reference tau mode
@@ -102,6 +108,20 @@ typedef struct asa_problem {
   float sm_scale;
   int32_t dtype;    /* asa_dtype of Q, K, V, Out, dOut, dQ, dK, dV        */
   int32_t tau_mode; /* asa_tau_mode (asa_forward; ignored by asa_backward) */
+  /* Element strides {batch, head, row} of Q, K, V and dOut (dout_strides:
+   * asa_backward only).  {0, 0, 0}: contiguous, {heads*n*head_dim,
+   * n*head_dim, head_dim}.  Otherwise each stride is >= 0 and a multiple of
+   * 8 elements for bf16 / fp16, 4 for fp32, and a head's rows lie within
+   * 2^31 bytes of its first ((n - 1) * row stride + head_dim elements), so
+   * that views such as a [batch, n, heads, head_dim] tensor transposed to
+   * [batch, heads, n, head_dim], or K and V shared across heads (head
+   * stride 0), are read in place.  No reference counterpart (the reference
+   * reads contiguous tensors through data_ptr, adasplashattention.cu:
+   * 568-571).                                                            */
+  int64_t q_strides[3];
+  int64_t k_strides[3];
+  int64_t v_strides[3];
+  int64_t dout_strides[3];
 } asa_problem;
 
 /* Per-call selection state written by asa_forward (and by

@@ -64,7 +64,13 @@ def test_query_sizes_headline():
 
 @pytest.mark.parametrize("bad,code,msg", [
     (dict(head_dim=256), 1, "Head dimension too large"),
-    (dict(head_dim=96), 2, "head_dim 96 not supported"),
+    (dict(head_dim=0), 1, "head_dim 0 must be >= 1"),
+    (dict(head_dim=50), 2, "head_dim 50 must be a multiple of 8"),
+    (dict(head_dim=6, dtype=0), 2, "head_dim 6 must be a multiple of 4"),
+    (dict(q_strides=(-64, 64, 64)), 1, "q_strides[0] = -64"),
+    (dict(k_strides=(0, 0, 68)), 1, "k_strides[2] = 68"),
+    (dict(v_strides=(0, 4, 1 << 20)), 1, "v_strides[1] = 4"),
+    (dict(dout_strides=(0, 0, 1 << 20)), 2, "dout row stride"),
     (dict(k_keep=0), 1, "k_keep"),
     (dict(k_keep=129), 1, "k_keep"),
     (dict(block_m=16), 2, "block_m"),
@@ -101,6 +107,38 @@ def test_null_pointers_are_rejected(lib):
                             ctypes.byref(st), None, None, None, None, None) == \
         _lib.ASA_ERR_INVALID_ARGUMENT
     assert "grad_mode" in lib.asa_last_error().decode()
+
+
+def test_any_whole_chunk_head_dim_and_strides_are_accepted(lib):
+    """head_dim: any multiple of 8 (16-bit) or 4 (fp32) up to 128; strides:
+    whole chunks, e.g. a [B, N, H, d] tensor viewed as [B, H, N, d] and K
+    shared across heads (head stride 0)."""
+    from splash_attention import _lib
+
+    z = _lib.Sizes()
+    for d, dt in ((8, _lib.DTYPE_BF16), (40, _lib.DTYPE_F16), (96, _lib.DTYPE_BF16),
+                  (4, _lib.DTYPE_F32), (100, _lib.DTYPE_F32), (128, _lib.DTYPE_F32)):
+        assert lib.asa_query_sizes(ctypes.byref(_problem(head_dim=d, dtype=dt)),
+                                   ctypes.byref(z)) == 0, lib.asa_last_error()
+    B, H, N, d = 4, 16, 4096, 64
+    p = _problem(q_strides=(N * H * d, d, H * d), k_strides=(N * d, 0, d),
+                 v_strides=(0, 0, 0), dout_strides=(N * H * d, d, H * d))
+    assert lib.asa_query_sizes(ctypes.byref(p), ctypes.byref(z)) == 0, lib.asa_last_error()
+
+
+def test_misaligned_tensors_are_rejected(lib):
+    from splash_attention import _lib
+
+    p = _problem()
+    st = _lib.State()
+    a, bad = 1 << 20, (1 << 20) + 8   # stand-in addresses: never dereferenced
+    rc = lib.asa_forward(ctypes.byref(p), bad, a, a, a, a, a, ctypes.byref(st), a, None)
+    assert rc == _lib.ASA_ERR_INVALID_ARGUMENT
+    assert "16-byte aligned" in lib.asa_last_error().decode()
+    rc = lib.asa_backward(ctypes.byref(p), 0, a, a, a, a, a, None, a, ctypes.byref(st), a, a,
+                          bad, a, None)
+    assert rc == _lib.ASA_ERR_INVALID_ARGUMENT
+    assert "16-byte aligned" in lib.asa_last_error().decode()
 
 
 def test_error_string_is_cleared_on_success(lib):

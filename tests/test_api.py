@@ -93,16 +93,23 @@ def test_grad_mode_validation():
                             grad_mode="bogus")
 
 
-@pytest.mark.parametrize("d,dk", [(1, 64), (40, 64), (64, 64), (65, 128), (100, 128), (128, 128)])
+@pytest.mark.parametrize("d", [1, 6, 40, 64, 65, 100, 128])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_kernel_layout_pads(d, dk, dtype):
-    """Any head dimension <= 128 runs at 64 or 128 with zero columns (scores
-    unchanged), in the caller's dtype; gradients flow back through it."""
+def test_kernel_layout_pads(d, dtype):
+    """A head dimension that is not a whole number of 16-byte chunks (8
+    elements in 16-bit types, 4 in fp32) is padded to one with zero columns
+    (scores unchanged), in the caller's dtype; gradients flow back through
+    it.  Whole-chunk head dimensions are left alone."""
+    e = 4 if dtype == torch.float32 else 8
+    dk = -(-d // e) * e
+    assert ops.kernel_head_dim(d, dtype) == dk
     g = torch.Generator().manual_seed(3)
     Q = torch.randn(1, 2, 5, d, generator=g).to(dtype).requires_grad_()
     K = torch.randn(1, 2, 7, d, generator=g).to(dtype)
     q, k = ops.to_kernel_layout(Q, K)
     assert q.shape == (1, 2, 5, dk) and k.shape == (1, 2, 7, dk)
+    if dk == d:
+        assert q is Q and k is K
     assert q.dtype == dtype
     assert torch.count_nonzero(q[..., d:]) == 0
     assert torch.equal(q[..., :d].to(dtype), Q.detach())

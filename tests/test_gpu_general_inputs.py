@@ -2,9 +2,12 @@
 against the CPU oracle at the caller's (unpadded) shape.
 
 The reference takes any head dimension up to D_MAX = 128
-(adasplashattention.cu:542).  Such inputs run on the d = 64 / 128 kernels
-with zero-padded columns (ops.to_kernel_layout), and float16 inputs on the
-float16 kernels; the default sm_scale is 1/sqrt(d) of the caller's d.
+(adasplashattention.cu:542).  A head dimension that is a whole number of
+16-byte chunks (a multiple of 8 in 16-bit types, of 4 in fp32) runs
+natively: the kernels compute at 64 or 128 and read and write only the d
+columns (no copy).  Others (d50_bf16, d6_fp32) are zero-padded to a whole
+chunk first (ops.to_kernel_layout).  float16 inputs run on the float16
+kernels; the default sm_scale is 1/sqrt(d) of the caller's d.
 Checked through the autograd function, the custom operator and the
 reference-style forward/backward.  Tolerances (max-norm relative): 1e-5
 for float32; 2e-2 for bfloat16; 4e-3 for float16 (fp32 arithmetic on
@@ -31,6 +34,8 @@ CASES = [
     ("d64_fp16", 64, torch.float16, 4e-3),
     ("d48_fp16", 48, torch.float16, 4e-3),
     ("d128_fp16", 128, torch.float16, 4e-3),
+    ("d50_bf16", 50, torch.bfloat16, 2e-2),
+    ("d6_fp32", 6, torch.float32, 1e-5),
 ]
 
 

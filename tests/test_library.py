@@ -1,5 +1,6 @@
 """torch.library registration (CPU): the custom operators exist and their
 fake implementations give the shapes and dtypes the kernels produce."""
+import pytest
 import torch
 
 import splash_attention  # noqa: F401  (registers adasplash::forward / ::backward)
@@ -25,16 +26,17 @@ def test_fake_shapes_on_meta_tensors():
     assert [tuple(x.shape) for x in g] == [(2, 3, 200, 64), (2, 3, 130, 64), (2, 3, 130, 64)]
 
 
-def test_fake_shapes_general_inputs():
-    """d not in {64, 128} and float16: the operator's output is in the
-    kernels' layout (d padded to 64, the input dtype); the gradients in the
-    caller's."""
-    Q = torch.empty(1, 2, 70, 40, device="meta", dtype=torch.float16)
-    outs = torch.ops.adasplash.forward(Q, Q, Q, None, None, 1.5, 8, 40 ** -0.5, "entmax")
-    assert (tuple(outs[0].shape), outs[0].dtype) == ((1, 2, 70, 64), torch.float16)
+@pytest.mark.parametrize("d,dk", [(40, 40), (36, 40)])
+def test_fake_shapes_general_inputs(d, dk):
+    """float16 at d = 40 (whole 16-byte chunks: taken as is) and d = 36
+    (padded to 40): the operator's output is in the kernels' layout, the
+    input dtype; the gradients in the caller's."""
+    Q = torch.empty(1, 2, 70, d, device="meta", dtype=torch.float16)
+    outs = torch.ops.adasplash.forward(Q, Q, Q, None, None, 1.5, 8, d ** -0.5, "entmax")
+    assert (tuple(outs[0].shape), outs[0].dtype) == ((1, 2, 70, dk), torch.float16)
     g = torch.ops.adasplash.backward(Q, Q, Q, None, None, outs[0], outs[0], *outs[1:], 1.5, 8,
-                                     40 ** -0.5, "entmax")
-    assert [(tuple(x.shape), x.dtype) for x in g] == [((1, 2, 70, 40), torch.float16)] * 3
+                                     d ** -0.5, "entmax")
+    assert [(tuple(x.shape), x.dtype) for x in g] == [((1, 2, 70, d), torch.float16)] * 3
 
 
 def test_benchmark_cli_parsing():
