@@ -303,6 +303,11 @@ enum SweepMode : int {
   kGivenScores = 2  // caller-given scores
 };
 
+// How the score pass addresses K: rows of exactly D elements at hd = D
+// (compile-time strides), rows at a run-time stride with hd = D, or any
+// stride and hd (column tests).
+enum KLayout : int { kKDense = 0, kKRows = 1, kKGeneral = 2 };
+
 // One wave's quarter of a 64-key tile (keys 16 w .. 16 w + 15) as MFMA A
 // operands, loaded straight from global memory (L2) into registers: lane
 // (c, g) holds key 16 w + c at the head-dimension slots that rows_x_frag
@@ -322,16 +327,17 @@ template <typename T, int D> struct KQuarter16 {
   // loads; a whole-row load with the operands rebuilt by two DPP row
   // rotations per register measured the same sweep time, which the
   // candidate appends, not the loads, set.)
-  // GENERAL: rows snb bytes apart (32-bit offsets from the head's first
-  // row, which the C ABI bounds below 2^31), columns >= hd read as zero;
-  // else rows of exactly D elements, hd = D.
-  template <bool GENERAL>
+  // KL (KLayout): rows of exactly D elements (kKDense), or rows snb bytes
+  // apart (32-bit offsets from the head's first row, which the C ABI
+  // bounds below 2^31) with hd = D (kKRows) or with columns >= hd read as
+  // zero (kKGeneral).
+  template <int KL>
   __device__ __forceinline__ void load(const T* Kb, int key, int NK, uint32_t snb, int hd, int g) {
     const int kk = key < NK ? key : 0;
-    if constexpr (GENERAL) {
+    if constexpr (KL != kKDense) {
       const unsigned char* src = reinterpret_cast<const unsigned char*>(Kb) + (uint32_t(kk) * snb + 16u * g);
       for (int s = 0; s < D / 32; ++s)
-        a[s] = 32 * s + 8 * g < hd ? *reinterpret_cast<const V8*>(src + 64 * s) : V8{};
+        a[s] = KL == kKRows || 32 * s + 8 * g < hd ? *reinterpret_cast<const V8*>(src + 64 * s) : V8{};
     } else {
       const T* src = Kb + size_t(kk) * D + 8 * g;
       for (int s = 0; s < D / 32; ++s) a[s] = *reinterpret_cast<const V8*>(src + 32 * s);
@@ -347,13 +353,13 @@ template <int D> struct KQuarter<u16, D> : KQuarter16<u16, D> {};
 template <int D> struct KQuarter<h16, D> : KQuarter16<h16, D> {};
 template <int D> struct KQuarter<float, D> {
   f32x4 a[D / 16];
-  template <bool GENERAL>
+  template <int KL>
   __device__ __forceinline__ void load(const float* Kb, int key, int NK, uint32_t snb, int hd, int g) {
     const int kk = key < NK ? key : 0;
-    if constexpr (GENERAL) {
+    if constexpr (KL != kKDense) {
       const unsigned char* src = reinterpret_cast<const unsigned char*>(Kb) + (uint32_t(kk) * snb + 16u * g);
       for (int j = 0; j < D / 16; ++j)
-        a[j] = 16 * j + 4 * g < hd ? *reinterpret_cast<const f32x4*>(src + 64 * j) : f32x4{};
+        a[j] = KL == kKRows || 16 * j + 4 * g < hd ? *reinterpret_cast<const f32x4*>(src + 64 * j) : f32x4{};
     } else {
       const float* src = Kb + size_t(kk) * D + 4 * g;
       for (int j = 0; j < D / 16; ++j) a[j] = *reinterpret_cast<const f32x4*>(src + 16 * j);
@@ -431,11 +437,10 @@ constexpr int ring_bytes() { return 4 * ring_tiles<D, R>() * 32 * D; }
 template <typename T, int D, int R>
 constexpr int select_waves_per_simd() { return sizeof(T) == 2 && D == 64 && R == 2 ? 3 : 1; }
 
-// WIDE: K rows of exactly D elements (hd = D, row stride D): compile-time
-// addressing, no column tests, and with 16-bit inputs sweep 1 reads K
-// through the LDS ring (whose loads read whole rows).  Else any row stride
-// and hd.
-template <typename T, int D, int MODE, int R, bool WIDE>
+// KL: the K layout (KLayout).  With hd = D (kKDense, kKRows) there are no
+// column tests, and with 16-bit inputs sweep 1 reads K through the LDS ring
+// (whose loads read whole rows).
+template <typename T, int D, int MODE, int R, int KL>
 __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void select_kernel(SelectParams p) {
   constexpr bool kExact = MODE != kRawDots;
   constexpr bool kTiles = MODE != kGivenScores;
@@ -562,7 +567,7 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
     if (nvis == 0) return;  // block-uniform
     KQuarter<T, D> kq[2];
     auto fetch = [&](KQuarter<T, D>& f, int e) {
-      f.template load<!WIDE>(Kb, (e & 0xffffff) * kBlock + kq0, NK, ksnb, p.d.hd, g);
+      f.template load<KL>(Kb, (e & 0xffffff) * kBlock + kq0, NK, ksnb, p.d.hd, g);
     };
     // The loads are unconditional (past the end of the list they repeat its
     // last tile), so the number in flight is the same on every path and the
@@ -644,7 +649,7 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
   constexpr int kRpi = kWave / kCpr;       // rows per DMA instruction
   auto qsw = [](int r) { return D == 64 ? (r >> 1) & 7 : r & 15; };
   constexpr int kRing = ring_tiles<D, R>();
-  constexpr bool kRingSweep = kTiles && is_half<T> && WIDE;
+  constexpr bool kRingSweep = kTiles && is_half<T> && KL != kKGeneral;
   auto sweep_ring = [&](auto u_tag, auto&& body) {
     constexpr int U = decltype(u_tag)::value;
     if (nvis == 0) return;  // block-uniform
@@ -656,8 +661,13 @@ __global__ __launch_bounds__(kThreads, (select_waves_per_simd<T, D, R>())) void 
       unsigned char* dst = ringw + slot * kSlot;
       for (int j = 0; j < kCh; ++j) {
         const int r = kRpi * j + L / kCpr, key = kq + r;
-        const T* src = Kb + size_t(key < NK ? key : 0) * D + 8 * ((L % kCpr) ^ qsw(r));
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+        const int kk = key < NK ? key : 0, ch = (L % kCpr) ^ qsw(r);
+        const void* src;
+        if constexpr (KL == kKDense)
+          src = Kb + size_t(kk) * D + 8 * ch;
+        else
+          src = reinterpret_cast<const unsigned char*>(Kb) + (uint32_t(kk) * ksnb + 16u * ch);
+        __builtin_amdgcn_global_load_lds(src,
                                          (__attribute__((address_space(3))) void*)(dst + j * kWave * 16),
                                          16, 0, 0);
       }
@@ -1094,11 +1104,11 @@ __global__ __launch_bounds__(kThreads) void tau_compact_kernel(SelectParams p, C
   }
 }
 
-template <typename T, int D, int MODE, int R, bool WIDE>
+template <typename T, int D, int MODE, int R, int KL>
 hipError_t launch_one(const SelectParams& p, hipStream_t s) {
   const SelLayout l = sel_layout(p.d.k, p.cap, p.d.nKB);
-  auto kern = select_kernel<T, D, MODE, R, WIDE>;
-  if (WIDE && is_half<T> && MODE != kGivenScores && ring_bytes<D, R>() > l.tkey)
+  auto kern = select_kernel<T, D, MODE, R, KL>;
+  if (KL != kKGeneral && is_half<T> && MODE != kGivenScores && ring_bytes<D, R>() > l.tkey)
     return hipErrorInvalidValue;
   if (l.total > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -1109,14 +1119,17 @@ hipError_t launch_one(const SelectParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// The WIDE variant (K rows of D elements) for the 16-bit MFMA sweeps with
-// raw dots (the usual scale > 0); the others take the general loads (and
+// The hd = D variants (kKDense, kKRows) for the 16-bit MFMA sweeps with raw
+// dots (the usual scale > 0); the others take the general loads (and
 // sweep 1 on the register path).
 template <typename T, int D, int MODE, int R>
 hipError_t launch_ring(const SelectParams& p, hipStream_t s) {
   if constexpr (is_half<T> && MODE == kRawDots)
-    if (p.d.hd == D && p.lk.sn == D) return launch_one<T, D, MODE, R, true>(p, s);
-  return launch_one<T, D, MODE, R, false>(p, s);
+    if (p.d.hd == D) {
+      if (p.lk.sn == D) return launch_one<T, D, MODE, R, kKDense>(p, s);
+      return launch_one<T, D, MODE, R, kKRows>(p, s);
+    }
+  return launch_one<T, D, MODE, R, kKGeneral>(p, s);
 }
 
 // Class sets per (row, position): more sets tighten the sweep-2 floor; the

@@ -359,6 +359,12 @@ def main():
     ap.add_argument("--no-dense-baseline", action="store_true")
     ap.add_argument("--no-exact-line", action="store_true",
                     help="skip the exact_tau_mode entry (the other tau mode, same workload)")
+    ap.add_argument("--layout", default="bhnd", choices=["bhnd", "bnhd"],
+                    help="bhnd: contiguous [B, H, N, d] operands (the headline); bnhd: Q, K, V, "
+                         "dO stored [B, N, H, d] and passed as transposed [B, H, N, d] views "
+                         "(read in place by the strided kernel variants; the step then calls "
+                         "the ops-level forward/backward, so autograd's gradient layout copies "
+                         "stay out of the timed region)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 plain device copies of 256 MiB (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -394,6 +400,18 @@ def main():
         out = sa.splash_attention(q, k, v, idx, idx, alpha, k_keep, scale, args.grad_mode,
                                   args.tau_mode)
         out.backward(dO)
+
+    if args.layout == "bnhd":
+        # the same values, stored [B, N, H, d]: views with row stride H d
+        qt, kt, vt, dOt = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (Q, K, V, dO))
+        qt, kt, vt, _, _ = sa.ops.check_inputs(qt, kt, vt, idx, idx)
+        assert not qt.is_contiguous()  # read in place, not copied
+
+        def step():
+            out, st = sa.ops.splash_forward(qt, kt, vt, idx, idx, alpha, k_keep, scale,
+                                            tau_mode=args.tau_mode)
+            sa.ops.splash_backward(qt, kt, vt, idx, idx, out, dOt, st, alpha, k_keep, scale,
+                                   args.grad_mode)
 
     for _ in range(args.warmup):
         step()
@@ -466,6 +484,7 @@ def main():
                    "B": B, "H": H, "N": N, "d": d, "alpha": alpha, "k_keep": k_keep,
                    "sm_scale": scale, "mask": "causal", "block": "64x64",
                    "grad_mode": args.grad_mode, "tau_mode": args.tau_mode,
+                   "layout": args.layout,
                    "parallelism": "single GPU",
                    "active_block_pairs": nnzb,
                    "support_pairs": nsup,
