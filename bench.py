@@ -53,8 +53,8 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "5e5aa603a6d546ee"
-HBM_TRAFFIC = {'bounds': 1110153, 'select': 138301030, 'tau': 34745447, 'tau_compact': 37483839, 'refine': 109730098, 'compact': 2744259, 'forward': 314870810, 'bwd_dq_sparse': 240781333, 'bwd_dkdv_sparse': 287896791}
+HBM_TRAFFIC_SOURCES = "3aaee9be14ac4c27"
+HBM_TRAFFIC = {'bounds': 1109175, 'select': 138735778, 'tau': 34745847, 'tau_compact': 37473512, 'refine': 110041449, 'compact': 2744943, 'forward': 330182086, 'bwd_dq_sparse': 240754922, 'bwd_dkdv_sparse': 287731122}
 
 
 def source_hash() -> str:
