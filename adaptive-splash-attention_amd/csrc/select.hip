@@ -380,7 +380,12 @@ struct SelLayout {
   int cand, cm, scm, scr, tk, tkey, fl, cnt, ctl, bits, vlist, total;
 };
 __host__ __device__ inline int align_up(int x, int a) { return (x + a - 1) / a * a; }
-__host__ __device__ inline int classes_per_lane(int k) { return k <= 32 ? 2 : 4; }
+// Class sets per (row, position) of sweep 1: 4 tighten the sweep-2 floor
+// (fewer candidates) but double the class-maxima exchange in LDS; up to
+// k = 64 the exchange at 2 sets keeps two select blocks per compute unit
+// (at d = 128, k = 64: 68 KB of LDS and 199 VGPRs against 86 KB and 257
+// for 4 sets, measured 11.8 against 17.4 ms at the c4 shape).
+__host__ __device__ inline int classes_per_lane(int k) { return k <= 64 ? 2 : 4; }
 // Sweep-2 value scratch: 16 floats per lane, the lane's 16-byte chunk j
 // stored at chunk j ^ ((lane >> 1) & 3), so that the 8 lanes a 16-byte
 // store serves per cycle hit distinct banks.
@@ -1132,8 +1137,7 @@ hipError_t launch_ring(const SelectParams& p, hipStream_t s) {
   return launch_one<T, D, MODE, R, kKGeneral>(p, s);
 }
 
-// Class sets per (row, position): more sets tighten the sweep-2 floor; the
-// larger k, the more candidates a loose floor admits.
+// Class sets per (row, position): classes_per_lane.
 template <typename T, int D, int MODE>
 hipError_t launch_r(const SelectParams& p, hipStream_t s) {
   if (classes_per_lane(p.d.k) == 2) return launch_ring<T, D, MODE, 2>(p, s);
