@@ -201,9 +201,11 @@ __global__ __launch_bounds__(kThreads) void forward_kernel(ForwardParams p) {
 // as c (s - tau / c) instead of once, an ulp-level difference from
 // forward_kernel.
 // DENSE: Q, K, V and Out contiguous [B, H, N, D] (hd = D), compile-time
-// strides; else any strides and hd.
+// strides; else any strides and hd.  Three waves per SIMD at d = 64; at
+// d = 128 its 70 KB of LDS allow two blocks per compute unit, and the
+// accumulators of both blocks' rows take up to 255 VGPRs.
 template <typename T, int D, int PC, bool EMIT, bool HALF, bool DENSE>
-__global__ __launch_bounds__(kThreads, 3) void forward_pair_kernel(ForwardParams p) {
+__global__ __launch_bounds__(kThreads, (D == 64 ? 3 : 2)) void forward_pair_kernel(ForwardParams p) {
   static_assert(is_half<T>, "16-bit inputs only");
   __shared__ FwdSmem<T, D> sm;
   using St = Stager<T, D>;
@@ -426,7 +428,7 @@ inline bool pair_fold_ok(const ForwardParams& p) {
 
 template <typename T, int D, bool EMIT, bool HALF>
 hipError_t launch_tde(const ForwardParams& p, hipStream_t s) {
-  if constexpr (is_half<T> && D == 64)
+  if constexpr (is_half<T>)
     if (pair_fold_ok(p)) return launch_pair<T, D, EMIT, HALF>(p, s);
   dim3 grid(p.d.nQB * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
