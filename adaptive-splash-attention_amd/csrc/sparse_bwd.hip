@@ -403,16 +403,14 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
     rank += (cnt16[i] > rn || (cnt16[i] == rn && i < c16)) ? 1 : 0;
   }
 
+  if (lane < 16) s_rank[w][rank] = lane;  // rows by descending count
   if (total <= kFlat) {  // wave-uniform
     // ---- balanced path.  Every row's whole list in s_flat (tile order,
     // then bit 16 g + 4 f + r: the chunked path's order); the lane groups
     // take the rows in a snake over the descending counts, so each group's
     // total is close to the mean and the lock-step loop runs near its
     // length.
-    if (lane < 16) {
-      s_off[w][lane] = off;
-      s_rank[w][rank] = lane;
-    }
+    if (lane < 16) s_off[w][lane] = off;
     // the first row's q and dO load while the lists are built
     prefetch(s_rank[w][grp]);
     int base = off;
@@ -469,11 +467,12 @@ __global__ __launch_bounds__(kThreads, 4) void dq_sparse_kernel(BackwardParams p
 
   // ---- chunked path (a wave with more than kFlat listed keys): rows in
   // rounds of RPR, each row's keys listed kRowList at a time per chunk of
-  // tiles and drained in lock step
+  // tiles and drained in lock step.  A round takes RPR rows of consecutive
+  // count ranks (the lock step lasts as long as its longest list).
   int* list = s_list[w][grp];
   for (int r0 = 0; r0 < 16; r0 += RPR) {
-    prefetch(r0 + grp);
-    start_row(r0 + grp);
+    prefetch(s_rank[w][r0 + grp]);
+    start_row(s_rank[w][r0 + grp]);
     auto drain = [&](int cnt) {
       const int nmax = groups_max<LPR>(cnt);
       for (int q = 0; q < nmax; q += kBatchQ) step(list, q, cnt);
