@@ -53,8 +53,8 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "3aaee9be14ac4c27"
-HBM_TRAFFIC = {'bounds': 1109175, 'select': 138735778, 'tau': 34745847, 'tau_compact': 37473512, 'refine': 110041449, 'compact': 2744943, 'forward': 330182086, 'bwd_dq_sparse': 240754922, 'bwd_dkdv_sparse': 287731122}
+HBM_TRAFFIC_SOURCES = "f741fe856863cb46"
+HBM_TRAFFIC = {'bounds': 1109174, 'select': 138709362, 'tau': 34745773, 'tau_compact': 37473437, 'refine': 109561948, 'compact': 2744942, 'forward': 329157597, 'bwd_dq_sparse': 240753426, 'bwd_dkdv_sparse': 287677077}
 
 
 def source_hash() -> str:
