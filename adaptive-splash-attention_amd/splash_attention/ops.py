@@ -256,15 +256,21 @@ def from_kernel_layout(t: torch.Tensor, d: int, dtype: torch.dtype) -> torch.Ten
 
 def strides_of(t: torch.Tensor) -> tuple:
     """Element strides {batch, head, row} of a [B, H, N, d] operand, as the
-    C ABI takes them (a dimension of size 1 gets stride 0)."""
-    return tuple(st if n > 1 else 0 for n, st in zip(t.shape[:3], t.stride()[:3]))
+    C ABI takes them.  A dimension of size 1 gets its contiguous stride (its
+    stride is never used), so the ABI's mark for a contiguous operand, all
+    three strides 0, comes out only for an operand broadcast along all
+    three dimensions, which readable_in_place rejects."""
+    B, H, N, d = t.shape
+    contiguous = (H * N * d, N * d, d)
+    return tuple(st if n > 1 else c for n, st, c in zip((B, H, N), t.stride()[:3], contiguous))
 
 
 def readable_in_place(t: torch.Tensor) -> bool:
     """Whether the kernels can read a [B, H, N, d] operand where it is (the
     C ABI's stride rules, asa_problem.q_strides): contiguous head dimension,
     16-byte aligned start, non-negative batch, head and row strides that are
-    whole 16-byte chunks, and a head's rows within 2^31 bytes of its first."""
+    whole 16-byte chunks, not all three 0, and a head's rows within 2^31
+    bytes of its first."""
     e = chunk_elems(t.dtype)
     if t.size(-1) > 1 and t.stride(-1) != 1:
         return False
@@ -272,6 +278,8 @@ def readable_in_place(t: torch.Tensor) -> bool:
         return False
     st = strides_of(t)
     if any(x < 0 or x % e for x in st):
+        return False
+    if st == (0, 0, 0):  # broadcast along batch, heads and rows: the ABI's "contiguous" mark
         return False
     return ((t.size(2) - 1) * st[2] + t.size(-1)) * t.element_size() < 2 ** 31
 

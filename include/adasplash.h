@@ -115,7 +115,10 @@ typedef struct asa_problem {
    * 2^31 bytes of its first ((n - 1) * row stride + head_dim elements), so
    * that views such as a [batch, n, heads, head_dim] tensor transposed to
    * [batch, heads, n, head_dim], or K and V shared across heads (head
-   * stride 0), are read in place.  No reference counterpart (the reference
+   * stride 0), are read in place.  The stride of a dimension of size 1 is
+   * not used.  {0, 0, 0} always means contiguous, so an operand broadcast
+   * along all three (every stride 0) is passed materialised.  No
+   * reference counterpart (the reference
    * reads contiguous tensors through data_ptr, adasplashattention.cu:
    * 568-571).                                                            */
   int64_t q_strides[3];

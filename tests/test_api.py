@@ -122,6 +122,34 @@ def test_kernel_layout_pads(d, dtype):
     assert torch.equal(Q.grad, torch.full_like(Q, 2))
 
 
+def test_operand_strides_for_the_c_abi():
+    """Strides handed to the C ABI ({batch, head, row}, elements): a size-1
+    dimension gets its contiguous stride, so {0, 0, 0} (the ABI's mark for
+    a contiguous operand) never stands for a broadcast one; an operand
+    broadcast along batch, heads and rows alike is copied instead of read
+    in place (read in place, its all-zero strides would send the kernels
+    over B*H*N rows of a one-row buffer)."""
+    d = 64
+    x = torch.zeros(2, 3, 5, d, dtype=torch.bfloat16)
+    assert ops.strides_of(x) == (3 * 5 * d, 5 * d, d) and ops.readable_in_place(x)
+    # one head's K shared by 4 heads, a single key row (batch 1)
+    k1 = torch.zeros(1, 1, 1, d, dtype=torch.bfloat16)
+    kh = k1.expand(1, 4, 1, d)
+    assert ops.strides_of(kh) == (4 * d, 0, d)
+    assert ops.readable_in_place(kh) and ops.kernel_operand(kh) is kh
+    # shared across heads with several rows: head stride 0, rows in place
+    k2 = torch.zeros(2, 1, 7, d, dtype=torch.bfloat16).expand(2, 3, 7, d)
+    assert ops.strides_of(k2) == (7 * d, 0, d) and ops.readable_in_place(k2)
+    # one row broadcast along all three: copied
+    kb = k1.expand(2, 3, 5, d)
+    assert ops.strides_of(kb) == (0, 0, 0) and not ops.readable_in_place(kb)
+    c = ops.kernel_operand(kb)
+    assert c is not kb and c.is_contiguous() and torch.equal(c, kb)
+    assert ops.strides_of(c) == (3 * 5 * d, 5 * d, d)
+    # a single row in every dimension: contiguous either way
+    assert ops.strides_of(k1) == (d, d, d) and ops.readable_in_place(k1)
+
+
 def test_reference_order_defaults_are_the_compiled_references():
     """forward/backward default to the compiled reference's K_KEEP = 8 and
     BLOCK_M = 32 (adasplashattention.cu:8-9, :17-19) and apply its host

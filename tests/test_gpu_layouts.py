@@ -88,6 +88,46 @@ def test_keys_shared_across_heads(dev, name, d, dtype):
         assert torch.equal(g, w.sum(1, keepdim=True))
 
 
+def test_broadcast_keys_single_row_and_all_dims(dev):
+    """One key row shared by every head (NK = 1, head stride 0) and one key
+    row repeated over the heads and rows of a single batch (head and row
+    strides 0) are read in place; one key row broadcast along batch, heads
+    and rows (all strides 0, the C ABI's mark for a contiguous operand) is
+    copied first.  Each equals the call on contiguous copies bit for bit."""
+    print("[layouts] broadcast key rows", flush=True)
+    d, H = 64, 4
+    g = torch.Generator().manual_seed(49)
+    Q = torch.randn(1, H, 96, d, generator=g).to(torch.bfloat16).to(dev)
+    k1 = torch.randn(1, 1, 1, d, generator=g).to(torch.bfloat16).to(dev)
+    v1 = torch.randn(1, 1, 1, d, generator=g).to(torch.bfloat16).to(dev)
+    dO = torch.randn(1, H, 96, d, generator=g).to(torch.bfloat16).to(dev)
+    qi = causal_idx(H, 96).to(dev)
+    ki = torch.zeros(H, 1, dtype=torch.int32, device=dev)
+    Kh, Vh = k1.expand(1, H, 1, d), v1.expand(1, H, 1, d)
+    _, k, v, _, _ = sa.ops.check_inputs(Q, Kh, Vh, qi, ki)
+    assert k is Kh and v is Vh
+    got = _run(dev, Q, Kh, Vh, dO, qi, ki, "entmax")
+    want = _run(dev, Q, Kh.contiguous(), Vh.contiguous(), dO, qi, ki, "entmax")
+    for n, a, b in zip(("out", "dQ", "dK", "dV"), got, want):
+        assert torch.equal(a, b), f"{n}: head-shared key row differs"
+    N = 80
+    for B in (1, 2):
+        Qb = Q[:, :, :N].expand(B, H, N, d).contiguous()
+        dOb = dO[:, :, :N].expand(B, H, N, d).contiguous()
+        qb = causal_idx(B * H, N).to(dev)
+        Kb, Vb = k1.expand(B, H, N, d), v1.expand(B, H, N, d)
+        _, k, v, _, _ = sa.ops.check_inputs(Qb, Kb, Vb, qb, qb)
+        if B == 1:
+            assert sa.ops.strides_of(Kb) == (H * N * d, 0, 0) and k is Kb
+        else:
+            assert sa.ops.strides_of(Kb) == (0, 0, 0)
+            assert k is not Kb and k.is_contiguous() and torch.equal(k, Kb)
+        got = _run(dev, Qb, Kb, Vb, dOb, qb, qb, "entmax")
+        want = _run(dev, Qb, Kb.contiguous(), Vb.contiguous(), dOb, qb, qb, "entmax")
+        for n, a, b in zip(("out", "dQ", "dK", "dV"), got, want):
+            assert torch.equal(a, b), f"{n}: broadcast key rows differ (batch {B})"
+
+
 def test_strided_dout_and_reference_order_calls(dev):
     """The reference-order backward with a transposed dOut and 32-row mask
     blocks (its defaults) equals the contiguous call; so does forward."""
