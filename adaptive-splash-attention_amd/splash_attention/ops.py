@@ -303,7 +303,13 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
 
 
 def _set_strides(p: _lib.Problem, **ts) -> None:
+    """The operands' strides into the problem descriptor; raises for an
+    operand the kernels cannot read in place (pass it through check_inputs
+    or kernel_operand first)."""
     for name, t in ts.items():
+        if not readable_in_place(t):
+            raise ValueError(f"{name}: shape {tuple(t.shape)} with strides {tuple(t.stride())} "
+                             "cannot be read in place; pass it through check_inputs first")
         arr = getattr(p, name + "_strides")
         for i, x in enumerate(strides_of(t)):
             arr[i] = x

@@ -148,6 +148,14 @@ def test_operand_strides_for_the_c_abi():
     assert ops.strides_of(c) == (3 * 5 * d, 5 * d, d)
     # a single row in every dimension: contiguous either way
     assert ops.strides_of(k1) == (d, d, d) and ops.readable_in_place(k1)
+    # the ops-level entry points refuse what they cannot read in place
+    from splash_attention import _lib
+    prob = _lib.Problem()
+    ops._set_strides(prob, q=x, k=kh)
+    assert tuple(prob.k_strides) == (4 * d, 0, d)
+    for bad in (kb, torch.zeros(2, 3, 5, 2 * d, dtype=torch.bfloat16)[..., ::2]):
+        with pytest.raises(ValueError, match="cannot be read in place"):
+            ops._set_strides(prob, k=bad)
 
 
 def test_reference_order_defaults_are_the_compiled_references():
