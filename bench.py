@@ -12,7 +12,11 @@ HBM.  value = effective TFLOP/s with the FlashAttention
 convention for dense causal fwd+bwd, 3.5 * 4 * BH * d * N^2 / 2 = 481.0 GFLOP
 per step.
 
-The K timed steps run uninstrumented.  Per-kernel durations come from a
+The K timed steps run uninstrumented, after W untimed ones.  The default
+W = 100 (about 85 ms of GPU work) times the steady state: measured with
+HIP events per step, the step time of a fresh process falls from ~0.91 to
+~0.81 ms over its first ~40 steps of sustained load (the GPU's clocks
+settling) and then holds.  Per-kernel durations come from a
 second pass of K steps in which the library records HIP events around each
 launch on the launch stream (asa_profile_*); the roofline of each kernel
 uses its algorithmic FLOPs / bytes per launch.
@@ -22,7 +26,7 @@ The line also carries the same step with the other tau mode
 i.e. dense alpha-entmax attention computed block-sparsely), timed the same
 way; --tau-mode exact swaps the two.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--tau-mode reference|exact]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 100] [--tau-mode reference|exact]
 """
 from __future__ import annotations
 
@@ -349,8 +353,8 @@ def cpu_baseline(heads=16, warmup=3, trials=10):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--grad-mode", default="entmax", choices=["entmax", "reference"])
     ap.add_argument("--tau-mode", default="reference", choices=["reference", "exact"],
                     help="reference: the reference's top-k threshold (the headline); exact: "
