@@ -57,8 +57,8 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "f741fe856863cb46"
-HBM_TRAFFIC = {'bounds': 1109174, 'select': 138709362, 'tau': 34745773, 'tau_compact': 37473437, 'refine': 109561948, 'compact': 2744942, 'forward': 329157597, 'bwd_dq_sparse': 240753426, 'bwd_dkdv_sparse': 287677077}
+HBM_TRAFFIC_SOURCES = "37d9703f77144a7d"
+HBM_TRAFFIC = {'bounds': 1109588, 'select': 138689444, 'tau': 34745517, 'tau_compact': 37473416, 'refine': 109806461, 'compact': 2744261, 'forward': 329855928, 'bwd_dq_sparse': 240750589, 'bwd_dkdv_sparse': 287664734}
 
 
 def source_hash() -> str:
