@@ -27,6 +27,44 @@ def test_header_declares_what_the_binding_binds():
     assert _declared() == sorted(_lib.EXPORTS)
 
 
+def _header_fields(struct):
+    """Field names of `typedef struct <struct> { ... }` in the C header, in order."""
+    text = open(os.path.join(ROOT, "include", "adasplash.h")).read()
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), text, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    names = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        # "type a, b, c" / "type *a" / "type a[3]"
+        m = re.match(r"^(?:const\s+)?\w+\s*\**\s*(.*)$", decl, re.S)
+        for part in m.group(1).split(","):
+            names.append(re.sub(r"[\s*]|\[.*\]", "", part))
+    return names
+
+
+def _integration_fields(cls):
+    """Field names of the ctypes class `cls` in INTEGRATION.md's binding example."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = re.search(r"class %s\(ctypes\.Structure\):\s*_fields_ = (.*?\])\n\n" % cls, text, re.S)
+    return re.findall(r'"(\w+)"', block.group(1))
+
+
+def test_struct_layouts_agree_header_binding_and_docs():
+    """asa_problem, asa_state and asa_sizes: the header, the package's ctypes
+    binding and INTEGRATION.md's example list the same fields in the same
+    order (a caller whose struct lacks a trailing field, such as the state's
+    status word, hands the library memory past its struct)."""
+    from splash_attention import _lib
+
+    for struct, cls in (("asa_problem", _lib.Problem), ("asa_state", _lib.State),
+                        ("asa_sizes", _lib.Sizes)):
+        want = _header_fields(struct)
+        assert [f[0] for f in cls._fields_] == want, struct
+        assert _integration_fields(cls.__name__) == want, struct
+
+
 def test_library_exports_every_declared_symbol(lib):
     for name in _declared():
         assert hasattr(lib, name), name
