@@ -2,7 +2,8 @@
 //
 // Reference: build_lookup_kernel (adasplashattention.cu:219-242), which
 // builds the query-major list (Qi_ptr / Qi_idx) with one serial thread per
-// (batch, head).  Here two 256-thread blocks per (batch, head) build
+// (batch, head).  Here 256-thread blocks (two per (batch, head), or one
+// per 32 mask lines for masks too large for LDS) build
 //   query-major:  q_ptr[nQB+1], q_list[nQB*nKB]  (same layout as Qi_ptr/Qi_idx)
 //   key-major:    k_ptr[nKB+1], k_list[nKB*nQB]  (feeds the atomic-free dK/dV)
 // with lists in ascending block order and zero-filled tails.  A wave takes
@@ -52,8 +53,8 @@ hipError_t launch_fold_halves(const uint8_t* half, uint8_t* mask, int BH, int NQ
 }
 
 hipError_t launch_compact(const CompactParams& p, hipStream_t s) {
-  hipLaunchKernelGGL(compact_kernel, dim3(2 * p.BH), dim3(kThreads), compact_detail::compact_lds_bytes(p),
-                     s, p);
+  hipLaunchKernelGGL(compact_kernel, dim3(compact_detail::compact_grid(p)), dim3(kThreads),
+                     compact_detail::compact_lds_bytes(p), s, p);
   return hipGetLastError();
 }
 

@@ -1100,12 +1100,14 @@ __global__ __launch_bounds__(kThreads) void tau_kernel(SelectParams p) {
 // score pass wrote): one launch, the compaction running beside the tau
 // rows instead of after them.
 template <int AC, int KMAX>
-__global__ __launch_bounds__(kThreads) void tau_compact_kernel(SelectParams p, CompactParams cp, int ntau) {
-  if (int(blockIdx.x) < ntau) {  // block-uniform
-    tau_row<AC, KMAX>(p, blockIdx.x);
-  } else {
+// The compaction's blocks come first: each runs longer than a block of tau
+// rows, and on large masks they are many (compact_grid).
+__global__ __launch_bounds__(kThreads) void tau_compact_kernel(SelectParams p, CompactParams cp, int ncomp) {
+  if (int(blockIdx.x) < ncomp) {  // block-uniform
     extern __shared__ int sm[];
-    compact_detail::compact_block(cp, sm, int(blockIdx.x) - ntau);
+    compact_detail::compact_block(cp, sm, blockIdx.x);
+  } else {
+    tau_row<AC, KMAX>(p, int(blockIdx.x) - ncomp);
   }
 }
 
@@ -1188,25 +1190,26 @@ hipError_t launch_tau(const SelectParams& p, hipStream_t s) {
 hipError_t launch_tau_compact(const SelectParams& p, const CompactParams& cp, hipStream_t s) {
   const size_t rows = size_t(p.d.BH) * p.d.NQ;
   const int ntau = int((rows + kThreads - 1) / kThreads);
-  const dim3 grid(unsigned(ntau + 2 * cp.BH));
+  const int ncomp = compact_detail::compact_grid(cp);
+  const dim3 grid(unsigned(ntau + ncomp));
   const size_t lds = compact_detail::compact_lds_bytes(cp);
   const bool reg = p.d.k <= 32;  // the row's values fit in registers
   switch (alpha_class_of(p.d.alpha)) {
     case kA15:
-      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kA15, 32>), grid, dim3(kThreads), lds, s, p, cp, ntau);
-      else hipLaunchKernelGGL((tau_compact_kernel<kA15, 0>), grid, dim3(kThreads), lds, s, p, cp, ntau);
+      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kA15, 32>), grid, dim3(kThreads), lds, s, p, cp, ncomp);
+      else hipLaunchKernelGGL((tau_compact_kernel<kA15, 0>), grid, dim3(kThreads), lds, s, p, cp, ncomp);
       break;
     case kA20:
-      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kA20, 32>), grid, dim3(kThreads), lds, s, p, cp, ntau);
-      else hipLaunchKernelGGL((tau_compact_kernel<kA20, 0>), grid, dim3(kThreads), lds, s, p, cp, ntau);
+      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kA20, 32>), grid, dim3(kThreads), lds, s, p, cp, ncomp);
+      else hipLaunchKernelGGL((tau_compact_kernel<kA20, 0>), grid, dim3(kThreads), lds, s, p, cp, ncomp);
       break;
     case kA125:
-      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kA125, 32>), grid, dim3(kThreads), lds, s, p, cp, ntau);
-      else hipLaunchKernelGGL((tau_compact_kernel<kA125, 0>), grid, dim3(kThreads), lds, s, p, cp, ntau);
+      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kA125, 32>), grid, dim3(kThreads), lds, s, p, cp, ncomp);
+      else hipLaunchKernelGGL((tau_compact_kernel<kA125, 0>), grid, dim3(kThreads), lds, s, p, cp, ncomp);
       break;
     default:
-      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kAGen, 32>), grid, dim3(kThreads), lds, s, p, cp, ntau);
-      else hipLaunchKernelGGL((tau_compact_kernel<kAGen, 0>), grid, dim3(kThreads), lds, s, p, cp, ntau);
+      if (reg) hipLaunchKernelGGL((tau_compact_kernel<kAGen, 32>), grid, dim3(kThreads), lds, s, p, cp, ncomp);
+      else hipLaunchKernelGGL((tau_compact_kernel<kAGen, 0>), grid, dim3(kThreads), lds, s, p, cp, ncomp);
       break;
   }
   return hipGetLastError();

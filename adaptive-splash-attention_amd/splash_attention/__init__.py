@@ -68,11 +68,13 @@ def forward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, k_keep: int = 
 
 
 def backward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, dOut, k_keep: int = 8,
-             grad_mode: str = "reference", block_m: int = 32, fix_nonfinite: bool = True):
+             grad_mode: str = "reference", block_m: int = 32, fix_nonfinite: bool = True,
+             bwd_passes: str = "support"):
     """Reference-compatible native backward (adasplashattention.cu:611-700):
     reruns the selection, then returns [dQ, dK, dV].  Defaults, ``sm_scale``
     and ``fix_nonfinite`` as in ``forward`` (the gradients' fix-up is
-    :684-697, with the names dQ, dK, dV in the warnings)."""
+    :684-697, with the names dQ, dK, dV in the warnings).  ``bwd_passes``
+    as in ``splash_attention`` (no reference counterpart)."""
     ops.check_shapes(Q, K, V)
     if not isinstance(dOut, torch.Tensor) or dOut.shape != Q.shape:
         raise ValueError(f"dOut shape {tuple(getattr(dOut, 'shape', ()))} must equal Q shape "
@@ -82,7 +84,9 @@ def backward(Q, K, V, Q_idx, K_idx, sm_scale: float, alpha: float, dOut, k_keep:
         sm_scale = 1.0 / math.sqrt(d)
     Q, K, V, qi, ki = ops.check_inputs(Q, K, V, Q_idx, K_idx)
     a = ops.clamp_alpha(alpha)
-    out, st = ops.splash_forward(Q, K, V, qi, ki, a, k_keep, sm_scale, block_m=block_m)
+    ops.check_bwd_passes(bwd_passes)
+    out, st = ops.splash_forward(Q, K, V, qi, ki, a, k_keep, sm_scale, block_m=block_m,
+                                 with_support=bwd_passes == "support")
     grads = ops.splash_backward(Q, K, V, qi, ki, out, dOut, st, a, k_keep, sm_scale, grad_mode)
     grads = [ops.from_kernel_layout(g, d, dtype) for g in grads]
     if fix_nonfinite:

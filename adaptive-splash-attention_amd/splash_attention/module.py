@@ -28,6 +28,10 @@ class AdaptiveSplashAttention(nn.Module):
         counterpart).
       block_m: query rows per mask block, 64 (default) or 32 (the
         reference's compile-time BLOCK_M; reference tau mode only).
+      bwd_passes: "support" (default: the backward over each row's
+        (row, key) pairs with nonzero weight) or "tiles" (over whole active
+        tiles on MFMA, faster when supports fill most of the active tiles);
+        no reference counterpart.
 
     forward(Q, K, V, Q_idx=None, K_idx=None): Q [B, H, NQ, d], K and V
     [B, H, NK, d]; Q_idx [B*H, NQ], K_idx [B*H, NK] positions (default
@@ -38,7 +42,8 @@ class AdaptiveSplashAttention(nn.Module):
 
     def __init__(self, head_dim: int = 64, alpha: float = 1.5, k_keep: int = 8,
                  adaptive_threshold: bool = True, sm_scale: float | None = None,
-                 grad_mode: str = "entmax", tau_mode: str = "reference", block_m: int = 64):
+                 grad_mode: str = "entmax", tau_mode: str = "reference", block_m: int = 64,
+                 bwd_passes: str = "support"):
         super().__init__()
         if not 1 <= int(head_dim) <= 128:
             raise ValueError(f"head_dim {head_dim} out of range [1, 128]")
@@ -52,6 +57,8 @@ class AdaptiveSplashAttention(nn.Module):
             raise ValueError("block_m must be 64 or 32")
         if block_m == 32 and tau_mode == "exact":
             raise ValueError("tau_mode 'exact' needs block_m = 64")
+        if bwd_passes not in ("support", "tiles"):
+            raise ValueError("bwd_passes must be 'support' or 'tiles'")
         self.head_dim = int(head_dim)
         self.alpha = float(alpha)
         self.k_keep = int(k_keep)
@@ -60,15 +67,17 @@ class AdaptiveSplashAttention(nn.Module):
         self.grad_mode = grad_mode
         self.tau_mode = tau_mode
         self.block_m = int(block_m)
+        self.bwd_passes = bwd_passes
 
     def extra_repr(self) -> str:
         return (f"head_dim={self.head_dim}, alpha={self.alpha}, k_keep={self.k_keep}, "
                 f"sm_scale={self.sm_scale}, grad_mode={self.grad_mode!r}, "
-                f"tau_mode={self.tau_mode!r}, block_m={self.block_m}")
+                f"tau_mode={self.tau_mode!r}, block_m={self.block_m}, "
+                f"bwd_passes={self.bwd_passes!r}")
 
     def forward(self, Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
                 Q_idx: torch.Tensor | None = None, K_idx: torch.Tensor | None = None) -> torch.Tensor:
         if Q.size(-1) != self.head_dim:
             raise ValueError(f"Q head dim {Q.size(-1)} != head_dim {self.head_dim}")
         return splash_attention(Q, K, V, Q_idx, K_idx, self.alpha, self.k_keep, self.sm_scale,
-                                self.grad_mode, self.tau_mode, self.block_m)
+                                self.grad_mode, self.tau_mode, self.block_m, self.bwd_passes)

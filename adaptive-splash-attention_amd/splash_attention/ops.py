@@ -33,6 +33,17 @@ GRAD_MODES = {"entmax": _lib.GRAD_ENTMAX, "reference": _lib.GRAD_REFERENCE}
 # "reference": the reference's top-k threshold; "exact": the alpha-entmax
 # threshold over the whole visible row (asa_tau_mode in adasplash.h)
 TAU_MODES = {"reference": _lib.TAU_REFERENCE, "exact": _lib.TAU_EXACT}
+# How the backward runs (the forward records the support masks only for
+# "support"):
+#   "support": over each row's (row, key) pairs with nonzero weight, from
+#              the support masks the forward records (512 bytes per active
+#              tile); VALU and gather work per pair, fastest when supports
+#              are small (headline: 0.33 ms against 0.83 ms)
+#   "tiles":   over whole active 64 x 64 tiles on MFMA, no masks; fastest
+#              when most entries of the active tiles are in the support
+#              (near-uniform rows: 1x4x4096x64, N(0,1)*0.1 inputs, k 8,
+#              block_m 32: 0.21 ms against 3.9 ms)
+BWD_PASSES = ("support", "tiles")
 
 
 @dataclass
@@ -97,10 +108,12 @@ class SplashState:
 
     @classmethod
     def from_tensors(cls, ts) -> "SplashState":
+        """A state from tensors() (an empty support-mask tensor, as the custom
+        operator returns without masks, reads as none)."""
         st = cls(*ts[:7])
         if len(ts) > 7:
             for n, t in zip(cls.SUPPORT, ts[7:]):
-                setattr(st, n, t)
+                setattr(st, n, t if t.numel() else None)
         return st
 
 
@@ -319,6 +332,12 @@ def check_tau_mode(tau_mode: str) -> int:
     if tau_mode not in TAU_MODES:
         raise ValueError(f"tau_mode must be one of {sorted(TAU_MODES)}")
     return TAU_MODES[tau_mode]
+
+
+def check_bwd_passes(bwd_passes: str) -> str:
+    if bwd_passes not in BWD_PASSES:
+        raise ValueError(f"bwd_passes must be one of {BWD_PASSES}, got {bwd_passes!r}")
+    return bwd_passes
 
 
 def check_block_m(block_m) -> int:

@@ -158,6 +158,16 @@ def test_operand_strides_for_the_c_abi():
             ops._set_strides(prob, k=bad)
 
 
+def test_bwd_passes_option_is_checked():
+    with pytest.raises(ValueError, match="bwd_passes"):
+        sa.AdaptiveSplashAttention(bwd_passes="dense")
+    with pytest.raises(ValueError, match="bwd_passes"):
+        ops.check_bwd_passes("pairs")
+    m = sa.AdaptiveSplashAttention(bwd_passes="tiles")
+    assert m.bwd_passes == "tiles" and "bwd_passes='tiles'" in m.extra_repr()
+    assert ops.check_bwd_passes("support") == "support"
+
+
 def test_reference_order_defaults_are_the_compiled_references():
     """forward/backward default to the compiled reference's K_KEEP = 8 and
     BLOCK_M = 32 (adasplashattention.cu:8-9, :17-19) and apply its host

@@ -20,19 +20,23 @@ def test_opcheck_forward(dev, d, dtype):
                           test_utils=("test_schema", "test_faketensor"))
     torch.library.opcheck(library.forward_op, args + ("exact",),
                           test_utils=("test_schema", "test_faketensor"))
+    torch.library.opcheck(library.forward_op, args + ("reference", 64, "tiles"),
+                          test_utils=("test_schema", "test_faketensor"))
 
 
-@pytest.mark.parametrize("dtype,d,tau_mode", [(torch.float32, 64, "reference"),
-                                              (torch.bfloat16, 64, "reference"),
-                                              (torch.float16, 40, "reference"),
-                                              (torch.float32, 64, "exact")])
-def test_compile_matches_eager(dev, dtype, d, tau_mode):
-    print(f"[lib] torch.compile aot_eager {dtype} d={d} tau_mode={tau_mode}", flush=True)
+@pytest.mark.parametrize("dtype,d,tau_mode,bwd_passes", [(torch.float32, 64, "reference", "support"),
+                                                         (torch.bfloat16, 64, "reference", "support"),
+                                                         (torch.float16, 40, "reference", "support"),
+                                                         (torch.float32, 64, "exact", "support"),
+                                                         (torch.bfloat16, 64, "reference", "tiles")])
+def test_compile_matches_eager(dev, dtype, d, tau_mode, bwd_passes):
+    print(f"[lib] torch.compile aot_eager {dtype} d={d} tau_mode={tau_mode} {bwd_passes}",
+          flush=True)
     B, H, N = 1, 2, 192
     Q, K, V, dO = make_inputs(B, H, N, N, d, seed=12, dtype=dtype)
     idx = causal_idx(B * H, N).to(dev)
     attn = sa.AdaptiveSplashAttention(head_dim=d, alpha=1.5, k_keep=16, sm_scale=0.125,
-                                      tau_mode=tau_mode)
+                                      tau_mode=tau_mode, bwd_passes=bwd_passes)
 
     def run(fn):
         q, k, v = (t.to(dev).requires_grad_(True) for t in (Q, K, V))
@@ -122,3 +126,35 @@ def test_benchmark_cli_rocprof_pmc(dev, tmp_path):
     # one 128-row block per (batch, head): 4 waves per select launch
     assert s["select_kernel"]["SQ_WAVES"] >= 4, s
     assert "forward_kernel" in s
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_bwd_passes_agree(dev, dtype, tol):
+    """bwd_passes "tiles" (whole active tiles on MFMA, no support masks
+    recorded) and "support" (the support-pair passes) give the same
+    gradients to the dtype's tolerance, through the module, the custom
+    operator and the reference-order backward; the operator returns an
+    empty support-mask tensor for "tiles"."""
+    print(f"[lib] bwd_passes agree {dtype}", flush=True)
+    B, H, N, d = 1, 2, 320, 64
+    Q, K, V, dO = make_inputs(B, H, N, N, d, seed=13, dtype=dtype, scale=0.3)
+    idx = causal_idx(B * H, N).to(dev)
+    got = {}
+    for passes in ("support", "tiles"):
+        attn = sa.AdaptiveSplashAttention(head_dim=d, alpha=1.5, k_keep=16, bwd_passes=passes)
+        q, k, v = (t.to(dev).requires_grad_(True) for t in (Q, K, V))
+        out = attn(q, k, v, idx, idx)
+        out.backward(dO.to(dev))
+        ref_order = sa.backward(Q.to(dev), K.to(dev), V.to(dev), idx, idx, d ** -0.5, 1.5,
+                                dO.to(dev), k_keep=16, grad_mode="entmax", block_m=64,
+                                bwd_passes=passes)
+        torch.cuda.synchronize()
+        got[passes] = [x.detach().float().cpu() for x in (out, q.grad, k.grad, v.grad)]
+        for a, b in zip(ref_order, got[passes][1:]):
+            assert torch.equal(a.float().cpu(), b)
+        sup = library.forward_op(Q.to(dev), K.to(dev), V.to(dev), idx, idx, 1.5, 16, d ** -0.5,
+                                 "entmax", "reference", 64, passes)[-1]
+        assert (sup.numel() > 0) == (passes == "support")
+    for name, a, b in zip(("out", "dQ", "dK", "dV"), got["tiles"], got["support"]):
+        err = (a - b).abs().max().item() / max(b.abs().max().item(), 1e-30)
+        assert err <= tol, f"{name}: tiles against support {err:.2e} > {tol}"
