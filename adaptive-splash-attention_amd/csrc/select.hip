@@ -1096,12 +1096,12 @@ __global__ __launch_bounds__(kThreads) void tau_kernel(SelectParams p) {
   tau_row<AC, KMAX>(p, blockIdx.x);
 }
 
-// tau_kernel's blocks, then compact_kernel's (both read only what the
+// compact_kernel's blocks, then tau_kernel's (both read only what the
 // score pass wrote): one launch, the compaction running beside the tau
-// rows instead of after them.
+// rows instead of after them.  The compaction's blocks come first: each
+// runs longer than a block of tau rows, and on large masks they are many
+// (compact_grid).
 template <int AC, int KMAX>
-// The compaction's blocks come first: each runs longer than a block of tau
-// rows, and on large masks they are many (compact_grid).
 __global__ __launch_bounds__(kThreads) void tau_compact_kernel(SelectParams p, CompactParams cp, int ncomp) {
   if (int(blockIdx.x) < ncomp) {  // block-uniform
     extern __shared__ int sm[];
