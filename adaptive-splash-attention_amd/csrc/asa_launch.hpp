@@ -123,6 +123,11 @@ struct ForwardParams {
   const float* top1;    // each row's best score (the score pass's first sorted value)
   // Support masks (optional: sup.mask == nullptr writes none).
   SupportMasks sup;
+  // Two query blocks per workgroup (16-bit inputs): 0 when the pairs fill
+  // at least one wave of resident workgroups on `cus` compute units, 1
+  // wherever the paired kernel applies, 2 never (asa_set_pairing).
+  int pairing;
+  int cus;
 };
 
 // Per-row constants of the support-mask backward, written by its dQ pass

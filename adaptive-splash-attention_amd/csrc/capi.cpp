@@ -263,6 +263,27 @@ int check_state(const asa_state* st, bool need_norms) {
   return ASA_OK;
 }
 
+// asa_set_pairing's mode (process-wide).
+std::atomic<int> g_pairing{ASA_PAIRING_AUTO};
+
+// Compute units of the current device, cached per device ordinal.
+int device_cus(int* cus) {
+  static std::atomic<int> cached[64] = {};
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev >= 0 && dev < 64 && cached[dev].load() > 0) {
+    *cus = cached[dev].load();
+    return ASA_OK;
+  }
+  int n = 0;
+  if (int rc = check_hip(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev),
+                         "hipDeviceGetAttribute"))
+    return rc;
+  if (dev >= 0 && dev < 64) cached[dev].store(n);
+  *cus = n;
+  return ASA_OK;
+}
+
 // Candidate capacity per row of the select kernel on the current device
 // (*cap), or an error when even the smallest capacity does not fit its LDS.
 int select_cap(const Shape& s, bool from_scores, int* cap) {
@@ -458,6 +479,8 @@ int forward_impl(const Shape& sh, const void* q, const void* k, const void* v,
   fp.norms = st->norms;
   fp.kbounds = reinterpret_cast<const int2*>(static_cast<const char*>(workspace) + tkv_bytes(sh));
   fp.sup.mask = st->sup_mask;
+  fp.pairing = g_pairing.load();
+  if (int rc = device_cus(&fp.cus)) return rc;
   asa::profile_begin("forward", s);
   hipError_t e = asa::launch_forward(fp, sh.dtype, s);
   asa::profile_end(s);
@@ -642,6 +665,13 @@ int asa_select_from_scores(const asa_problem* p, const float* scores, const int3
   const Csr64 c64 = kernel_csr(sh, st, workspace, fwd_csr_offset(sh));
   if (int rc = run_select(sh, nullptr, nullptr, scores, q_idx, k_idx, st, c64, workspace, s))
     return rc;
+  return ok();
+}
+
+int asa_set_pairing(int mode) {
+  if (mode != ASA_PAIRING_AUTO && mode != ASA_PAIRING_ALWAYS && mode != ASA_PAIRING_NEVER)
+    return fail(ASA_ERR_INVALID_ARGUMENT, "unknown pairing mode %d", mode);
+  g_pairing.store(mode);
   return ok();
 }
 

@@ -426,10 +426,22 @@ inline bool pair_fold_ok(const ForwardParams& p) {
   return alpha_class_of(p.d.alpha) != kAGen && c >= 0x1p-8f && c <= 0x1p8f;
 }
 
+// The paired kernel pays where its workgroups fill the GPU: it runs half as
+// many as the one-block kernel, and with fewer pairs than one wave of
+// resident ones (three per compute unit at d = 64, two at 128) the
+// one-block kernel's twice as many workgroups finish first (measured,
+// bf16 fwd: 2x8x4096x64, 512 pairs: 107 against 87 us; 1x1x32768x64: 620
+// against 352 us; 1024 pairs: 112 against 134 us).
+inline bool pair_pays(const ForwardParams& p) {
+  if (p.pairing != 0) return p.pairing == 1;
+  const size_t pairs = size_t((p.d.nQB + 1) / 2) * size_t(p.d.BH);
+  return pairs >= size_t(p.cus > 0 ? p.cus : 1) * (p.d.D == 64 ? 3 : 2);
+}
+
 template <typename T, int D, bool EMIT, bool HALF>
 hipError_t launch_tde(const ForwardParams& p, hipStream_t s) {
   if constexpr (is_half<T>)
-    if (pair_fold_ok(p)) return launch_pair<T, D, EMIT, HALF>(p, s);
+    if (pair_fold_ok(p) && pair_pays(p)) return launch_pair<T, D, EMIT, HALF>(p, s);
   dim3 grid(p.d.nQB * p.d.BH);
   switch (alpha_class_of(p.d.alpha)) {
     case kA15: hipLaunchKernelGGL((forward_kernel<T, D, kE2, EMIT, HALF>), grid, dim3(kThreads), 0, s, p); break;

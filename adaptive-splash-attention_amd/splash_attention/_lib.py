@@ -12,7 +12,7 @@ import threading
 
 from . import _build
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 ASA_OK = 0
 ASA_ERR_INVALID_ARGUMENT = 1
@@ -44,6 +44,7 @@ EXPORTS = (
     "asa_forward_noalloc",
     "asa_backward",
     "asa_select_from_scores",
+    "asa_set_pairing",
     "asa_profile_enable",
     "asa_profile_read",
 )
@@ -147,6 +148,8 @@ def load() -> ctypes.CDLL:
         lib.asa_select_from_scores.restype = ctypes.c_int
         lib.asa_select_from_scores.argtypes = [ctypes.POINTER(Problem), _V, _V, _V,
                                                ctypes.POINTER(State), _V, _V]
+        lib.asa_set_pairing.restype = ctypes.c_int
+        lib.asa_set_pairing.argtypes = [ctypes.c_int]
         lib.asa_profile_enable.restype = ctypes.c_int
         lib.asa_profile_enable.argtypes = [ctypes.c_int]
         lib.asa_profile_read.restype = ctypes.c_int
@@ -167,6 +170,18 @@ def query_sizes(p: Problem) -> Sizes:
     z = Sizes()
     check(load().asa_query_sizes(ctypes.byref(p), ctypes.byref(z)))
     return z
+
+
+PAIRING = {"auto": 0, "always": 1, "never": 2}  # asa_pairing
+
+
+def set_pairing(mode: str) -> None:
+    """Forward kernel for 16-bit inputs (asa_set_pairing, process-wide):
+    "auto" (default) pairs query blocks when the pairs fill the GPU,
+    "always" wherever the paired kernel applies, "never" not at all."""
+    if mode not in PAIRING:
+        raise ValueError(f"pairing must be one of {sorted(PAIRING)}, got {mode!r}")
+    check(load().asa_set_pairing(PAIRING[mode]))
 
 
 def profile_enable(on: bool) -> None:

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define ASA_ABI_VERSION 7
+#define ASA_ABI_VERSION 8
 
 typedef enum asa_status {
   ASA_OK = 0,
@@ -262,6 +262,21 @@ int asa_select_from_scores(const asa_problem *p, const float *scores, const int3
  * them and reports, per kernel name, the number of launches and the summed
  * duration in milliseconds, then clears the record.  Call it when no other
  * thread is launching.  Returns the number of distinct kernels (<= max).  */
+/* Which forward kernel runs for 16-bit inputs (no reference counterpart;
+ * for tuning and tests): ASA_PAIRING_AUTO (default) runs two query blocks
+ * per workgroup when those workgroups fill at least one wave of the GPU
+ * (three per compute unit at head_dim <= 64, two above) and one block per
+ * workgroup otherwise; ASA_PAIRING_ALWAYS pairs wherever the paired
+ * kernel applies; ASA_PAIRING_NEVER never pairs.  The two kernels give
+ * the same results to the last ulps.  Process-wide; read by each
+ * asa_forward / asa_forward_noalloc call. */
+typedef enum asa_pairing {
+  ASA_PAIRING_AUTO = 0,
+  ASA_PAIRING_ALWAYS = 1,
+  ASA_PAIRING_NEVER = 2
+} asa_pairing;
+int asa_set_pairing(int mode);
+
 int asa_profile_enable(int on);
 int asa_profile_read(int max, char (*names)[64], int *counts, double *total_ms);
 

@@ -21,3 +21,13 @@ def dev():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def pairing():
+    """Set the forward's pairing mode for one test (asa_set_pairing: which
+    forward kernel runs for 16-bit inputs), restoring the default after it."""
+    from splash_attention import _lib
+
+    yield _lib.set_pairing
+    _lib.set_pairing("auto")

@@ -76,11 +76,20 @@ CASES = [
 ]
 
 
+# Each case with the paired forward wherever it applies ("always": on
+# these small shapes the default runs one query block per workgroup, as it
+# does on any problem whose pairs would not fill the GPU), and the 16-bit
+# cases also with the default choice ("auto").
+PCASES = [c + ("always",) for c in CASES] + [c + ("auto",) for c in CASES if c[-1] != torch.float32]
+
+
 @pytest.mark.parametrize("mode", ["entmax", "reference"])
-@pytest.mark.parametrize("name,B,H,NQ,NK,d,alpha,k,scale,dtype", CASES, ids=[c[0] for c in CASES])
-def test_attention_parity(dev, name, B, H, NQ, NK, d, alpha, k, scale, dtype, mode):
-    print(f"[attn] {name} mode={mode} B={B} H={H} NQ={NQ} NK={NK} d={d} a={alpha} k={k} {dtype}",
-          flush=True)
+@pytest.mark.parametrize("name,B,H,NQ,NK,d,alpha,k,scale,dtype,pmode", PCASES,
+                         ids=[f"{c[0]}-{c[-1]}" for c in PCASES])
+def test_attention_parity(dev, pairing, name, B, H, NQ, NK, d, alpha, k, scale, dtype, pmode, mode):
+    print(f"[attn] {name} mode={mode} pairing={pmode} B={B} H={H} NQ={NQ} NK={NK} d={d} "
+          f"a={alpha} k={k} {dtype}", flush=True)
+    pairing(pmode)
     Q, K, V, dO = make_inputs(B, H, NQ, NK, d, seed=0, dtype=dtype)
     BH = B * H
     qidx = causal_idx(BH, NQ) + (NK - NQ if NK > NQ else 0)
@@ -92,3 +101,24 @@ def test_attention_parity(dev, name, B, H, NQ, NK, d, alpha, k, scale, dtype, mo
     assert_tau_close(st.taus.cpu().numpy(), own.taus, alpha)
     np.testing.assert_array_equal(st.mask.cpu().numpy(), own.mask, err_msg=f"{name}: mask")
     _check(f"{name}/{mode}", dtype, out, st, grads, fw, og, check_state=False)
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 64), (torch.float16, 128)])
+def test_pairing_modes_agree(dev, pairing, dtype, d):
+    """The paired and the one-block forward kernels give the same output to
+    the last ulps (the paired one folds the clip into its products); on a
+    shape with few query-block pairs the default runs the one-block kernel,
+    bit for bit."""
+    print(f"[attn] pairing modes {dtype} d={d}", flush=True)
+    B, H, N = 1, 2, 300
+    Q, K, V, dO = make_inputs(B, H, N, N, d, seed=5, dtype=dtype)
+    idx = causal_idx(B * H, N)
+    res = {}
+    for pm in ("always", "never", "auto"):
+        pairing(pm)
+        out, st, grads = _gpu(dev, Q, K, V, dO, idx, idx, 1.5, 16, d ** -0.5, "entmax")
+        res[pm] = [np32(x) for x in (out, *grads)]
+    for a, b in zip(res["auto"], res["never"]):
+        np.testing.assert_array_equal(a, b)
+    for n, a, b in zip(("out", "dQ", "dK", "dV"), res["always"], res["never"]):
+        assert_close(f"{n}: paired against one-block", a, b, TOL[dtype])

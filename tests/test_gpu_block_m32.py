@@ -132,11 +132,12 @@ TOL16 = {torch.bfloat16: 2e-2, torch.float16: 4e-3}
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("mode", ["entmax", "reference"])
-def test_attention_block_m32_16bit_magnets(dev, mode, dtype, d):
-    """16-bit inputs: at d = 64 the paired forward (bf16, and fp16 with its
-    P scaling), at d = 128 the one-block forward; with 32-row masks a
-    wave's half drops the union tiles its mask row lacks (its clip bounds
-    set to -0 there).  The magnets make every pair of halves differ."""
+def test_attention_block_m32_16bit_magnets(dev, pairing, mode, dtype, d):
+    """16-bit inputs through the paired forward (bf16, and fp16 with its P
+    scaling, at d = 64 and 128); with 32-row masks a wave's half drops the
+    union tiles its mask row lacks (its clip bounds set to -0 there).  The
+    magnets make every pair of halves differ."""
+    pairing("always")  # the paired forward's 32-row gating, as on large problems
     print(f"[bm32] attention magnets {dtype} d={d} {mode}", flush=True)
     Q, K, V, dO, qi, ki = _magnets(2, 256, d)
     Q, K, V = (t.to(dtype) for t in (Q, K, V))
