@@ -57,8 +57,8 @@ COPY_BYTES = 256 << 20   # --copy-calibration copy size
 # library built from the sources whose hash is HBM_TRAFFIC_SOURCES
 # (source_hash()).  A line from a library built from other sources reports
 # traffic null and says why: counters of another build are not evidence.
-HBM_TRAFFIC_SOURCES = "37d9703f77144a7d"
-HBM_TRAFFIC = {'bounds': 1109588, 'select': 138689444, 'tau': 34745517, 'tau_compact': 37473416, 'refine': 109806461, 'compact': 2744261, 'forward': 329855928, 'bwd_dq_sparse': 240750589, 'bwd_dkdv_sparse': 287664734}
+HBM_TRAFFIC_SOURCES = "2d00522ce6db3e3c"
+HBM_TRAFFIC = {'bounds': 1109233, 'select': 138861915, 'tau': 34745917, 'tau_compact': 37510848, 'refine': 109582540, 'compact': 2762350, 'forward': 329894294, 'bwd_dq_sparse': 240749933, 'bwd_dkdv_sparse': 287676950}
 
 
 def source_hash() -> str:
