@@ -158,3 +158,18 @@ def test_bwd_passes_agree(dev, dtype, tol):
     for name, a, b in zip(("out", "dQ", "dK", "dV"), got["tiles"], got["support"]):
         err = (a - b).abs().max().item() / max(b.abs().max().item(), 1e-30)
         assert err <= tol, f"{name}: tiles against support {err:.2e} > {tol}"
+
+
+def test_benchmark_cli_tile_backward(dev):
+    """--bwd-passes tiles: the timed backward runs the dense tile passes
+    (bwd_dq, bwd_dkdv), and the forward records no support masks."""
+    from splash_attention import benchmark
+
+    print("[lib] benchmark cli tile backward", flush=True)
+    r = benchmark.run_config(1, 2, 128, 64, 1.5, 8, torch.float32, "entmax", True,
+                             input_scale=0.1, warmup=1, trials=2, kernel_times=True,
+                             bwd_passes="tiles")
+    ks = r["kernel_us"]
+    assert r["bwd_passes"] == "tiles"
+    assert ks["bwd_dq"] > 0 and ks["bwd_dkdv"] > 0, ks
+    assert "bwd_dq_sparse" not in ks and "bwd_dkdv_sparse" not in ks, ks

@@ -54,6 +54,10 @@ def test_benchmark_cli_parsing():
     assert args.config == [(2, 2, 256, 64)] and args.baseline == "vanilla" and args.backward
     assert args.tau_mode == "reference"
     assert benchmark.build_parser().parse_args(["--tau-mode", "exact"]).tau_mode == "exact"
+    assert args.bwd_passes == "support"
+    assert benchmark.build_parser().parse_args(["--bwd-passes", "tiles"]).bwd_passes == "tiles"
+    with pytest.raises(SystemExit):
+        benchmark.build_parser().parse_args(["--bwd-passes", "dense"])
 
 
 def test_benchmark_cli_rocprof_command_and_summary(tmp_path):
