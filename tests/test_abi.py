@@ -45,7 +45,8 @@ def _header_fields(struct):
 
 
 def _integration_fields(cls):
-    """Field names of the ctypes class `cls` in INTEGRATION.md's binding example."""
+    """Field names of the ctypes class `cls` in the integration guide's
+    binding example (the guide at the repository root)."""
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     block = re.search(r"class %s\(ctypes\.Structure\):\s*_fields_ = (.*?\])\n\n" % cls, text, re.S)
     return re.findall(r'"(\w+)"', block.group(1))
@@ -53,7 +54,7 @@ def _integration_fields(cls):
 
 def test_struct_layouts_agree_header_binding_and_docs():
     """asa_problem, asa_state and asa_sizes: the header, the package's ctypes
-    binding and INTEGRATION.md's example list the same fields in the same
+    binding and the integration guide's example list the same fields in the same
     order (a caller whose struct lacks a trailing field, such as the state's
     status word, hands the library memory past its struct)."""
     from splash_attention import _lib
