@@ -6,7 +6,9 @@ Every draw picks the dtype (fp32, bf16, fp16), batch and heads, NQ and NK
 number of 16-byte chunks), alpha (1.25, 1.5, 2, 2.5 or one in (1.05, 2.9)),
 k, 64- or 32-row mask blocks, the positions (causal, causal with an
 offset, non-causal, or random positions, so that some rows see no key),
-the gradient mode and the backward passes (support pairs or tiles).
+the gradient mode and the backward passes (support pairs or tiles).  A
+second set of draws runs tau_mode="exact" against dense alpha-entmax
+attention in float64.
 
 Q and K lie on a 1/16 grid in [-4, 4] and sm_scale is a power of two, so
 every score is exact in fp32 on the GPU and in the oracle.  Without that
@@ -120,3 +122,73 @@ def test_randomized_parity(dev, i):
         assert e <= TOL[dt], f"{name}: relative error {e:.3e} > {TOL[dt]:.0e}"
         errs.append(e)
     print("  errs " + " ".join(f"{e:.2e}" for e in errs), flush=True)
+
+
+def _draw_exact(rng):
+    c = _draw(rng)
+    c["dt"] = rng.choice([torch.float32, torch.bfloat16])
+    if c["dt"] == torch.float32 and c["d"] % 4:
+        c["d"] = 64
+    c["alpha"] = rng.choice([1.25, 1.5, 2.0, round(rng.uniform(1.05, 2.0), 3)])
+    return c
+
+
+_rng_exact = random.Random(20261203)
+EXACT_CASES = [_draw_exact(_rng_exact) for _ in range(24)]
+
+
+@pytest.mark.parametrize("i", range(len(EXACT_CASES)))
+def test_randomized_exact_mode(dev, i):
+    """tau_mode="exact" on drawn problems against dense alpha-entmax
+    attention in float64 (oracle/dense.py) and its exact Jacobian
+    gradients (entmax mode).  alpha <= 2: above 2 the Jacobian weight
+    P^(2-alpha) is unbounded at the support's edge (the exact-mode tests
+    give such gradients 1e-4).  Tolerances as above, relative to each
+    tensor's natural scale; tau to 1e-5 (fp32) or 2e-2 (bf16) on rows that
+    see a key; fp32 masks hold every block with a support key (p > 1e-7)."""
+    from oracle import dense
+
+    c = EXACT_CASES[i]
+    dt, B, H, NQ, NK, d = c["dt"], c["B"], c["H"], c["NQ"], c["NK"], c["d"]
+    alpha, k, scale = c["alpha"], c["k"], c["scale"]
+    print(f"[random] exact case {i}: {str(dt)[6:]} B{B} H{H} NQ{NQ} NK{NK} d{d} alpha {alpha} "
+          f"k {k} {c['kind']} seed {c['seed']}", flush=True)
+    g = torch.Generator().manual_seed(c["seed"])
+    Q, K = ((torch.round(torch.randn(B, H, n, d, generator=g) * 16) / 16).clamp(-4, 4)
+            for n in (NQ, NK))
+    V = torch.randn(B, H, NK, d, generator=g)
+    dO = torch.randn(B, H, NQ, d, generator=g)
+    Q, K, V, dO = (t.to(dt) for t in (Q, K, V, dO))
+    qi, ki = _positions(c, g)
+
+    q, kk, v, qi_, ki_ = sa.ops.check_inputs(*(t.to(dev) for t in (Q, K, V, qi, ki)))
+    out, st = sa.ops.splash_forward(q, kk, v, qi_, ki_, alpha, k, scale, tau_mode="exact")
+    grads = sa.ops.splash_backward(q, kk, v, qi_, ki_, out, dO.to(dev), st, alpha, k, scale,
+                                   "entmax")
+    torch.cuda.synchronize()
+
+    vis = ki.numpy()[:, None, :] <= qi.numpy()[:, :, None]
+    ref_out, P, taus = dense.attention_forward(np32(Q), np32(K), np32(V), vis, alpha, scale)
+    dq, dk, dv = dense.attention_backward(np32(Q), np32(K), np32(V), P, np32(dO), alpha, scale)
+    seen = vis.any(-1)
+    gt = st.taus.cpu().numpy().reshape(taus.shape)
+    dtau = float(np.abs(gt - taus)[seen].max()) if seen.any() else 0.0
+    assert dtau <= (1e-5 if dt == torch.float32 else 2e-2), f"tau differs by {dtau:.2e}"
+    if dt == torch.float32:
+        nqb, nkb = -(-NQ // 64), -(-NK // 64)
+        sup = np.zeros((B * H, nqb * 64, nkb * 64), bool)
+        sup[:, :NQ, :NK] = (P > 1e-7) & vis
+        need = sup.reshape(B * H, nqb, 64, nkb, 64).any(axis=(2, 4))
+        assert not (need & ~st.mask.cpu().numpy().astype(bool)).any(), "support block missing"
+
+    def mx(t):
+        return float(np.abs(np32(t)).max()) if t.numel() else 0.0
+
+    floors = {"out": mx(V), "dQ": scale * mx(K) * mx(dO) * mx(V),
+              "dK": scale * mx(Q) * mx(dO) * mx(V), "dV": mx(dO)}
+    for name, got, want in (("out", out, ref_out), ("dQ", grads[0], dq), ("dK", grads[1], dk),
+                            ("dV", grads[2], dv)):
+        gg = np32(got)[..., :d]  # the ops-level calls return a head dimension padded to a chunk
+        assert np.all(np.isfinite(gg)), f"{name} not finite"
+        e = rel_err(gg, np.asarray(want).reshape(gg.shape), max(floors[name], 1e-30))
+        assert e <= TOL[dt], f"{name}: relative error {e:.3e} > {TOL[dt]:.0e}"
