@@ -8,7 +8,9 @@ k, 64- or 32-row mask blocks, the positions (causal, causal with an
 offset, non-causal, or random positions, so that some rows see no key),
 the gradient mode and the backward passes (support pairs or tiles).  A
 second set of draws runs tau_mode="exact" against dense alpha-entmax
-attention in float64.
+attention in float64, and a third reads the operands in place from random
+layouts (transposed views, row slices, broadcast heads or batch), which
+must give the same bits as contiguous copies.
 
 Q and K lie on a 1/16 grid in [-4, 4] and sm_scale is a power of two, so
 every score is exact in fp32 on the GPU and in the oracle.  Without that
@@ -192,3 +194,63 @@ def test_randomized_exact_mode(dev, i):
         assert np.all(np.isfinite(gg)), f"{name} not finite"
         e = rel_err(gg, np.asarray(want).reshape(gg.shape), max(floors[name], 1e-30))
         assert e <= TOL[dt], f"{name}: relative error {e:.3e} > {TOL[dt]:.0e}"
+
+
+def _draw_layout(rng):
+    c = _draw(rng)
+    c["NK"] = c["NQ"] if c["kind"] == "causal" else c["NK"]
+    c["kind"] = "offset" if c["kind"] == "random" else c["kind"]
+    c["lay"] = (rng.choice("ctw"), rng.choice("ctwhb"), rng.choice("ctwhb"), rng.choice("ctw"))
+    return c
+
+
+_rng_layout = random.Random(20261204)
+LAYOUT_CASES = [_draw_layout(_rng_layout) for _ in range(24)]
+
+
+def _view(leaf, lay, B, H, strided):
+    """The operand the call sees: leaf itself ('c'), a [B, N, H, d] buffer
+    viewed as [B, H, N, d] ('t'), a row slice of a wider buffer ('w'), or a
+    [B, 1, N, d] / [1, H, N, d] leaf broadcast over heads ('h') or batch
+    ('b'); strided=False gives the same values contiguous."""
+    if lay in "hb":
+        v = leaf.expand(B, H, *leaf.shape[2:])
+        return v if strided else v.contiguous()
+    if not strided or lay == "c":
+        return leaf
+    if lay == "t":
+        return leaf.transpose(1, 2).contiguous().transpose(1, 2)
+    pad = 16 // leaf.element_size()
+    buf = torch.zeros(*leaf.shape[:3], leaf.shape[3] + pad, dtype=leaf.dtype, device=leaf.device)
+    return buf.index_copy(3, torch.arange(leaf.shape[3], device=leaf.device), leaf)[..., :leaf.shape[3]]
+
+
+@pytest.mark.parametrize("i", range(len(LAYOUT_CASES)))
+def test_randomized_layouts_bit_identical(dev, i):
+    """Operands read in place (transposed views, row slices of wider
+    buffers, K or V shared across heads or the batch with stride 0, dOut
+    strided) give, through the autograd function, the same bits as the
+    same values passed contiguous: out and the leaves' gradients."""
+    c = LAYOUT_CASES[i]
+    dt, B, H, NQ, NK, d = c["dt"], c["B"], c["H"], c["NQ"], c["NK"], c["d"]
+    print(f"[random] layout case {i}: {str(dt)[6:]} B{B} H{H} NQ{NQ} NK{NK} d{d} "
+          f"layouts {''.join(c['lay'])} {c['mode']} {c['bwd']} block_m {c['bm']}", flush=True)
+    g = torch.Generator().manual_seed(c["seed"])
+    shapes = [(B, H, NQ, d), (B, H, NK, d), (B, H, NK, d), (B, H, NQ, d)]
+    base = []
+    for (b_, h_, n_, d_), lay in zip(shapes, c["lay"]):
+        shp = (b_, 1, n_, d_) if lay == "h" else (1, h_, n_, d_) if lay == "b" else (b_, h_, n_, d_)
+        base.append(torch.randn(*shp, generator=g).to(dt).to(dev))
+    qi, ki = (t.to(dev) for t in _positions(c, g))
+    res = []
+    for strided in (True, False):
+        leaves = [t.detach().clone().requires_grad_() for t in base[:3]]
+        ops_ = [_view(lf, lay, B, H, strided) for lf, lay in zip(leaves, c["lay"][:3])]
+        dov = _view(base[3], c["lay"][3], B, H, strided)
+        out = sa.splash_attention(*ops_, qi, ki, c["alpha"], c["k"], c["scale"], c["mode"],
+                                  block_m=c["bm"], bwd_passes=c["bwd"])
+        out.backward(dov)
+        res.append([out.detach()] + [lf.grad for lf in leaves])
+    torch.cuda.synchronize()
+    for name, a, b in zip(("out", "dQ", "dK", "dV"), res[0], res[1]):
+        assert torch.equal(a, b), f"{name} differs from the contiguous call"
