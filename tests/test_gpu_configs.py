@@ -252,3 +252,25 @@ def test_dq_balanced_and_chunked_paths(dev, mode):
     assert_close("dq paths out", np32(out), fw.out, 1e-5)
     for nm, g, w in zip(("dQ", "dK", "dV"), grads, og):
         assert_close(f"dq paths {nm}", np32(g), w, 1e-5)
+
+
+@pytest.mark.parametrize("tau_mode", ["reference", "exact"])
+def test_headline_step_is_deterministic(dev, tau_mode):
+    """The headline step (B4 H16 N4096 d64 bf16, alpha 1.5, k 32), twice on
+    the same inputs: out, tau, the mask and all three gradients equal bit
+    for bit.  At this size thousands of workgroups run at once, so the
+    order-dependent steps (candidate appends by LDS atomics in the score
+    pass, the compaction's counts, the support-pair lists) are exercised
+    under real concurrency; every sum they feed is formed in a fixed order."""
+    print(f"[cfg] headline determinism {tau_mode}", flush=True)
+    B, H, N, d = 4, 16, 4096, 64
+    Q, K, V, dO = (_gauss((B, H, N, d), s, torch.bfloat16).to(dev) for s in (11, 12, 13, 14))
+    idx = causal_idx(B * H, N).to(dev)
+    res = []
+    for _ in range(2):
+        out, st = sa.ops.splash_forward(Q, K, V, idx, idx, 1.5, 32, 0.125, tau_mode=tau_mode)
+        grads = sa.ops.splash_backward(Q, K, V, idx, idx, out, dO, st, 1.5, 32, 0.125, "entmax")
+        torch.cuda.synchronize()
+        res.append([out, st.taus, st.mask, *grads])
+    for name, a, b in zip(("out", "tau", "mask", "dQ", "dK", "dV"), *res):
+        assert torch.equal(a, b), f"{name} differs between two identical steps"
