@@ -1,6 +1,8 @@
 """asa_forward_noalloc (the forward whose workspace is the library's own
 device array) against asa_forward, through the C ABI: two calls in a row,
-the second on a smaller problem, every output and state buffer bit for bit.
+the second on a smaller problem, and a sequence of sixteen drawn problems,
+every output and state buffer bit for bit; its size rejection; and the call
+captured in a HIP graph.
 No reference counterpart (the reference allocates inside the extension)."""
 import pytest
 import torch
@@ -107,3 +109,65 @@ def test_noalloc_forward_replays_in_a_hip_graph(dev):
             n = int(want.q_ptr[bh, -1])
             assert torch.equal(gst.sup_mask[bh, :n], want.sup_mask[bh, :n]), f"sup_mask {bh}"
     del graph
+
+
+def test_noalloc_random_sequence_matches_forward(dev):
+    """Sixteen drawn problems in a row through asa_forward_noalloc, each
+    against asa_forward bit for bit (out and every state buffer): dtypes,
+    ragged NQ != NK, head dimensions, k, 64- or 32-row mask blocks, both tau
+    modes, causal, non-causal or random positions.  The library's array keeps
+    the previous call's bytes, of another size and layout, every time."""
+    import random
+
+    from splash_attention import ops
+
+    rng = random.Random(7)
+    for i in range(16):
+        dt = rng.choice([torch.float32, torch.bfloat16, torch.float16])
+        step = 4 if dt == torch.float32 else 8
+        B, H = rng.choice([1, 2]), rng.choice([1, 2, 3])
+        NQ, NK = rng.choice([1, 65, 300, 777, 1024]), rng.choice([1, 64, 200, 640, 1100])
+        d = rng.choice([64, 128, rng.randrange(step, 129, step)])
+        k, bm = rng.choice([2, 8, 32, 64]), rng.choice([64, 32])
+        tau_mode = "exact" if bm == 64 and rng.random() < 0.4 else "reference"
+        kind = rng.choice(["causal", "noncausal", "random"])
+        seed = rng.randrange(10 ** 6)
+        print(f"[noalloc] draw {i}: {str(dt)[6:]} B{B} H{H} NQ{NQ} NK{NK} d{d} k{k} "
+              f"block_m {bm} {tau_mode} {kind}", flush=True)
+        g = torch.Generator().manual_seed(seed)
+        Q = torch.randn(B, H, NQ, d, generator=g).to(dt).to(dev)
+        K = torch.randn(B, H, NK, d, generator=g).to(dt).to(dev)
+        V = torch.randn(B, H, NK, d, generator=g).to(dt).to(dev)
+        if kind == "random":
+            qi = torch.randint(0, NK + 3, (B * H, NQ), generator=g).to(torch.int32)
+            ki = torch.randint(0, NK + 3, (B * H, NK), generator=g).to(torch.int32)
+        else:
+            ki = torch.arange(NK, dtype=torch.int32).expand(B * H, NK).contiguous()
+            last = NK - 1 if kind == "noncausal" else None
+            qi = (torch.full((B * H, NQ), last, dtype=torch.int32) if last is not None else
+                  (torch.arange(NQ, dtype=torch.int32) + (NK - NQ)).expand(B * H, NQ).contiguous())
+        q, kk, v, qi, ki = ops.check_inputs(Q, K, V, qi.to(dev), ki.to(dev))
+        res = []
+        for noalloc in (True, False):
+            out, st = ops.splash_forward(q, kk, v, qi, ki, 1.5, k, 0.125, with_topk=True,
+                                         tau_mode=tau_mode, noalloc=noalloc, block_m=bm)
+            torch.cuda.synchronize()
+            res.append((out, st))
+        (got_out, got), (want_out, want) = res
+        assert torch.equal(got_out.view(torch.uint8), want_out.view(torch.uint8)), f"draw {i}: out"
+        for name in ("taus", "norms", "mask", "q_ptr", "q_list", "k_ptr", "k_list",
+                     "topk_idx", "topk_val", "status"):
+            a, b = getattr(got, name), getattr(want, name)
+            if a.dtype.is_floating_point:
+                a, b = a.view(torch.int32), b.view(torch.int32)
+            assert torch.equal(a, b), f"draw {i}: {name}"
+        # support masks of the active 64-row tiles (the kernels' tiles: with
+        # 32-row mask blocks, the union of each pair of mask rows)
+        m = want.mask.reshape(B * H, -1, want.mask.shape[-1]) != 0
+        if bm == 32:
+            if m.shape[1] % 2:
+                m = torch.cat([m, torch.zeros_like(m[:, :1])], 1)
+            m = m.reshape(B * H, -1, 2, m.shape[-1]).any(2)
+        for bh in range(B * H):
+            n = int(m[bh].sum())
+            assert torch.equal(got.sup_mask[bh, :n], want.sup_mask[bh, :n]), f"draw {i}: sup {bh}"
